@@ -1,0 +1,325 @@
+"""Benchmark of the decode hot path on one MI355X; prints ONE JSON line.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-extras]
+
+Headline (``value``): paged decode attention on the Llama-3-8B batch-64 shape
+64 sequences, 32 query / 8 KV heads, head_dim 128,
+block_size 16, lengths ~ U[512, 4096] (seed 0), vLLM's interleaved K|V cache,
+bf16. A step is one ``paged_attention_decode`` call over the whole batch with
+preallocated output and split-K workspace; W untimed steps, then K timed steps
+between device synchronisations. ``value`` is algorithmic HBM bytes (every K
+and V row once, plus q and out) per second, in TB/s.
+
+``roofline``: the same bytes over the op's mean duration measured with HIP
+events on the stream the kernels run on (torch's current stream), against the
+8 TB/s HBM peak. ``cpu_baseline``: the oracle (the reference's CPU path,
+restated in ``oracle/reference.py``) timed on this host's cores over a bounded
+sample of the same workload; the GPU output is checked against it on that
+sample before anything is reported.
+
+``extras``: the other BASELINE configs -- 128K-token split-K decode (fp16,
+batch 1 and 4, HND cache, 1% outlier rows), the head-dim-256 / group-8 stress
+batch, gemm_tn at the decode-layer shapes next to hipBLASLt (``F.linear``),
+and the norm / activation ops -- each timed as the median of cold-cache calls
+(a 1 GiB buffer is rewritten before every call, larger than the 256 MB
+Infinity Cache).
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import statistics
+import sys
+import time
+
+import torch
+import torch.nn.functional as F
+
+import decodekernels_amd as dk
+
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+FLUSH_BYTES = 1 << 30
+
+
+# ---------------------------------------------------------------------------
+# Inputs
+# ---------------------------------------------------------------------------
+def paged_cache_on_device(seq_lens, num_kv_heads, head_dim, block_size, dtype, layout, seed, outlier_frac=0.0):
+    """Seeded paged KV cache built on the GPU (same layouts and block-table
+    rules as ``decodekernels_amd.testing.make_paged_kv``, without a host round trip)."""
+    dev = torch.device("cuda")
+    g = torch.Generator(device=dev).manual_seed(seed)
+    nblk = [-(-n // block_size) for n in seq_lens]
+    num_blocks = sum(nblk) + 3
+    if layout == "vllm":
+        kv = torch.randn(num_blocks, num_kv_heads, block_size, 2 * head_dim, generator=g, device=dev, dtype=dtype)
+        k, v = kv.transpose(1, 2).split(head_dim, dim=-1)
+    elif layout == "hnd":
+        k = torch.randn(num_blocks, num_kv_heads, block_size, head_dim, generator=g, device=dev, dtype=dtype).transpose(1, 2)
+        v = torch.randn(num_blocks, num_kv_heads, block_size, head_dim, generator=g, device=dev, dtype=dtype).transpose(1, 2)
+    else:
+        k = torch.randn(num_blocks, block_size, num_kv_heads, head_dim, generator=g, device=dev, dtype=dtype)
+        v = torch.randn(num_blocks, block_size, num_kv_heads, head_dim, generator=g, device=dev, dtype=dtype)
+    if outlier_frac > 0:
+        rows = torch.rand(num_blocks, block_size, num_kv_heads, 1, generator=g, device=dev) < outlier_frac
+        scale = torch.where(rows, 8.0, 1.0).to(dtype)
+        k.mul_(scale)
+        v.mul_(scale)
+    perm = torch.randperm(num_blocks, generator=g, device=dev).to(torch.int32)
+    width = max(max(nblk), 1)
+    bt = torch.zeros(len(seq_lens), width, dtype=torch.int32, device=dev)
+    off = 0
+    for s, n in enumerate(nblk):
+        bt[s, :n] = perm[off : off + n]
+        off += n
+    lens = torch.tensor(seq_lens, dtype=torch.int32, device=dev)
+    return k, v, bt, lens
+
+
+def attention_case(num_seqs, hq, hkv, d, bs, seq_lens, dtype, layout, seed, q_scale=1.0, outlier_frac=0.0):
+    k, v, bt, lens = paged_cache_on_device(seq_lens, hkv, d, bs, dtype, layout, seed, outlier_frac)
+    g = torch.Generator(device="cuda").manual_seed(seed + 1)
+    q = torch.randn(num_seqs, hq, d, generator=g, device="cuda", dtype=dtype) * q_scale
+    max_len = max(seq_lens)
+    out = torch.empty_like(q)
+    ws = dk.alloc_workspace(num_seqs, hq, d, max_len, "cuda")
+    elt = torch.finfo(dtype).bits // 8
+    nbytes = sum(seq_lens) * 2 * hkv * d * elt + 2 * q.numel() * elt
+
+    def run():
+        dk.paged_attention_decode(q, k, v, bt, lens, max_seq_len=max_len, out=out, workspace=ws)
+
+    return dict(q=q, k=k, v=v, bt=bt, lens=lens, out=out, run=run, bytes=nbytes, seq_lens=seq_lens, dtype=dtype)
+
+
+def llama3_8b_decode_case():
+    g = torch.Generator().manual_seed(0)
+    seq_lens = torch.randint(512, 4097, (64,), generator=g).tolist()
+    return attention_case(64, 32, 8, 128, 16, seq_lens, torch.bfloat16, "vllm", seed=0, q_scale=128**-0.5)
+
+
+# ---------------------------------------------------------------------------
+# Timing
+# ---------------------------------------------------------------------------
+_FLUSH: torch.Tensor | None = None
+
+
+def flush_caches() -> None:
+    global _FLUSH
+    if _FLUSH is None:
+        _FLUSH = torch.empty(FLUSH_BYTES // 4, dtype=torch.int32, device="cuda")
+    _FLUSH.add_(1)
+
+
+def time_back_to_back(fn, steps: int, warmup: int) -> float:
+    """Mean ms per call over `steps` back-to-back calls, HIP events on the current stream."""
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        fn()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps
+
+
+def time_cold(fn, iters: int = 30, warmup: int = 3) -> dict:
+    """Median / p10 / p90 microseconds of single calls, caches flushed before each."""
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(iters)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(iters)]
+    for i in range(iters):
+        flush_caches()
+        starts[i].record()
+        fn()
+        ends[i].record()
+    torch.cuda.synchronize()
+    us = sorted(s.elapsed_time(e) * 1e3 for s, e in zip(starts, ends))
+    return {"median_us": round(statistics.median(us), 2), "p10_us": round(us[int(0.1 * (iters - 1))], 2),
+            "p90_us": round(us[int(0.9 * (iters - 1))], 2)}
+
+
+# ---------------------------------------------------------------------------
+# Extras
+# ---------------------------------------------------------------------------
+def extras_attention() -> dict:
+    res = {}
+    for b in (1, 4):
+        c = attention_case(b, 32, 8, 128, 16, [131072] * b, torch.float16, "hnd", seed=10 + b, outlier_frac=0.01)
+        t = time_cold(c["run"], iters=20)
+        gbs = c["bytes"] / (t["median_us"] * 1e-6) / 1e9
+        res[f"split_k_128k_b{b}_fp16"] = {**t, "GB/s": round(gbs, 1), "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 1),
+                                           "MB": round(c["bytes"] / 1e6, 1)}
+        del c
+    g = torch.Generator().manual_seed(5)
+    lens = torch.exp(torch.rand(256, generator=g) * math.log(32768)).long().clamp(1, 32768)
+    lens[torch.randperm(256, generator=g)[:8]] = 0
+    for dtype, tag in ((torch.float16, "fp16"), (torch.bfloat16, "bf16")):
+        c = attention_case(256, 16, 2, 256, 32, lens.tolist(), dtype, "nhd", seed=20)
+        t = time_cold(c["run"], iters=20)
+        gbs = c["bytes"] / (t["median_us"] * 1e-6) / 1e9
+        res[f"d256_g8_stress_{tag}"] = {**t, "GB/s": round(gbs, 1), "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 1),
+                                        "MB": round(c["bytes"] / 1e6, 1)}
+        del c
+    return res
+
+
+def extras_gemm() -> dict:
+    torch.backends.cuda.preferred_blas_library("cublaslt")  # hipBLASLt on ROCm
+    res = {}
+    g = torch.Generator(device="cuda").manual_seed(30)
+    for name, n in (("qkv", 6144), ("o", 4096), ("gate_up", 28672)):
+        w = torch.randn(n, 4096, generator=g, device="cuda", dtype=torch.bfloat16) * 0.02
+        for m in (1, 8, 32, 64, 4096):
+            a = torch.randn(m, 4096, generator=g, device="cuda", dtype=torch.bfloat16) * 0.02
+            out = torch.empty(m, n, device="cuda", dtype=torch.bfloat16)
+            torch.ops.decode_kernels.gemm_tn(out, a, w, None)
+            ref = F.linear(a, w)
+            err = (out.float() - ref.float()).abs().max().item()
+            if err > 2e-2:
+                raise AssertionError(f"gemm {name} M={m}: max abs err {err:.3e} vs hipBLASLt before timing")
+            iters = 10 if m == 4096 else 30
+            t_dk = time_cold(lambda: torch.ops.decode_kernels.gemm_tn(out, a, w, None), iters=iters)
+            t_bl = time_cold(lambda: F.linear(a, w), iters=iters)
+            flops = 2.0 * m * n * 4096
+            nbytes = (m * 4096 + n * 4096 + m * n) * 2
+            res[f"{name}_M{m}"] = {
+                "dk_us": t_dk["median_us"], "hipblaslt_us": t_bl["median_us"],
+                "dk_over_hipblaslt": round(t_dk["median_us"] / t_bl["median_us"], 3),
+                "TFLOP/s": round(flops / (t_dk["median_us"] * 1e-6) / 1e12, 1),
+                "GB/s": round(nbytes / (t_dk["median_us"] * 1e-6) / 1e9, 1),
+            }
+            if m == 4096:
+                res[f"{name}_M{m}"]["pct_mfma_peak"] = round(100 * res[f"{name}_M{m}"]["TFLOP/s"] / BF16_PEAK_TFLOPS, 1)
+        del w
+    return res
+
+
+def extras_norms() -> dict:
+    g = torch.Generator(device="cuda").manual_seed(40)
+    t, h, d = 64, 4096, 14336
+    x = torch.randn(t, h, generator=g, device="cuda", dtype=torch.bfloat16)
+    r = torch.randn(t, h, generator=g, device="cuda", dtype=torch.bfloat16)
+    w = (1 + 0.1 * torch.randn(h, generator=g, device="cuda")).to(torch.bfloat16)
+    out = torch.empty_like(x)
+    xs = torch.randn(t, 2 * d, generator=g, device="cuda", dtype=torch.bfloat16)
+    ys = torch.empty(t, d, device="cuda", dtype=torch.bfloat16)
+    res = {}
+    for name, fn, nbytes in (
+        ("rms_norm_64x4096", lambda: torch.ops.decode_kernels.rms_norm(out, x, w, 1e-5), 2 * t * h * 2),
+        ("fused_add_rms_norm_64x4096", lambda: torch.ops.decode_kernels.fused_add_rms_norm(x, r, w, 1e-5), 4 * t * h * 2),
+        ("silu_and_mul_64x2x14336", lambda: torch.ops.decode_kernels.silu_and_mul(ys, xs), 3 * t * d * 2),
+    ):
+        tm = time_cold(fn, iters=50)
+        res[name] = {**tm, "GB/s": round(nbytes / (tm["median_us"] * 1e-6) / 1e9, 1)}
+    return res
+
+
+# ---------------------------------------------------------------------------
+# CPU baseline (the oracle on the host cores) + pre-report correctness check
+# ---------------------------------------------------------------------------
+def cpu_baseline_and_check(case, budget_s: float = 20.0) -> dict:
+    from oracle.reference import paged_attention_reference
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    q, bt, lens = case["q"].cpu(), case["bt"].cpu(), case["lens"].cpu()
+    k, v = case["k"].cpu(), case["v"].cpu()  # bf16, as the reference's CPU path receives them
+    gpu_out = case["out"].float().cpu()
+    elt = 2
+    hkv, d = case["k"].shape[2], case["k"].shape[3]
+    done_bytes, elapsed, seqs = 0, 0.0, 0
+    worst = 0.0
+    paged_attention_reference(q[:1], k, v, bt[:1], lens[:1])  # warm-up
+    for s in range(q.shape[0]):
+        t0 = time.perf_counter()
+        ref = paged_attention_reference(q[s : s + 1], k, v, bt[s : s + 1], lens[s : s + 1])
+        elapsed += time.perf_counter() - t0
+        worst = max(worst, (gpu_out[s] - ref[0].float()).abs().max().item())
+        done_bytes += int(lens[s]) * 2 * hkv * d * elt + 2 * q.shape[1] * d * elt
+        seqs += 1
+        if elapsed >= budget_s:
+            break
+    del k, v
+    if worst > 2e-2:
+        raise AssertionError(f"paged_attention_decode differs from the oracle by {worst:.3e} (> 2e-2)")
+    return {
+        "value": round(done_bytes / elapsed / 1e12, 6),
+        "unit": "TB/s",
+        "cores": cores,
+        "kind": "port",
+        "sample": f"oracle.reference.paged_attention_reference (torch CPU, fp32) on the first {seqs} of 64 "
+        f"sequences of the same workload ({done_bytes / 1e6:.0f} MB of bf16 KV, bf16 inputs), one sequence per call, "
+        f"{elapsed:.1f} s; GPU output matched to {worst:.2e} max abs on those sequences",
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--no-extras", action="store_true", help="skip the secondary configs")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline (and its correctness check)")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: every work unit of this path fits one MI355X and no multi-GPU "
+              "figure is defined (sharding is design-only). Run with --gpus 1.", file=sys.stderr)
+        return 2
+    if not dk.is_available():
+        raise RuntimeError("decodekernels_amd HIP extension not available (build it with __graft_entry__.build())")
+
+    case = llama3_8b_decode_case()
+    case["run"]()
+    torch.cuda.synchronize()
+    ms = time_back_to_back(case["run"], args.steps, args.warmup)
+    gbs = case["bytes"] / (ms * 1e-3) / 1e9
+    cold = time_cold(case["run"], iters=30)
+
+    result = {
+        "metric": "paged-attn decode HBM TB/s (% peak) + µs/call; gemm_tn TFLOP/s; µs per op",
+        "value": round(gbs / 1e3, 4),
+        "unit": "TB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 5),
+        "us_per_call": round(ms * 1e3, 2),
+        "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 1),
+        "cold_cache": cold,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) K/V, q scaled by 1/sqrt(128))",
+        "config": {
+            "workload": "llama3-8b paged decode attention, batch 64",
+            "num_seqs": 64, "num_q_heads": 32, "num_kv_heads": 8, "head_dim": 128, "block_size": 16,
+            "seq_lens": "U[512,4096] seed 0", "total_tokens": sum(case["seq_lens"]), "kv_layout": "vllm interleaved",
+            "algorithmic_MB": round(case["bytes"] / 1e6, 1),
+        },
+        "roofline": {
+            "bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+        },
+    }
+    if not args.no_cpu:
+        result["cpu_baseline"] = cpu_baseline_and_check(case)
+    del case
+    torch.cuda.empty_cache()
+    if not args.no_extras:
+        result["extras"] = {"attention": extras_attention(), "gemm_bf16_K4096": extras_gemm(), "norm_act_bf16": extras_norms()}
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

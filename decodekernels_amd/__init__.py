@@ -1,0 +1,38 @@
+"""decodekernels_amd: the LLM decode hot path as hand-written HIP kernels for MI355X (gfx950).
+
+    import decodekernels_amd as dk
+    out = dk.paged_attention_decode(q, k_cache, v_cache, block_tables, seq_lens)
+
+Same public API as DecodeKernels' ``decode_kernels`` package
+(``decode_kernels/__init__.py:7-27``); the ops are registered under the same
+``torch.ops.decode_kernels.*`` names.
+"""
+
+from .ops import (
+    MAX_GQA_GROUP,
+    PARTITION_SIZE,
+    SUPPORTED_HEAD_DIMS,
+    alloc_workspace,
+    fused_add_rms_norm,
+    gemm,
+    is_available,
+    num_partitions,
+    paged_attention_decode,
+    rms_norm,
+    silu_and_mul,
+)
+
+__all__ = [
+    "MAX_GQA_GROUP",
+    "PARTITION_SIZE",
+    "SUPPORTED_HEAD_DIMS",
+    "alloc_workspace",
+    "fused_add_rms_norm",
+    "gemm",
+    "is_available",
+    "num_partitions",
+    "paged_attention_decode",
+    "rms_norm",
+    "silu_and_mul",
+]
+__version__ = "0.1.0"

@@ -1,0 +1,147 @@
+"""ctypes handle on the C ABI (``include/decodekernels_amd.h``) of
+``libdecodekernels_amd.so``.
+
+For callers that hold raw device pointers rather than torch tensors (other
+runtimes, FFI bindings), and for tests that exercise the boundary without the
+torch binding. ``torch`` is imported first on purpose: the library then binds
+to the HIP runtime torch already loaded instead of a second copy.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+from pathlib import Path
+
+import torch  # noqa: F401  (load torch's HIP runtime before ours; see module docstring)
+
+LIB_PATH = Path(__file__).resolve().parent / "libdecodekernels_amd.so"
+HEADER_PATH = Path(__file__).resolve().parent.parent / "include" / "decodekernels_amd.h"
+
+DK_FLOAT16 = 0
+DK_BFLOAT16 = 1
+HIP_ERROR_INVALID_VALUE = 1
+
+
+class PagedAttnParams(ctypes.Structure):
+    """Mirror of ``dk_paged_attn_params``."""
+
+    _fields_ = [
+        ("out", ctypes.c_void_p),
+        ("q", ctypes.c_void_p),
+        ("k_cache", ctypes.c_void_p),
+        ("v_cache", ctypes.c_void_p),
+        ("block_tables", ctypes.c_void_p),
+        ("seq_lens", ctypes.c_void_p),
+        ("tmp_out", ctypes.c_void_p),
+        ("max_logits", ctypes.c_void_p),
+        ("exp_sums", ctypes.c_void_p),
+        ("q_stride_seq", ctypes.c_int64),
+        ("q_stride_head", ctypes.c_int64),
+        ("out_stride_seq", ctypes.c_int64),
+        ("out_stride_head", ctypes.c_int64),
+        ("k_stride_block", ctypes.c_int64),
+        ("k_stride_token", ctypes.c_int64),
+        ("k_stride_head", ctypes.c_int64),
+        ("v_stride_block", ctypes.c_int64),
+        ("v_stride_token", ctypes.c_int64),
+        ("v_stride_head", ctypes.c_int64),
+        ("bt_stride", ctypes.c_int64),
+        ("num_seqs", ctypes.c_int32),
+        ("num_q_heads", ctypes.c_int32),
+        ("num_kv_heads", ctypes.c_int32),
+        ("block_size", ctypes.c_int32),
+        ("max_partitions", ctypes.c_int32),
+        ("scale", ctypes.c_float),
+    ]
+
+
+_LIB: ctypes.CDLL | None = None
+
+_SIGNATURES = {
+    "dk_paged_attention_decode": (
+        ctypes.c_int,
+        [ctypes.POINTER(PagedAttnParams), ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p],
+    ),
+    "dk_gemm_tn": (
+        ctypes.c_int,
+        [ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p]
+        + [ctypes.c_int] * 6
+        + [ctypes.c_void_p],
+    ),
+    "dk_rms_norm": (
+        ctypes.c_int,
+        [ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_int]
+        + [ctypes.c_int64, ctypes.c_int64, ctypes.c_float, ctypes.c_void_p],
+    ),
+    "dk_fused_add_rms_norm": (
+        ctypes.c_int,
+        [ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_int]
+        + [ctypes.c_int64, ctypes.c_int64, ctypes.c_float, ctypes.c_void_p],
+    ),
+    "dk_silu_and_mul": (
+        ctypes.c_int,
+        [ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int64, ctypes.c_int64]
+        + [ctypes.c_void_p],
+    ),
+    "dk_last_error": (ctypes.c_char_p, []),
+    "dk_error_string": (ctypes.c_char_p, [ctypes.c_int]),
+    "dk_version": (ctypes.c_char_p, []),
+}
+
+
+def lib() -> ctypes.CDLL:
+    """Loads the C-ABI library (raises if it has not been built)."""
+    global _LIB
+    if _LIB is None:
+        if not LIB_PATH.exists():
+            raise RuntimeError(f"{LIB_PATH} is not built; run `python -m decodekernels_amd._build`")
+        handle = ctypes.CDLL(os.fspath(LIB_PATH))
+        for name, (restype, argtypes) in _SIGNATURES.items():
+            fn = getattr(handle, name)
+            fn.restype = restype
+            fn.argtypes = argtypes
+        _LIB = handle
+    return _LIB
+
+
+def declared_functions() -> list[str]:
+    """Names of every function the C header declares."""
+    text = HEADER_PATH.read_text()
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\*?\s+\*?(dk_\w+)\s*\(", text, flags=re.M)))
+
+
+def last_error() -> str:
+    return lib().dk_last_error().decode()
+
+
+def dtype_code(dtype: torch.dtype) -> int:
+    if dtype == torch.float16:
+        return DK_FLOAT16
+    if dtype == torch.bfloat16:
+        return DK_BFLOAT16
+    raise ValueError(f"expected float16 or bfloat16, got {dtype}")
+
+
+def attn_params(out, q, k_cache, v_cache, block_tables, seq_lens, scale, workspace=None) -> PagedAttnParams:
+    """Fills ``dk_paged_attn_params`` from tensors (strides in elements)."""
+    p = PagedAttnParams()
+    p.out, p.q = out.data_ptr(), q.data_ptr()
+    p.k_cache, p.v_cache = k_cache.data_ptr(), v_cache.data_ptr()
+    p.block_tables, p.seq_lens = block_tables.data_ptr(), seq_lens.data_ptr()
+    if workspace is not None and workspace[0].numel() > 0:
+        p.tmp_out, p.max_logits, p.exp_sums = (t.data_ptr() for t in workspace)
+        p.max_partitions = workspace[0].shape[2]
+    else:
+        p.max_partitions = 1
+    p.q_stride_seq, p.q_stride_head = q.stride(0), q.stride(1)
+    p.out_stride_seq, p.out_stride_head = out.stride(0), out.stride(1)
+    p.k_stride_block, p.k_stride_token, p.k_stride_head = k_cache.stride()[:3]
+    p.v_stride_block, p.v_stride_token, p.v_stride_head = v_cache.stride()[:3]
+    p.bt_stride = block_tables.stride(0)
+    p.num_seqs, p.num_q_heads, _ = q.shape
+    p.num_kv_heads = k_cache.shape[2]
+    p.block_size = k_cache.shape[1]
+    p.scale = scale
+    return p

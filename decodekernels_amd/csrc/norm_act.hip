@@ -1,0 +1,318 @@
+// Bandwidth-bound decoder-layer ops for gfx950, with vLLM / DecodeKernels
+// semantics (reference: csrc/norm_act.cuh:1-200, decode_kernels/reference.py:89-104):
+//
+//   rms_norm(out, x, w, eps):           out = round(x * inv_rms * w)
+//   fused_add_rms_norm(x, res, w, eps): res = round(x + res); x = round(res * inv_rms * w)
+//   silu_and_mul(out, x):               out = round(silu(x[:, :d]) * x[:, d:])
+//
+// All arithmetic is fp32; rounding to the model dtype is to nearest even. The
+// sum of squares of fused_add_rms_norm is taken over the *rounded* residual.
+// inv_rms = 1 / sqrt(mean + eps) with a correctly rounded square root and
+// division, which is how torch's CPU rsqrt evaluates it.
+//
+// Layout on CDNA4: one workgroup per row for the norms, with the row held in
+// registers between the reduction and the write (each element of x, residual
+// and weight is read from HBM exactly once). A row of H elements is split
+// into 16-byte vectors, NV per thread; NV is a template parameter so the
+// vectors stay in VGPRs. silu_and_mul has no reduction, so it runs a 2-D grid
+// (row, 2048-column chunk) of 16-byte vector lanes for more parallelism than
+// one workgroup per row. Rows that are not 16-byte vectorisable take a scalar
+// path that re-reads the row.
+#include <cmath>
+
+#include "../../include/decodekernels_amd.h"
+#include "dk_device.h"
+#include "dk_host.h"
+
+namespace dk {
+namespace normact {
+
+constexpr int kVec = 8;  // 16-bit elements per 16-byte vector
+
+__device__ __forceinline__ float inv_rms(float ss, int H, float eps) {
+  return 1.0f / __fsqrt_rn(ss / static_cast<float>(H) + eps);
+}
+
+template <typename E>
+__device__ __forceinline__ float sumsq8(u32x4 v, float ss) {
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const float a = E::lo(v[e]);
+    const float b = E::hi(v[e]);
+    ss = fmaf(a, a, ss);
+    ss = fmaf(b, b, ss);
+  }
+  return ss;
+}
+
+template <typename E>
+__device__ __forceinline__ u32x4 scale8(u32x4 x, u32x4 w, float inv) {
+  u32x4 o;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) o[e] = pack2<E>(E::lo(x[e]) * inv * E::lo(w[e]), E::hi(x[e]) * inv * E::hi(w[e]));
+  return o;
+}
+
+// ---------------------------------------------------------------------------
+// rms_norm
+// ---------------------------------------------------------------------------
+template <typename E, int NV>
+__global__ __launch_bounds__(1024) void rms_norm_vec_kernel(uint16_t* __restrict__ out, const uint16_t* __restrict__ in,
+                                                            const uint16_t* __restrict__ weight, int H,
+                                                            int64_t in_stride, int64_t out_stride, float eps) {
+  __shared__ float slots[1024 / kWave];
+  const u32x4* x = reinterpret_cast<const u32x4*>(in + blockIdx.x * in_stride);
+  u32x4* y = reinterpret_cast<u32x4*>(out + blockIdx.x * out_stride);
+  const u32x4* w = reinterpret_cast<const u32x4*>(weight);
+  const int nvec = H / kVec;
+  u32x4 xv[NV];
+  float ss = 0.0f;
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int i = threadIdx.x + j * blockDim.x;
+    xv[j] = i < nvec ? x[i] : u32x4{0u, 0u, 0u, 0u};
+    ss = sumsq8<E>(xv[j], ss);
+  }
+  const float inv = inv_rms(block_sum(ss, slots), H, eps);
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int i = threadIdx.x + j * blockDim.x;
+    if (i < nvec) y[i] = scale8<E>(xv[j], w[i], inv);
+  }
+}
+
+template <typename E>
+__global__ __launch_bounds__(1024) void rms_norm_scalar_kernel(uint16_t* __restrict__ out,
+                                                               const uint16_t* __restrict__ in,
+                                                               const uint16_t* __restrict__ weight, int H,
+                                                               int64_t in_stride, int64_t out_stride, float eps) {
+  __shared__ float slots[1024 / kWave];
+  const uint16_t* x = in + blockIdx.x * in_stride;
+  uint16_t* y = out + blockIdx.x * out_stride;
+  float ss = 0.0f;
+  for (int i = threadIdx.x; i < H; i += blockDim.x) {
+    const float f = E::to_float(x[i]);
+    ss = fmaf(f, f, ss);
+  }
+  const float inv = inv_rms(block_sum(ss, slots), H, eps);
+  for (int i = threadIdx.x; i < H; i += blockDim.x) y[i] = E::from_float(E::to_float(x[i]) * inv * E::to_float(weight[i]));
+}
+
+// ---------------------------------------------------------------------------
+// fused_add_rms_norm
+// ---------------------------------------------------------------------------
+template <typename E, int NV>
+__global__ __launch_bounds__(1024) void fused_add_rms_norm_vec_kernel(uint16_t* __restrict__ input,
+                                                                      uint16_t* __restrict__ residual,
+                                                                      const uint16_t* __restrict__ weight, int H,
+                                                                      int64_t in_stride, int64_t res_stride,
+                                                                      float eps) {
+  __shared__ float slots[1024 / kWave];
+  u32x4* x = reinterpret_cast<u32x4*>(input + blockIdx.x * in_stride);
+  u32x4* r = reinterpret_cast<u32x4*>(residual + blockIdx.x * res_stride);
+  const u32x4* w = reinterpret_cast<const u32x4*>(weight);
+  const int nvec = H / kVec;
+  u32x4 rv[NV];
+  float ss = 0.0f;
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int i = threadIdx.x + j * blockDim.x;
+    u32x4 s = {0u, 0u, 0u, 0u};
+    if (i < nvec) {
+      const u32x4 a = x[i];
+      const u32x4 b = r[i];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) s[e] = pack2<E>(E::lo(a[e]) + E::lo(b[e]), E::hi(a[e]) + E::hi(b[e]));
+      r[i] = s;
+    }
+    rv[j] = s;
+    ss = sumsq8<E>(s, ss);
+  }
+  const float inv = inv_rms(block_sum(ss, slots), H, eps);
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int i = threadIdx.x + j * blockDim.x;
+    if (i < nvec) x[i] = scale8<E>(rv[j], w[i], inv);
+  }
+}
+
+template <typename E>
+__global__ __launch_bounds__(1024) void fused_add_rms_norm_scalar_kernel(uint16_t* __restrict__ input,
+                                                                         uint16_t* __restrict__ residual,
+                                                                         const uint16_t* __restrict__ weight, int H,
+                                                                         int64_t in_stride, int64_t res_stride,
+                                                                         float eps) {
+  __shared__ float slots[1024 / kWave];
+  uint16_t* x = input + blockIdx.x * in_stride;
+  uint16_t* r = residual + blockIdx.x * res_stride;
+  float ss = 0.0f;
+  for (int i = threadIdx.x; i < H; i += blockDim.x) {
+    const uint16_t z = E::from_float(E::to_float(x[i]) + E::to_float(r[i]));
+    r[i] = z;
+    const float f = E::to_float(z);
+    ss = fmaf(f, f, ss);
+  }
+  const float inv = inv_rms(block_sum(ss, slots), H, eps);
+  // Each thread re-reads only the residual elements it wrote itself.
+  for (int i = threadIdx.x; i < H; i += blockDim.x) x[i] = E::from_float(E::to_float(r[i]) * inv * E::to_float(weight[i]));
+}
+
+// ---------------------------------------------------------------------------
+// silu_and_mul
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float silu(float g) { return g / (1.0f + expf(-g)); }
+
+constexpr int kSiluThreads = 256;
+
+template <typename E>
+__global__ __launch_bounds__(kSiluThreads) void silu_and_mul_vec_kernel(uint16_t* __restrict__ out,
+                                                                        const uint16_t* __restrict__ in, int d,
+                                                                        int64_t in_stride, int64_t out_stride) {
+  const int i = blockIdx.y * kSiluThreads + threadIdx.x;  // vector index in the row
+  if (i >= d / kVec) return;
+  const uint16_t* row = in + blockIdx.x * in_stride;
+  const u32x4 g = reinterpret_cast<const u32x4*>(row)[i];
+  const u32x4 u = reinterpret_cast<const u32x4*>(row + d)[i];
+  u32x4 o;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) o[e] = pack2<E>(silu(E::lo(g[e])) * E::lo(u[e]), silu(E::hi(g[e])) * E::hi(u[e]));
+  reinterpret_cast<u32x4*>(out + blockIdx.x * out_stride)[i] = o;
+}
+
+template <typename E>
+__global__ __launch_bounds__(kSiluThreads) void silu_and_mul_scalar_kernel(uint16_t* __restrict__ out,
+                                                                           const uint16_t* __restrict__ in, int d,
+                                                                           int64_t in_stride, int64_t out_stride) {
+  const int i = blockIdx.y * kSiluThreads + threadIdx.x;
+  if (i >= d) return;
+  const uint16_t* row = in + blockIdx.x * in_stride;
+  out[blockIdx.x * out_stride + i] = E::from_float(silu(E::to_float(row[i])) * E::to_float(row[d + i]));
+}
+
+// ---------------------------------------------------------------------------
+// Host-side shape selection
+// ---------------------------------------------------------------------------
+struct RowShape {
+  int threads;
+  int nv;  // vectors per thread (1, 2, 4, 8); 0 = scalar path
+};
+
+// Vector path: about 256 threads per row, each holding NV 16-byte vectors.
+RowShape row_shape(int H, bool vec) {
+  if (vec) {
+    const int nvec = H / kVec;
+    for (int nv : {1, 2, 4, 8}) {
+      const int t = static_cast<int>(ceil_div64(nvec, nv));
+      if (t <= 256 || (nv == 8 && t <= 1024)) {
+        const int threads = static_cast<int>(ceil_div64(t, kWave) * kWave);
+        return {threads < kWave ? kWave : threads, nv};
+      }
+    }
+  }
+  int threads = static_cast<int>(ceil_div64(H, kWave) * kWave);
+  threads = threads < kWave ? kWave : (threads > 1024 ? 1024 : threads);
+  return {threads, 0};
+}
+
+template <typename E>
+hipError_t launch_rms_norm(uint16_t* out, const uint16_t* in, const uint16_t* w, int rows, int H, int64_t is,
+                           int64_t os, float eps, bool vec, hipStream_t s) {
+  const RowShape rs = row_shape(H, vec);
+  const dim3 grid(rows), block(rs.threads);
+  switch (rs.nv) {
+    case 1: hipLaunchKernelGGL((rms_norm_vec_kernel<E, 1>), grid, block, 0, s, out, in, w, H, is, os, eps); break;
+    case 2: hipLaunchKernelGGL((rms_norm_vec_kernel<E, 2>), grid, block, 0, s, out, in, w, H, is, os, eps); break;
+    case 4: hipLaunchKernelGGL((rms_norm_vec_kernel<E, 4>), grid, block, 0, s, out, in, w, H, is, os, eps); break;
+    case 8: hipLaunchKernelGGL((rms_norm_vec_kernel<E, 8>), grid, block, 0, s, out, in, w, H, is, os, eps); break;
+    default: hipLaunchKernelGGL((rms_norm_scalar_kernel<E>), grid, block, 0, s, out, in, w, H, is, os, eps); break;
+  }
+  return hipGetLastError();
+}
+
+template <typename E>
+hipError_t launch_fused_add(uint16_t* x, uint16_t* r, const uint16_t* w, int rows, int H, int64_t is, int64_t rs_,
+                            float eps, bool vec, hipStream_t s) {
+  const RowShape rs = row_shape(H, vec);
+  const dim3 grid(rows), block(rs.threads);
+  switch (rs.nv) {
+    case 1: hipLaunchKernelGGL((fused_add_rms_norm_vec_kernel<E, 1>), grid, block, 0, s, x, r, w, H, is, rs_, eps); break;
+    case 2: hipLaunchKernelGGL((fused_add_rms_norm_vec_kernel<E, 2>), grid, block, 0, s, x, r, w, H, is, rs_, eps); break;
+    case 4: hipLaunchKernelGGL((fused_add_rms_norm_vec_kernel<E, 4>), grid, block, 0, s, x, r, w, H, is, rs_, eps); break;
+    case 8: hipLaunchKernelGGL((fused_add_rms_norm_vec_kernel<E, 8>), grid, block, 0, s, x, r, w, H, is, rs_, eps); break;
+    default: hipLaunchKernelGGL((fused_add_rms_norm_scalar_kernel<E>), grid, block, 0, s, x, r, w, H, is, rs_, eps); break;
+  }
+  return hipGetLastError();
+}
+
+template <typename E>
+hipError_t launch_silu(uint16_t* out, const uint16_t* in, int rows, int d, int64_t is, int64_t os, bool vec,
+                       hipStream_t s) {
+  const int per_row = vec ? d / kVec : d;
+  const dim3 grid(rows, static_cast<unsigned>(ceil_div64(per_row, kSiluThreads)));
+  if (vec) {
+    hipLaunchKernelGGL((silu_and_mul_vec_kernel<E>), grid, dim3(kSiluThreads), 0, s, out, in, d, is, os);
+  } else {
+    hipLaunchKernelGGL((silu_and_mul_scalar_kernel<E>), grid, dim3(kSiluThreads), 0, s, out, in, d, is, os);
+  }
+  return hipGetLastError();
+}
+
+bool dtype_ok(int dtype) { return dtype == DK_FLOAT16 || dtype == DK_BFLOAT16; }
+
+}  // namespace normact
+}  // namespace dk
+
+using namespace dk;
+using namespace dk::normact;
+
+extern "C" int dk_rms_norm(int dtype, void* out, const void* input, const void* weight, int rows, int H,
+                           int64_t in_stride, int64_t out_stride, float eps, void* stream) {
+  clear_error();
+  if (!dtype_ok(dtype)) return fail("rms_norm: expected float16 or bfloat16, got dtype code %d", dtype);
+  if (rows < 0 || H < 0) return fail("rms_norm: rows and H must be non-negative");
+  if (rows == 0 || H == 0) return hipSuccess;
+  if (out == nullptr || input == nullptr || weight == nullptr) return fail("rms_norm: pointers must not be NULL");
+  const bool vec = H % kVec == 0 && in_stride % kVec == 0 && out_stride % kVec == 0 && aligned_to(input, 16) &&
+                   aligned_to(out, 16) && aligned_to(weight, 16);
+  auto* o = static_cast<uint16_t*>(out);
+  auto* x = static_cast<const uint16_t*>(input);
+  auto* w = static_cast<const uint16_t*>(weight);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  return static_cast<int>(dtype == DK_BFLOAT16 ? launch_rms_norm<Bf16>(o, x, w, rows, H, in_stride, out_stride, eps, vec, s)
+                                               : launch_rms_norm<F16>(o, x, w, rows, H, in_stride, out_stride, eps, vec, s));
+}
+
+extern "C" int dk_fused_add_rms_norm(int dtype, void* input, void* residual, const void* weight, int rows, int H,
+                                     int64_t in_stride, int64_t res_stride, float eps, void* stream) {
+  clear_error();
+  if (!dtype_ok(dtype)) return fail("fused_add_rms_norm: expected float16 or bfloat16, got dtype code %d", dtype);
+  if (rows < 0 || H < 0) return fail("fused_add_rms_norm: rows and H must be non-negative");
+  if (rows == 0 || H == 0) return hipSuccess;
+  if (input == nullptr || residual == nullptr || weight == nullptr)
+    return fail("fused_add_rms_norm: pointers must not be NULL");
+  const bool vec = H % kVec == 0 && in_stride % kVec == 0 && res_stride % kVec == 0 && aligned_to(input, 16) &&
+                   aligned_to(residual, 16) && aligned_to(weight, 16);
+  auto* x = static_cast<uint16_t*>(input);
+  auto* r = static_cast<uint16_t*>(residual);
+  auto* w = static_cast<const uint16_t*>(weight);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  return static_cast<int>(dtype == DK_BFLOAT16 ? launch_fused_add<Bf16>(x, r, w, rows, H, in_stride, res_stride, eps, vec, s)
+                                               : launch_fused_add<F16>(x, r, w, rows, H, in_stride, res_stride, eps, vec, s));
+}
+
+extern "C" int dk_silu_and_mul(int dtype, void* out, const void* input, int rows, int d, int64_t in_stride,
+                               int64_t out_stride, void* stream) {
+  clear_error();
+  if (!dtype_ok(dtype)) return fail("silu_and_mul: expected float16 or bfloat16, got dtype code %d", dtype);
+  if (rows < 0 || d < 0) return fail("silu_and_mul: rows and d must be non-negative");
+  if (rows == 0 || d == 0) return hipSuccess;
+  if (out == nullptr || input == nullptr) return fail("silu_and_mul: pointers must not be NULL");
+  if (ceil_div64(d, kSiluThreads) > 65535) return fail("silu_and_mul: d is too large");
+  const bool vec =
+      d % kVec == 0 && in_stride % kVec == 0 && out_stride % kVec == 0 && aligned_to(input, 16) && aligned_to(out, 16);
+  auto* o = static_cast<uint16_t*>(out);
+  auto* x = static_cast<const uint16_t*>(input);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  return static_cast<int>(dtype == DK_BFLOAT16 ? launch_silu<Bf16>(o, x, rows, d, in_stride, out_stride, vec, s)
+                                               : launch_silu<F16>(o, x, rows, d, in_stride, out_stride, vec, s));
+}

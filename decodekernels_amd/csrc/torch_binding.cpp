@@ -1,0 +1,274 @@
+// PyTorch binding of the decode kernels: `torch.ops.decode_kernels.*`.
+//
+// The five schemas, the dispatch key (CUDA, which is where PyTorch-ROCm puts
+// HIP tensors) and the argument-check messages are DecodeKernels' interface
+// (csrc/ops.cu:44-286), kept identical so callers and tests written against
+// the reference see the same ops and the same errors. Each impl checks tensor
+// metadata, fills the C-ABI arguments and enqueues the HIP kernels on the
+// current stream of the input's device; nothing here allocates memory, so the
+// ops can be captured in a graph.
+//
+// Importing the Python module `decodekernels_amd._C` (this library) runs the
+// static op registration.
+#include <Python.h>
+
+#include <ATen/ATen.h>
+#include <c10/hip/HIPGuard.h>
+#include <c10/hip/HIPStream.h>
+#include <torch/library.h>
+
+#include <algorithm>
+#include <optional>
+
+#include "decodekernels_amd.h"
+
+namespace {
+
+int dtype_code(at::ScalarType t, const char* name) {
+  if (t == at::ScalarType::Half) return DK_FLOAT16;
+  if (t == at::ScalarType::BFloat16) return DK_BFLOAT16;
+  TORCH_CHECK(false, name, ": expected float16 or bfloat16, got ", t);
+}
+
+void check_status(int err, const char* name) {
+  if (err == 0) return;
+  const char* detail = dk_last_error();
+  TORCH_CHECK(false, name, " failed: ", dk_error_string(err), (detail[0] != '\0' ? " (" : ""), detail,
+              (detail[0] != '\0' ? ")" : ""));
+}
+
+void check_same(const at::Tensor& a, const at::Tensor& b, const char* what) {
+  TORCH_CHECK(a.scalar_type() == b.scalar_type(), what, ": dtype mismatch (", a.scalar_type(), " vs ",
+              b.scalar_type(), ")");
+  TORCH_CHECK(a.device() == b.device(), what, ": tensors must be on the same device");
+}
+
+void* stream_of(const at::Tensor& t) {
+  return static_cast<void*>(c10::hip::getCurrentHIPStream(t.device().index()).stream());
+}
+
+bool aligned(const void* p, int64_t bytes) { return reinterpret_cast<uintptr_t>(p) % static_cast<uintptr_t>(bytes) == 0; }
+
+// Row stride of a [..., H] tensor whose leading dims collapse into one
+// uniformly strided row index (csrc/ops.cu:189-197).
+int64_t row_stride(const at::Tensor& t, const char* name) {
+  TORCH_CHECK(t.stride(-1) == 1, name, ": last dimension must be contiguous");
+  if (t.dim() == 1) return t.size(0);
+  for (int64_t d = 1; d + 1 < t.dim(); ++d) {
+    TORCH_CHECK(t.stride(d - 1) == t.stride(d) * t.size(d), name, ": leading dimensions must be collapsible");
+  }
+  return t.stride(-2);
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
+// paged_attention_decode (csrc/ops.cu:44-144)
+// ---------------------------------------------------------------------------
+void paged_attention_decode(at::Tensor& out, const at::Tensor& q, const at::Tensor& k_cache,
+                            const at::Tensor& v_cache, const at::Tensor& block_tables, const at::Tensor& seq_lens,
+                            double scale, int64_t max_seq_len, at::Tensor& tmp_out, at::Tensor& max_logits,
+                            at::Tensor& exp_sums) {
+  TORCH_CHECK(q.is_cuda(), "paged_attention_decode: q must be a CUDA tensor");
+  TORCH_CHECK(q.dim() == 3 && out.dim() == 3, "q and out must be [num_seqs, num_q_heads, head_dim]");
+  TORCH_CHECK(k_cache.dim() == 4 && v_cache.dim() == 4,
+              "k_cache and v_cache must be [num_blocks, block_size, num_kv_heads, head_dim]");
+  check_same(q, out, "q/out");
+  check_same(q, k_cache, "q/k_cache");
+  check_same(q, v_cache, "q/v_cache");
+  TORCH_CHECK(out.sizes() == q.sizes(), "out must have the same shape as q");
+  TORCH_CHECK(k_cache.sizes() == v_cache.sizes(), "k_cache and v_cache shapes differ");
+
+  const int64_t num_seqs = q.size(0);
+  const int64_t num_q_heads = q.size(1);
+  const int64_t head_dim = q.size(2);
+  const int64_t num_kv_heads = k_cache.size(2);
+  TORCH_CHECK(k_cache.size(3) == head_dim, "cache head_dim does not match q");
+  TORCH_CHECK(head_dim == 64 || head_dim == 128 || head_dim == 256, "head_dim must be 64, 128 or 256, got ",
+              head_dim);
+  TORCH_CHECK(num_kv_heads > 0 && num_q_heads % num_kv_heads == 0, "num_q_heads must be a multiple of num_kv_heads");
+  TORCH_CHECK(num_q_heads / num_kv_heads <= DK_MAX_GQA_GROUP, "GQA group size above ", DK_MAX_GQA_GROUP,
+              " is not supported");
+  TORCH_CHECK(q.stride(2) == 1 && out.stride(2) == 1 && k_cache.stride(3) == 1 && v_cache.stride(3) == 1,
+              "head_dim must be the contiguous (innermost) dimension");
+  const int64_t vec = head_dim / 32;
+  for (int d = 0; d < 3; ++d) {
+    TORCH_CHECK(k_cache.stride(d) % vec == 0 && v_cache.stride(d) % vec == 0,
+                "KV-cache strides must be multiples of head_dim / 32 for vectorised loads");
+  }
+  TORCH_CHECK(aligned(k_cache.data_ptr(), vec * 2) && aligned(v_cache.data_ptr(), vec * 2),
+              "KV-cache pointers must be aligned to head_dim / 16 bytes");
+  TORCH_CHECK(block_tables.scalar_type() == at::kInt && block_tables.dim() == 2 && block_tables.stride(1) == 1,
+              "block_tables must be a 2-D int32 tensor with a contiguous last dimension");
+  TORCH_CHECK(seq_lens.scalar_type() == at::kInt && seq_lens.dim() == 1 && seq_lens.is_contiguous(),
+              "seq_lens must be a contiguous 1-D int32 tensor");
+  TORCH_CHECK(block_tables.size(0) >= num_seqs && seq_lens.size(0) >= num_seqs,
+              "block_tables and seq_lens must have at least num_seqs rows");
+  TORCH_CHECK(max_seq_len >= 0, "max_seq_len must be non-negative");
+
+  const bool split = max_seq_len > DK_PARTITION_SIZE;
+  const int64_t needed_parts = (max_seq_len + DK_PARTITION_SIZE - 1) / DK_PARTITION_SIZE;
+  int64_t max_partitions = 1;
+  if (split) {
+    TORCH_CHECK(tmp_out.scalar_type() == at::kFloat && max_logits.scalar_type() == at::kFloat &&
+                    exp_sums.scalar_type() == at::kFloat,
+                "split-K workspace tensors must be float32");
+    TORCH_CHECK(tmp_out.is_contiguous() && max_logits.is_contiguous() && exp_sums.is_contiguous(),
+                "split-K workspace tensors must be contiguous");
+    TORCH_CHECK(tmp_out.dim() == 4 && tmp_out.size(0) == num_seqs && tmp_out.size(1) == num_q_heads &&
+                    tmp_out.size(2) >= needed_parts && tmp_out.size(3) == head_dim,
+                "tmp_out must be [num_seqs, num_q_heads, >= ceil(max_seq_len / 512), head_dim]");
+    TORCH_CHECK(max_logits.sizes() == exp_sums.sizes() && max_logits.dim() == 3 && max_logits.size(0) == num_seqs &&
+                    max_logits.size(1) == num_q_heads && max_logits.size(2) == tmp_out.size(2),
+                "max_logits / exp_sums must be [num_seqs, num_q_heads, max_partitions]");
+    max_partitions = tmp_out.size(2);
+  }
+  if (num_seqs == 0) return;
+
+  dk_paged_attn_params p{};
+  p.out = out.data_ptr();
+  p.q = q.data_ptr();
+  p.k_cache = k_cache.data_ptr();
+  p.v_cache = v_cache.data_ptr();
+  p.block_tables = block_tables.data_ptr<int32_t>();
+  p.seq_lens = seq_lens.data_ptr<int32_t>();
+  p.tmp_out = split ? tmp_out.data_ptr<float>() : nullptr;
+  p.max_logits = split ? max_logits.data_ptr<float>() : nullptr;
+  p.exp_sums = split ? exp_sums.data_ptr<float>() : nullptr;
+  p.q_stride_seq = q.stride(0);
+  p.q_stride_head = q.stride(1);
+  p.out_stride_seq = out.stride(0);
+  p.out_stride_head = out.stride(1);
+  p.k_stride_block = k_cache.stride(0);
+  p.k_stride_token = k_cache.stride(1);
+  p.k_stride_head = k_cache.stride(2);
+  p.v_stride_block = v_cache.stride(0);
+  p.v_stride_token = v_cache.stride(1);
+  p.v_stride_head = v_cache.stride(2);
+  p.bt_stride = block_tables.stride(0);
+  p.num_seqs = static_cast<int32_t>(num_seqs);
+  p.num_q_heads = static_cast<int32_t>(num_q_heads);
+  p.num_kv_heads = static_cast<int32_t>(num_kv_heads);
+  p.block_size = static_cast<int32_t>(k_cache.size(1));
+  p.max_partitions = static_cast<int32_t>(max_partitions);
+  p.scale = static_cast<float>(scale);
+
+  const int dt = dtype_code(q.scalar_type(), "paged_attention_decode");
+  const c10::hip::OptionalHIPGuard guard(q.device());
+  check_status(dk_paged_attention_decode(&p, dt, static_cast<int>(head_dim), static_cast<int>(max_seq_len),
+                                         stream_of(q)),
+               "paged_attention_decode");
+}
+
+// ---------------------------------------------------------------------------
+// gemm_tn (csrc/ops.cu:149-182)
+// ---------------------------------------------------------------------------
+void gemm_tn(at::Tensor& c, const at::Tensor& a, const at::Tensor& b, const std::optional<at::Tensor>& bias) {
+  TORCH_CHECK(a.is_cuda(), "gemm_tn: tensors must be on CUDA");
+  TORCH_CHECK(a.dim() == 2 && b.dim() == 2 && c.dim() == 2, "gemm_tn: a [M,K], b [N,K], c [M,N]");
+  check_same(a, b, "a/b");
+  check_same(a, c, "a/c");
+  const int64_t M = a.size(0), K = a.size(1), N = b.size(0);
+  TORCH_CHECK(b.size(1) == K, "gemm_tn: K mismatch");
+  TORCH_CHECK(c.size(0) == M && c.size(1) == N, "gemm_tn: c must be [M, N]");
+  TORCH_CHECK(a.stride(1) == 1 && b.stride(1) == 1 && c.stride(1) == 1, "gemm_tn: last dims must be contiguous");
+  TORCH_CHECK(K % 8 == 0 && a.stride(0) % 8 == 0 && b.stride(0) % 8 == 0,
+              "gemm_tn: K and row strides of a/b must be multiples of 8");
+  TORCH_CHECK(aligned(a.data_ptr(), 16) && aligned(b.data_ptr(), 16), "gemm_tn: a and b must be 16-byte aligned");
+  const void* bias_ptr = nullptr;
+  if (bias.has_value()) {
+    check_same(a, *bias, "a/bias");
+    TORCH_CHECK(bias->dim() == 1 && bias->size(0) == N && bias->is_contiguous(), "gemm_tn: bias must be [N]");
+    bias_ptr = bias->data_ptr();
+  }
+  const int dt = dtype_code(a.scalar_type(), "gemm_tn");
+  const c10::hip::OptionalHIPGuard guard(a.device());
+  check_status(dk_gemm_tn(dt, a.data_ptr(), b.data_ptr(), bias_ptr, c.data_ptr(), static_cast<int>(M),
+                          static_cast<int>(N), static_cast<int>(K), static_cast<int>(a.stride(0)),
+                          static_cast<int>(b.stride(0)), static_cast<int>(c.stride(0)), stream_of(a)),
+               "gemm_tn");
+}
+
+// ---------------------------------------------------------------------------
+// rms_norm / fused_add_rms_norm / silu_and_mul (csrc/ops.cu:200-265)
+// ---------------------------------------------------------------------------
+void rms_norm(at::Tensor& out, const at::Tensor& input, const at::Tensor& weight, double eps) {
+  TORCH_CHECK(input.is_cuda(), "rms_norm: input must be on CUDA");
+  check_same(input, out, "input/out");
+  check_same(input, weight, "input/weight");
+  TORCH_CHECK(out.sizes() == input.sizes(), "rms_norm: out must match input shape");
+  const int64_t H = input.size(-1);
+  TORCH_CHECK(weight.dim() == 1 && weight.size(0) == H && weight.is_contiguous(), "rms_norm: weight must be [H]");
+  const int64_t rows = input.numel() / std::max<int64_t>(H, 1);
+  const int64_t in_stride = row_stride(input, "rms_norm(input)");
+  const int64_t out_stride = row_stride(out, "rms_norm(out)");
+  const int dt = dtype_code(input.scalar_type(), "rms_norm");
+  const c10::hip::OptionalHIPGuard guard(input.device());
+  check_status(dk_rms_norm(dt, out.data_ptr(), input.data_ptr(), weight.data_ptr(), static_cast<int>(rows),
+                           static_cast<int>(H), in_stride, out_stride, static_cast<float>(eps), stream_of(input)),
+               "rms_norm");
+}
+
+void fused_add_rms_norm(at::Tensor& input, at::Tensor& residual, const at::Tensor& weight, double eps) {
+  TORCH_CHECK(input.is_cuda(), "fused_add_rms_norm: input must be on CUDA");
+  check_same(input, residual, "input/residual");
+  check_same(input, weight, "input/weight");
+  TORCH_CHECK(residual.sizes() == input.sizes(), "fused_add_rms_norm: residual must match input shape");
+  const int64_t H = input.size(-1);
+  TORCH_CHECK(weight.dim() == 1 && weight.size(0) == H && weight.is_contiguous(),
+              "fused_add_rms_norm: weight must be [H]");
+  const int64_t rows = input.numel() / std::max<int64_t>(H, 1);
+  const int64_t in_stride = row_stride(input, "fused_add_rms_norm(input)");
+  const int64_t res_stride = row_stride(residual, "fused_add_rms_norm(residual)");
+  const int dt = dtype_code(input.scalar_type(), "fused_add_rms_norm");
+  const c10::hip::OptionalHIPGuard guard(input.device());
+  check_status(dk_fused_add_rms_norm(dt, input.data_ptr(), residual.data_ptr(), weight.data_ptr(),
+                                     static_cast<int>(rows), static_cast<int>(H), in_stride, res_stride,
+                                     static_cast<float>(eps), stream_of(input)),
+               "fused_add_rms_norm");
+}
+
+void silu_and_mul(at::Tensor& out, const at::Tensor& input) {
+  TORCH_CHECK(input.is_cuda(), "silu_and_mul: input must be on CUDA");
+  check_same(input, out, "input/out");
+  const int64_t d = input.size(-1) / 2;
+  TORCH_CHECK(input.size(-1) == 2 * d, "silu_and_mul: last dimension must be even");
+  TORCH_CHECK(out.size(-1) == d && out.numel() * 2 == input.numel(), "silu_and_mul: out must be [..., d]");
+  const int64_t rows = d == 0 ? 0 : input.numel() / (2 * d);
+  const int64_t in_stride = row_stride(input, "silu_and_mul(input)");
+  const int64_t out_stride = row_stride(out, "silu_and_mul(out)");
+  const int dt = dtype_code(input.scalar_type(), "silu_and_mul");
+  const c10::hip::OptionalHIPGuard guard(input.device());
+  check_status(dk_silu_and_mul(dt, out.data_ptr(), input.data_ptr(), static_cast<int>(rows), static_cast<int>(d),
+                               in_stride, out_stride, stream_of(input)),
+               "silu_and_mul");
+}
+
+// ---------------------------------------------------------------------------
+// Registration (csrc/ops.cu:270-286)
+// ---------------------------------------------------------------------------
+TORCH_LIBRARY(decode_kernels, m) {
+  m.def(
+      "paged_attention_decode(Tensor! out, Tensor q, Tensor k_cache, Tensor v_cache, Tensor block_tables, "
+      "Tensor seq_lens, float scale, int max_seq_len, Tensor! tmp_out, Tensor! max_logits, Tensor! exp_sums) -> ()");
+  m.def("gemm_tn(Tensor! c, Tensor a, Tensor b, Tensor? bias) -> ()");
+  m.def("rms_norm(Tensor! out, Tensor input, Tensor weight, float eps) -> ()");
+  m.def("fused_add_rms_norm(Tensor! input, Tensor! residual, Tensor weight, float eps) -> ()");
+  m.def("silu_and_mul(Tensor! out, Tensor input) -> ()");
+}
+
+TORCH_LIBRARY_IMPL(decode_kernels, CUDA, m) {
+  m.impl("paged_attention_decode", &paged_attention_decode);
+  m.impl("gemm_tn", &gemm_tn);
+  m.impl("rms_norm", &rms_norm);
+  m.impl("fused_add_rms_norm", &fused_add_rms_norm);
+  m.impl("silu_and_mul", &silu_and_mul);
+}
+
+// Python module entry point: an empty module; importing it loads this
+// library and runs the registrations above.
+static struct PyModuleDef dk_module = {PyModuleDef_HEAD_INIT, "_C",
+                                       "decodekernels_amd._C: registers torch.ops.decode_kernels.* (gfx950 HIP kernels)",
+                                       -1, nullptr};
+
+PyMODINIT_FUNC PyInit__C(void) { return PyModule_Create(&dk_module); }

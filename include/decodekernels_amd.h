@@ -1,0 +1,124 @@
+/*
+ * decodekernels_amd — C ABI of the MI355X (gfx950) decode kernels.
+ *
+ * This is the torch-free boundary of the library: plain pointers, element
+ * strides and sizes, a dtype code and a HIP stream passed as `void*`.
+ * Every entry point validates its arguments on the host first, then enqueues
+ * work on `stream` and returns without synchronising. The return value is a
+ * hipError_t code (0 = success); for argument errors the code is
+ * hipErrorInvalidValue (1) and dk_last_error() describes the failure.
+ * No entry point allocates device memory, so all of them can be recorded
+ * into a HIP graph.
+ *
+ * Each function replaces one launcher of DecodeKernels (the reference), whose
+ * `dk::launch_*<T>` templates take the same argument lists for one element
+ * type T in {__half, __nv_bfloat16}; here the type is the `dtype` argument.
+ */
+#ifndef DECODEKERNELS_AMD_H_
+#define DECODEKERNELS_AMD_H_
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Element type of every 16-bit tensor argument. */
+enum dk_dtype {
+  DK_FLOAT16 = 0,
+  DK_BFLOAT16 = 1,
+};
+
+/* Tokens per split-K partition of the workspace contract (reference:
+ * csrc/paged_attention.cuh:34, decode_kernels/ops.py:14). */
+#define DK_PARTITION_SIZE 512
+/* Largest GQA group (query heads per KV head) (csrc/paged_attention.cuh:37). */
+#define DK_MAX_GQA_GROUP 8
+
+/*
+ * Launch descriptor of paged decode attention. Same fields and meaning as
+ * the reference's `dk::PagedAttnParams` (csrc/paged_attention.cuh:39-58):
+ *   out          [num_seqs, num_q_heads, head_dim]              (dtype)
+ *   q            [num_seqs, num_q_heads, head_dim]              (dtype)
+ *   k/v_cache    [num_blocks, block_size, num_kv_heads, head_dim] (dtype),
+ *                any strides on the first three dims, head_dim contiguous
+ *   block_tables [num_seqs, >= max blocks per seq] int32, row stride bt_stride
+ *   seq_lens     [num_seqs] int32, read on the device
+ *   tmp_out      [num_seqs, num_q_heads, max_partitions, head_dim] fp32  } only when
+ *   max_logits   [num_seqs, num_q_heads, max_partitions] fp32           } max_seq_len
+ *   exp_sums     [num_seqs, num_q_heads, max_partitions] fp32           } > 512
+ * Strides are in elements.
+ */
+typedef struct dk_paged_attn_params {
+  void* out;
+  const void* q;
+  const void* k_cache;
+  const void* v_cache;
+  const int32_t* block_tables;
+  const int32_t* seq_lens;
+  float* tmp_out;
+  float* max_logits;
+  float* exp_sums;
+  int64_t q_stride_seq, q_stride_head;
+  int64_t out_stride_seq, out_stride_head;
+  int64_t k_stride_block, k_stride_token, k_stride_head;
+  int64_t v_stride_block, v_stride_token, v_stride_head;
+  int64_t bt_stride;
+  int32_t num_seqs, num_q_heads, num_kv_heads, block_size, max_partitions;
+  float scale;
+} dk_paged_attn_params;
+
+/*
+ * Single-token decode attention over a paged KV cache, with flash-decoding
+ * split-K when max_seq_len > DK_PARTITION_SIZE.
+ * Replaces dk::launch_paged_attention_decode<T> (csrc/paged_attention.cuh:312-333).
+ * head_dim in {64, 128, 256}; num_q_heads / num_kv_heads <= DK_MAX_GQA_GROUP.
+ * max_seq_len is an upper bound on seq_lens that selects the single-pass or
+ * split-K path; with split-K, p->max_partitions must be >= ceil(max_seq_len / 512).
+ */
+int dk_paged_attention_decode(const dk_paged_attn_params* p, int dtype, int head_dim, int max_seq_len, void* stream);
+
+/*
+ * C[M,N] = A[M,K] * B[N,K]^T (+ bias[N]), fp32 accumulation, one rounding.
+ * Replaces dk::launch_gemm_tn<T> (csrc/gemm_wmma.cuh:209-219).
+ * K, lda and ldb must be multiples of 8; A and B 16-byte aligned; bias may be NULL.
+ */
+int dk_gemm_tn(int dtype, const void* A, const void* B, const void* bias, void* C, int M, int N, int K, int lda,
+               int ldb, int ldc, void* stream);
+
+/*
+ * out = x * rsqrt(mean(x^2) + eps) * weight, per row of H elements.
+ * Replaces dk::launch_rms_norm<T> (csrc/norm_act.cuh:153-166).
+ */
+int dk_rms_norm(int dtype, void* out, const void* input, const void* weight, int rows, int H, int64_t in_stride,
+                int64_t out_stride, float eps, void* stream);
+
+/*
+ * In place: residual = round(input + residual); input = rms_norm(residual) * weight.
+ * Replaces dk::launch_fused_add_rms_norm<T> (csrc/norm_act.cuh:168-183).
+ */
+int dk_fused_add_rms_norm(int dtype, void* input, void* residual, const void* weight, int rows, int H,
+                          int64_t in_stride, int64_t res_stride, float eps, void* stream);
+
+/*
+ * out[r, :d] = silu(input[r, :d]) * input[r, d:2d].
+ * Replaces dk::launch_silu_and_mul<T> (csrc/norm_act.cuh:185-198).
+ */
+int dk_silu_and_mul(int dtype, void* out, const void* input, int rows, int d, int64_t in_stride, int64_t out_stride,
+                    void* stream);
+
+/* Description of the last argument error raised on this thread ("" if none).
+ * The reference reports these through TORCH_CHECK messages (csrc/ops.cu). */
+const char* dk_last_error(void);
+
+/* hipGetErrorString for a code returned above. */
+const char* dk_error_string(int code);
+
+/* Library version string. */
+const char* dk_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DECODEKERNELS_AMD_H_ */

@@ -1,0 +1,71 @@
+"""Shared helpers of the GPU parity tests: oracle evaluation on the CPU and the
+tolerances of the acceptance bar.
+
+* attention and GEMM: max abs error against the *unrounded* fp32 oracle,
+  <= 2e-2 for bf16 and <= 5e-3 for fp16;
+* norms and activation: at most 1 ulp of the model dtype from the oracle's
+  (rounded) output; the fused residual is bit-exact.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from oracle.reference import (
+    fused_add_rms_norm_reference,
+    gemm_reference,
+    paged_attention_reference,
+    rms_norm_reference,
+    silu_and_mul_reference,
+)
+
+MAX_ABS = {torch.bfloat16: 2e-2, torch.float16: 5e-3}
+
+
+def attention_f32(q, k_cache, v_cache, block_tables, seq_lens, scale=None) -> torch.Tensor:
+    """fp32 oracle output (no final rounding), computed on the CPU."""
+    return paged_attention_reference(
+        q.float().cpu(), k_cache.float().cpu(), v_cache.float().cpu(), block_tables.cpu(), seq_lens.cpu(), scale
+    )
+
+
+def gemm_f32(a, b, bias=None) -> torch.Tensor:
+    return gemm_reference(a.float().cpu(), b.float().cpu(), None if bias is None else bias.float().cpu())
+
+
+def assert_max_abs(got: torch.Tensor, ref_f32: torch.Tensor, dtype: torch.dtype, what: str = "") -> float:
+    err = (got.float().cpu() - ref_f32.float()).abs().max().item() if got.numel() else 0.0
+    assert err <= MAX_ABS[dtype], f"{what} max abs error {err:.3e} > {MAX_ABS[dtype]:.0e} ({dtype})"
+    assert torch.isfinite(got).all(), f"{what} non-finite output"
+    return err
+
+
+def ulp_distance(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
+    """Elementwise distance in units in the last place between two 16-bit float tensors."""
+    assert a.dtype == b.dtype and a.dtype in (torch.float16, torch.bfloat16)
+
+    def key(t):
+        bits = t.contiguous().view(torch.int16).to(torch.int32) & 0xFFFF
+        mag = bits & 0x7FFF
+        return torch.where(bits >= 0x8000, -mag, mag)
+
+    return (key(a.cpu()) - key(b.cpu())).abs()
+
+
+def assert_ulp(got: torch.Tensor, ref: torch.Tensor, max_ulp: int = 1, what: str = "") -> int:
+    d = int(ulp_distance(got, ref).max().item()) if got.numel() else 0
+    assert d <= max_ulp, f"{what} {d} ulp from the oracle (> {max_ulp})"
+    return d
+
+
+__all__ = [
+    "MAX_ABS",
+    "assert_max_abs",
+    "assert_ulp",
+    "attention_f32",
+    "fused_add_rms_norm_reference",
+    "gemm_f32",
+    "rms_norm_reference",
+    "silu_and_mul_reference",
+    "ulp_distance",
+]
