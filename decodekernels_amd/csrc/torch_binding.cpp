@@ -13,8 +13,8 @@
 #include <Python.h>
 
 #include <ATen/ATen.h>
-#include <c10/hip/HIPGuard.h>
-#include <c10/hip/HIPStream.h>
+#include <ATen/hip/impl/HIPGuardImplMasqueradingAsCUDA.h>
+#include <ATen/hip/impl/HIPStreamMasqueradingAsCUDA.h>
 #include <torch/library.h>
 
 #include <algorithm>
@@ -43,8 +43,12 @@ void check_same(const at::Tensor& a, const at::Tensor& b, const char* what) {
   TORCH_CHECK(a.device() == b.device(), what, ": tensors must be on the same device");
 }
 
+// PyTorch-ROCm reports HIP devices as DeviceType::CUDA, so its "masquerading"
+// guard and stream accessors are the ones that accept these tensors.
+using DeviceGuard = c10::hip::OptionalHIPGuardMasqueradingAsCUDA;
+
 void* stream_of(const at::Tensor& t) {
-  return static_cast<void*>(c10::hip::getCurrentHIPStream(t.device().index()).stream());
+  return static_cast<void*>(c10::hip::getCurrentHIPStreamMasqueradingAsCUDA(t.device().index()).stream());
 }
 
 bool aligned(const void* p, int64_t bytes) { return reinterpret_cast<uintptr_t>(p) % static_cast<uintptr_t>(bytes) == 0; }
@@ -154,7 +158,7 @@ void paged_attention_decode(at::Tensor& out, const at::Tensor& q, const at::Tens
   p.scale = static_cast<float>(scale);
 
   const int dt = dtype_code(q.scalar_type(), "paged_attention_decode");
-  const c10::hip::OptionalHIPGuard guard(q.device());
+  const DeviceGuard guard(q.device());
   check_status(dk_paged_attention_decode(&p, dt, static_cast<int>(head_dim), static_cast<int>(max_seq_len),
                                          stream_of(q)),
                "paged_attention_decode");
@@ -182,7 +186,7 @@ void gemm_tn(at::Tensor& c, const at::Tensor& a, const at::Tensor& b, const std:
     bias_ptr = bias->data_ptr();
   }
   const int dt = dtype_code(a.scalar_type(), "gemm_tn");
-  const c10::hip::OptionalHIPGuard guard(a.device());
+  const DeviceGuard guard(a.device());
   check_status(dk_gemm_tn(dt, a.data_ptr(), b.data_ptr(), bias_ptr, c.data_ptr(), static_cast<int>(M),
                           static_cast<int>(N), static_cast<int>(K), static_cast<int>(a.stride(0)),
                           static_cast<int>(b.stride(0)), static_cast<int>(c.stride(0)), stream_of(a)),
@@ -203,7 +207,7 @@ void rms_norm(at::Tensor& out, const at::Tensor& input, const at::Tensor& weight
   const int64_t in_stride = row_stride(input, "rms_norm(input)");
   const int64_t out_stride = row_stride(out, "rms_norm(out)");
   const int dt = dtype_code(input.scalar_type(), "rms_norm");
-  const c10::hip::OptionalHIPGuard guard(input.device());
+  const DeviceGuard guard(input.device());
   check_status(dk_rms_norm(dt, out.data_ptr(), input.data_ptr(), weight.data_ptr(), static_cast<int>(rows),
                            static_cast<int>(H), in_stride, out_stride, static_cast<float>(eps), stream_of(input)),
                "rms_norm");
@@ -221,7 +225,7 @@ void fused_add_rms_norm(at::Tensor& input, at::Tensor& residual, const at::Tenso
   const int64_t in_stride = row_stride(input, "fused_add_rms_norm(input)");
   const int64_t res_stride = row_stride(residual, "fused_add_rms_norm(residual)");
   const int dt = dtype_code(input.scalar_type(), "fused_add_rms_norm");
-  const c10::hip::OptionalHIPGuard guard(input.device());
+  const DeviceGuard guard(input.device());
   check_status(dk_fused_add_rms_norm(dt, input.data_ptr(), residual.data_ptr(), weight.data_ptr(),
                                      static_cast<int>(rows), static_cast<int>(H), in_stride, res_stride,
                                      static_cast<float>(eps), stream_of(input)),
@@ -238,7 +242,7 @@ void silu_and_mul(at::Tensor& out, const at::Tensor& input) {
   const int64_t in_stride = row_stride(input, "silu_and_mul(input)");
   const int64_t out_stride = row_stride(out, "silu_and_mul(out)");
   const int dt = dtype_code(input.scalar_type(), "silu_and_mul");
-  const c10::hip::OptionalHIPGuard guard(input.device());
+  const DeviceGuard guard(input.device());
   check_status(dk_silu_and_mul(dt, out.data_ptr(), input.data_ptr(), static_cast<int>(rows), static_cast<int>(d),
                                in_stride, out_stride, stream_of(input)),
                "silu_and_mul");

@@ -1,8 +1,12 @@
 """Shared helpers of the GPU parity tests: oracle evaluation on the CPU and the
 tolerances of the acceptance bar.
 
-* attention and GEMM: max abs error against the *unrounded* fp32 oracle,
-  <= 2e-2 for bf16 and <= 5e-3 for fp16;
+* attention and GEMM: abs error against the *unrounded* fp32 oracle of at
+  most 2e-2 for bf16 and 5e-3 for fp16, plus half an ulp of the model dtype at
+  the reference value -- the final rounding to bf16/fp16 that the reference
+  itself performs (``.to(q.dtype)``), which alone exceeds 5e-3 once |out| >= 16
+  in fp16 (e.g. attention over outlier V rows). For |ref| < 1 the extra term is
+  at most 2.4e-4 (fp16) / 2e-3 (bf16);
 * norms and activation: at most 1 ulp of the model dtype from the oracle's
   (rounded) output; the fused residual is bit-exact.
 """
@@ -33,11 +37,26 @@ def gemm_f32(a, b, bias=None) -> torch.Tensor:
     return gemm_reference(a.float().cpu(), b.float().cpu(), None if bias is None else bias.float().cpu())
 
 
+def half_ulp(ref_f32: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
+    """Half the spacing of `dtype` at |ref| (the worst-case rounding of a correct result)."""
+    a = ref_f32.float().abs().to(dtype)
+    return 0.5 * (torch.nextafter(a, torch.full_like(a, float("inf"))) - a).float()
+
+
 def assert_max_abs(got: torch.Tensor, ref_f32: torch.Tensor, dtype: torch.dtype, what: str = "") -> float:
-    err = (got.float().cpu() - ref_f32.float()).abs().max().item() if got.numel() else 0.0
-    assert err <= MAX_ABS[dtype], f"{what} max abs error {err:.3e} > {MAX_ABS[dtype]:.0e} ({dtype})"
+    """Asserts |got - ref| <= MAX_ABS[dtype] + half_ulp(ref) elementwise; returns the max abs error."""
     assert torch.isfinite(got).all(), f"{what} non-finite output"
-    return err
+    if got.numel() == 0:
+        return 0.0
+    ref = ref_f32.float().cpu()
+    diff = (got.float().cpu() - ref).abs()
+    excess = diff - (MAX_ABS[dtype] + half_ulp(ref, dtype))
+    worst = int(excess.argmax())
+    assert excess.max().item() <= 0, (
+        f"{what} abs error {diff.flatten()[worst].item():.3e} at |ref| = {ref.flatten()[worst].abs().item():.3g} "
+        f"exceeds {MAX_ABS[dtype]:.0e} + half an ulp ({dtype})"
+    )
+    return diff.max().item()
 
 
 def ulp_distance(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
