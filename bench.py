@@ -21,8 +21,8 @@ sample before anything is reported.
 batch 1 and 4, HND cache, 1% outlier rows), the head-dim-256 / group-8 stress
 batch, gemm_tn at the decode-layer shapes next to hipBLASLt (``F.linear``),
 and the norm / activation ops -- each timed as the median of cold-cache calls
-(a 1 GiB buffer is rewritten before every call, larger than the 256 MB
-Infinity Cache).
+(a 1 GiB buffer is read before every call, 4x the 256 MB Infinity
+Cache).
 """
 
 from __future__ import annotations
@@ -109,10 +109,12 @@ _FLUSH: torch.Tensor | None = None
 
 
 def flush_caches() -> None:
+    """Reads 1 GiB (4x the Infinity Cache) so the next call starts cold. A read,
+    not a write: dirty lines left behind would be written back during the call."""
     global _FLUSH
     if _FLUSH is None:
-        _FLUSH = torch.empty(FLUSH_BYTES // 4, dtype=torch.int32, device="cuda")
-    _FLUSH.add_(1)
+        _FLUSH = torch.ones(FLUSH_BYTES // 4, dtype=torch.int32, device="cuda")
+    torch.amax(_FLUSH)
 
 
 def time_back_to_back(fn, steps: int, warmup: int) -> float:
