@@ -7,11 +7,15 @@
 // Two kernels, both on v_mfma_f32_16x16x32_{bf16,f16}:
 //
 // * skinny (M <= 64, decode): the op streams the weight matrix once, so it is
-//   bound by HBM bandwidth. A workgroup owns 16 output columns and all M rows;
-//   its 4 waves split K into interleaved 32-column steps, each lane loading 16
-//   bytes of a weight row per step straight into its MFMA operand, U steps in
-//   flight per wave. The activations (<= 64 rows) are read through L2, where
-//   they stay resident. The 4 partial tiles are summed through LDS.
+//   bound by HBM bandwidth -- and, per CU, by how many cache lines its loads
+//   touch: an MFMA fragment load of 16 rows touches 16 lines. Weight fragments
+//   therefore go straight to registers (each weight byte is used once), while
+//   activation tiles are loaded once per workgroup with contiguous 16-byte
+//   loads into LDS and shared by the waves that own different output columns.
+//   8 waves per workgroup, split between N (16 columns each) and K so that a
+//   launch keeps >= 192 workgroups; buffer loads with descriptor bounds make
+//   rows past M/N and columns past K read as zero, and a DEPTH-deep register
+//   ring keeps weight loads in flight across the per-step barrier.
 // * tiled (M > 64, prefill): 128x128 output tile per 256-thread workgroup,
 //   2x2 waves of 64x64, K in 64-column stages double-buffered in LDS (rows
 //   padded by 16 bytes against bank conflicts); the next stage's global loads
@@ -19,6 +23,8 @@
 #include "../../include/decodekernels_amd.h"
 #include "dk_device.h"
 #include "dk_host.h"
+
+
 
 namespace dk {
 namespace gemm {
@@ -32,61 +38,160 @@ __device__ __forceinline__ u32x4 frag_or_zero(const uint16_t* base, int64_t ld, 
 // ---------------------------------------------------------------------------
 // Skinny kernel
 // ---------------------------------------------------------------------------
-constexpr int kSkinnyWaves = 4;
-constexpr int kSkinnyThreads = kSkinnyWaves * kWave;
+// Word 3 of a gfx9-family buffer resource for raw (untyped) loads.
+constexpr int kRsrcWord3 = 0x00020000;
+// Byte offset that is outside every buffer resource used here: loads there
+// return zero without touching memory.
+constexpr int kOutOfRange = 0x7fffffff;
 
-template <typename E, int MT, int U>
-__global__ __launch_bounds__(kSkinnyThreads) void gemm_skinny_kernel(const uint16_t* __restrict__ A,
-                                                                     const uint16_t* __restrict__ B,
-                                                                     const uint16_t* __restrict__ bias,
-                                                                     uint16_t* __restrict__ C, int M, int N, int K,
-                                                                     int lda, int ldb, int ldc) {
-  __shared__ f32x4 red[kSkinnyWaves][MT][kWave];
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base, int64_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0,
+                                           static_cast<int>(bytes < kOutOfRange ? bytes : kOutOfRange), kRsrcWord3);
+}
+
+// ---------------------------------------------------------------------------
+// Skinny kernel (M <= 64) with LDS-shared activations
+// ---------------------------------------------------------------------------
+// Workgroup = WN x WK waves: wave (wn, wk) owns output columns n0 + 16 wn ...
+// and K chunks c = j * WK + wk (BK = 64 columns each). The activation tile
+// of a chunk (16 MT rows x 64) is loaded once per K-group with contiguous
+// 16-byte loads (8 lanes cover a 128-byte row segment), written to LDS and
+// read by the WN waves of that group, so each activation byte crosses the
+// L1 once per workgroup instead of once per wave. Weight fragments go
+// straight from HBM to registers through a DEPTH-deep ring. All waves step
+// through the chunks together (one barrier per step); the WK partial tiles
+// are summed through LDS at the end.
+constexpr int kLdsBK = 64;
+constexpr int kLdsARow = kLdsBK + 8;  // padded LDS row (elements)
+
+template <int MT, int WN>
+struct ARegs {
+  static constexpr int kVecs = 16 * MT * kLdsBK / 8;                             // 16-byte vectors per tile
+  static constexpr int kPerLane = (kVecs + WN * kWave - 1) / (WN * kWave);     // per lane of the K-group
+  static constexpr bool kPartial = kVecs % (WN * kWave) != 0;                  // some lanes idle
+  u32x4 v[kPerLane];
+};
+
+template <typename E, int MT, int WN, int WK, int DEPTH>
+__global__ __launch_bounds__(WN * WK * kWave) void gemm_skinny_lds_kernel(const uint16_t* __restrict__ A,
+                                                                          const uint16_t* __restrict__ B,
+                                                                          const uint16_t* __restrict__ bias,
+                                                                          uint16_t* __restrict__ C, int M, int N,
+                                                                          int K, int lda, int ldb, int ldc) {
+  constexpr int NT = WN * WK * kWave;
+  constexpr int KS = kLdsBK / 32;  // k-steps per chunk
+  using AR = ARegs<MT, WN>;
+  static_assert(!AR::kPartial || AR::kPerLane == 1, "a partial activation load is one vector per lane");
+  // The activation tiles and, after the K loop's last barrier, the partial
+  // output tiles share one LDS allocation.
+  constexpr size_t kBytesA = sizeof(uint16_t) * WK * 2 * 16 * MT * kLdsARow;
+  constexpr size_t kBytesRed = sizeof(f32x4) * WK * WN * MT * kWave;
+  __shared__ __attribute__((aligned(16))) unsigned char smem[kBytesA > kBytesRed ? kBytesA : kBytesRed];
+  auto lds_a = reinterpret_cast<uint16_t(*)[2][16 * MT * kLdsARow]>(smem);
+  auto red = reinterpret_cast<f32x4(*)[WN][MT][kWave]>(smem);
+
   const int lane = threadIdx.x % kWave;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const int wn = wave % WN;
+  const int wk = wave / WN;
+  const int gl = wn * kWave + lane;  // lane index inside the K-group
   const int l16 = lane % 16;
   const int lg = lane / 16;
-  const int n0 = blockIdx.x * 16;
+  const int n0 = blockIdx.x * (16 * WN);
+  const int ncol0 = n0 + 16 * wn;
+
+  const __amdgpu_buffer_rsrc_t rb =
+      rsrc(B + static_cast<int64_t>(ncol0) * ldb, static_cast<int64_t>(max(0, min(16, N - ncol0))) * ldb * 2);
+  const __amdgpu_buffer_rsrc_t ra = rsrc(A, static_cast<int64_t>(M) * lda * 2);
+  const __amdgpu_buffer_rsrc_t r_none = rsrc(A, 0);
+  const int boff = l16 * ldb * 2 + 16 * lg;
+
+  const int n_chunks = (K + kLdsBK - 1) / kLdsBK;
+  const int steps = (n_chunks + WK - 1) / WK;  // chunk steps of the whole workgroup
+
+  // Activation tile of chunk c: vector v of the group covers row v / 8, columns 8 (v % 8) ...
+  auto load_a = [&](int step, AR& r) {
+    const int c = step * WK + wk;
+    const bool live = step < steps && c < n_chunks;
+    const __amdgpu_buffer_rsrc_t rr = live ? ra : r_none;
+#pragma unroll
+    for (int j = 0; j < AR::kPerLane; ++j) {
+      const int v = gl + j * WN * kWave;
+      const int row = v / 8;
+      const int k = c * kLdsBK + 8 * (v % 8);
+      const bool in = k < K && (!AR::kPartial || v < AR::kVecs);
+      r.v[j] = __builtin_amdgcn_raw_buffer_load_b128(rr, in ? row * lda * 2 + 2 * k : kOutOfRange, 0, 0);
+    }
+  };
+  auto store_a = [&](int buf, const AR& r) {
+#pragma unroll
+    for (int j = 0; j < AR::kPerLane; ++j) {
+      const int v = gl + j * WN * kWave;
+      if (!AR::kPartial || v < AR::kVecs) *reinterpret_cast<u32x4*>(&lds_a[wk][buf][(v / 8) * kLdsARow + 8 * (v % 8)]) = r.v[j];
+    }
+  };
+  // Weight fragments of chunk step `step` for this wave: KS k-steps.
+  auto load_b = [&](int step, u32x4 (&bf)[KS]) {
+    const int c = step * WK + wk;
+    const bool live = step < steps && c < n_chunks;
+    const __amdgpu_buffer_rsrc_t rr = live ? rb : r_none;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      const int k = c * kLdsBK + 32 * s + 8 * lg;
+      bf[s] = __builtin_amdgcn_raw_buffer_load_b128(rr, k < K ? boff + 2 * (c * kLdsBK + 32 * s) : kOutOfRange, 0, 0);
+    }
+  };
 
   f32x4 acc[MT];
 #pragma unroll
   for (int i = 0; i < MT; ++i) acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  const int ksteps = (K + 31) / 32;
-  const int brow = n0 + l16;
-  // Round j of wave w covers k-steps (j * kSkinnyWaves + w) * U + u, u < U.
-  for (int base = wave * U; base < ksteps; base += kSkinnyWaves * U) {
-    u32x4 bf[U];
-    u32x4 af[U][MT];
+  u32x4 bring[DEPTH][KS];
+  AR areg;
+  load_a(0, areg);
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int k = (base + u) * 32 + 8 * lg;
-      bf[u] = frag_or_zero(B, ldb, brow, N, k, K);
+  for (int d = 0; d < DEPTH; ++d) load_b(d, bring[d]);
+  store_a(0, areg);
+  load_a(1, areg);
+  __syncthreads();
+
+  for (int base = 0; base < steps; base += DEPTH) {
 #pragma unroll
-      for (int i = 0; i < MT; ++i) af[u][i] = frag_or_zero(A, lda, 16 * i + l16, M, k, K);
-    }
+    for (int d = 0; d < DEPTH; ++d) {
+      const int step = base + d;
+      if (step < steps) {
+        const uint16_t* at = lds_a[wk][step & 1];
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
+        for (int s = 0; s < KS; ++s) {
 #pragma unroll
-      for (int i = 0; i < MT; ++i) acc[i] = E::mfma_16x16x32(af[u][i], bf[u], acc[i]);
+          for (int i = 0; i < MT; ++i) {
+            const u32x4 af = *reinterpret_cast<const u32x4*>(&at[(16 * i + l16) * kLdsARow + 32 * s + 8 * lg]);
+            acc[i] = E::mfma_16x16x32(af, bring[d][s], acc[i]);
+          }
+        }
+      }
+      load_b(step + DEPTH, bring[d]);
+      if (step + 1 < steps) store_a((step + 1) & 1, areg);
+      load_a(step + 2, areg);
+      __syncthreads();
     }
   }
 
 #pragma unroll
-  for (int i = 0; i < MT; ++i) red[wave][i][lane] = acc[i];
+  for (int i = 0; i < MT; ++i) red[wk][wn][i][lane] = acc[i];
   __syncthreads();
 
-  // Output element e of this tile: row m = e / 16, column n0 + e % 16.
-  for (int e = threadIdx.x; e < MT * 16 * 16; e += kSkinnyThreads) {
-    const int m = e / 16;
-    const int n = n0 + e % 16;
+  // acc[i] of wave (wn, *) lane l, reg r: C[16 i + 4 (l/16) + r][n0 + 16 wn + l % 16].
+  for (int e = threadIdx.x; e < MT * 16 * 16 * WN; e += NT) {
+    const int cn = e % (16 * WN);
+    const int m = e / (16 * WN);
+    const int n = n0 + cn;
     if (m >= M || n >= N) continue;
-    // acc layout: tile i = m / 16, lane = 16 * ((m % 16) / 4) + (n % 16), reg (m % 4).
     const int i = m / 16;
-    const int src_lane = 16 * ((m % 16) / 4) + (e % 16);
+    const int src_lane = 16 * ((m % 16) / 4) + (cn % 16);
     float v = 0.0f;
 #pragma unroll
-    for (int w = 0; w < kSkinnyWaves; ++w) v += red[w][i][src_lane][m % 4];
+    for (int w = 0; w < WK; ++w) v += red[w][cn / 16][i][src_lane][m % 4];
     if (bias != nullptr) v += E::to_float(bias[n]);
     C[static_cast<int64_t>(m) * ldc + n] = E::from_float(v);
   }
@@ -196,14 +301,31 @@ template <typename E>
 hipError_t launch(const uint16_t* A, const uint16_t* B, const uint16_t* bias, uint16_t* C, int M, int N, int K,
                   int lda, int ldb, int ldc, hipStream_t s) {
   if (M <= 64) {
-    const dim3 grid(static_cast<unsigned>(ceil_div64(N, 16)));
-    const dim3 block(kSkinnyThreads);
-    if (M <= 16) {
-      hipLaunchKernelGGL((gemm_skinny_kernel<E, 1, 8>), grid, block, 0, s, A, B, bias, C, M, N, K, lda, ldb, ldc);
-    } else if (M <= 32) {
-      hipLaunchKernelGGL((gemm_skinny_kernel<E, 2, 4>), grid, block, 0, s, A, B, bias, C, M, N, K, lda, ldb, ldc);
-    } else {
-      hipLaunchKernelGGL((gemm_skinny_kernel<E, 4, 4>), grid, block, 0, s, A, B, bias, C, M, N, K, lda, ldb, ldc);
+    {
+      // 8 waves; as many along N as keep >= 192 workgroups (more columns per
+      // workgroup share each activation tile), the rest split K.
+      const int wn = (M > 32 && N >= 24576) ? 8 : (N >= 64 * 192 ? 4 : (N >= 32 * 192 ? 2 : 1));
+      const int mt = M <= 16 ? 1 : (M <= 32 ? 2 : 4);
+      const dim3 g2(static_cast<unsigned>(ceil_div64(N, 16 * wn)));
+      const dim3 b2(8 * kWave);
+#define DK_SKINNY_LDS(MT_, WN_)                                                                               \
+  hipLaunchKernelGGL((gemm_skinny_lds_kernel<E, MT_, WN_, 8 / WN_, 3>), g2, b2, 0, s, A, B, bias, C, M, N, K, lda, \
+                     ldb, ldc)
+      switch (mt * 10 + wn) {
+        case 11: DK_SKINNY_LDS(1, 1); break;
+        case 12: DK_SKINNY_LDS(1, 2); break;
+        case 14: DK_SKINNY_LDS(1, 4); break;
+        case 21: DK_SKINNY_LDS(2, 1); break;
+        case 22: DK_SKINNY_LDS(2, 2); break;
+        case 24: DK_SKINNY_LDS(2, 4); break;
+        case 18: DK_SKINNY_LDS(1, 8); break;
+        case 28: DK_SKINNY_LDS(2, 8); break;
+        case 41: DK_SKINNY_LDS(4, 1); break;
+        case 42: DK_SKINNY_LDS(4, 2); break;
+        case 44: DK_SKINNY_LDS(4, 4); break;
+        default: DK_SKINNY_LDS(4, 8); break;
+      }
+#undef DK_SKINNY_LDS
     }
     return hipGetLastError();
   }
@@ -229,6 +351,8 @@ extern "C" int dk_gemm_tn(int dtype, const void* A, const void* B, const void* b
   if (!aligned_to(A, 16) || !aligned_to(B, 16)) return fail("gemm_tn: a and b must be 16-byte aligned");
   if (C == nullptr || (K > 0 && (A == nullptr || B == nullptr))) return fail("gemm_tn: pointers must not be NULL");
   if (M > 64 && ceil_div64(M, gemm::kBM) > 65535) return fail("gemm_tn: M is too large");
+  if (M <= 64 && (static_cast<int64_t>(M) * lda * 2 >= (int64_t{1} << 31) || int64_t{16} * ldb * 2 >= (int64_t{1} << 31)))
+    return fail("gemm_tn: row strides too large for 32-bit buffer offsets");
   hipStream_t s = static_cast<hipStream_t>(stream);
   const auto* a = static_cast<const uint16_t*>(A);
   const auto* b = static_cast<const uint16_t*>(B);
