@@ -264,6 +264,37 @@ def cpu_baseline_and_check(case, budget_s: float = 20.0) -> dict:
     }
 
 
+TRAFFIC_PROFILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
+                               "paged_attention_llama3_8b_b64_bf16_traffic.md")
+CALIBRATION_BYTES = 256 << 20
+
+
+def pmc_workload(calls: int = 5) -> None:
+    """What the counter runs profile: the headline op `calls` times, then a
+    copy of CALIBRATION_BYTES (read once, written once) to scale the counters."""
+    case = llama3_8b_decode_case()
+    for _ in range(calls):
+        case["run"]()
+    torch.cuda.synchronize()
+    src = torch.ones(CALIBRATION_BYTES // 4, dtype=torch.int32, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(calls):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(f"pmc workload done: {calls} attention calls, {calls} copies of {CALIBRATION_BYTES >> 20} MiB", flush=True)
+
+
+def measured_traffic() -> int | None:
+    """HBM bytes per headline call from the committed counter summary, if any."""
+    try:
+        for line in open(TRAFFIC_PROFILE):
+            if line.startswith("traffic_bytes_per_call:"):
+                return int(line.split(":")[1])
+    except OSError:
+        pass
+    return None
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -271,6 +302,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-extras", action="store_true", help="skip the secondary configs")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline (and its correctness check)")
+    ap.add_argument("--pmc-workload", action="store_true", help="run only what the rocprofv3 --pmc passes profile")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: every work unit of this path fits one MI355X and no multi-GPU "
@@ -278,6 +310,9 @@ def main() -> int:
         return 2
     if not dk.is_available():
         raise RuntimeError("decodekernels_amd HIP extension not available (build it with __graft_entry__.build())")
+    if args.pmc_workload:
+        pmc_workload()
+        return 0
 
     case = llama3_8b_decode_case()
     case["run"]()
@@ -310,7 +345,7 @@ def main() -> int:
         },
         "roofline": {
             "bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+            "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
         },
     }
     if not args.no_cpu:
