@@ -51,6 +51,12 @@ constexpr int kPart = DK_PARTITION_SIZE;  // workspace granularity (tokens)
 #ifndef DK_ATTN_LOAD_AUX
 #define DK_ATTN_LOAD_AUX 0  // cache-policy bits of the K/V buffer loads
 #endif
+#ifndef DK_ATTN_OCC_D128
+#define DK_ATTN_OCC_D128 2  // waves per SIMD targeted at head_dim 128
+#endif
+#ifndef DK_ATTN_OCC_D64
+#define DK_ATTN_OCC_D64 4  // waves per SIMD targeted at head_dim 64
+#endif
 #ifndef DK_ATTN_UNIT_SLOTS
 #define DK_ATTN_UNIT_SLOTS 2  // 512-token workspace slots per split-K work unit (1 or 2)
 #endif
@@ -125,9 +131,18 @@ struct TileRegs {
 // than this, so accumulators are rescaled rarely (weights stay <= 2^8).
 constexpr float kLazyMax = 8.0f;
 
+// Waves per SIMD the register allocation targets: head_dim 64 fits four and
+// head_dim 128 three without spilling; head_dim 256 keeps its natural
+// allocation (one wave, no spills).
+template <int D>
+constexpr int attn_occupancy() {
+  return D >= 256 ? 1 : (D == 128 ? DK_ATTN_OCC_D128 : DK_ATTN_OCC_D64);
+}
+
 // NW waves per workgroup; each wave keeps DEPTH tiles of loads in flight.
 template <typename E, int D, bool SPLIT, bool BS16, int ALIGN, int NW>
-__global__ __launch_bounds__(NW * kWave) void paged_attention_kernel(const KParams p) {
+__global__ __launch_bounds__(NW * kWave) __attribute__((amdgpu_waves_per_eu(attn_occupancy<D>(), attn_occupancy<D>())))
+void paged_attention_kernel(const KParams p) {
   constexpr int CH = D / 32;  // 32-column chunks per row
   constexpr int NB = D / 16;  // 16-column output blocks
   constexpr int DEPTH = D >= 256 ? 2 : DK_ATTN_DEPTH;
