@@ -1,0 +1,246 @@
+"""Swap the decode kernels into vLLM.
+
+Same API and rules as DecodeKernels' ``decode_kernels/vllm_patch.py``
+(written against vLLM 0.32): three substitutions, each behind a strict
+eligibility check that falls back to vLLM's own code for anything it does not
+handle, with counters so a silent fallback cannot pass for a result.
+
+* attention ``forward`` of vLLM's decode backends -- pure-decode batches (one
+  query token per request) run ``paged_attention_decode`` on vLLM's KV cache
+  in place. The reference patches ``FlashAttentionImpl``; on ROCm builds of
+  vLLM the decode path may live in the ROCm or Triton backend instead, so every
+  known backend class that exists is patched. The cache layout is read from
+  the tensor: the interleaved ``[blocks, kv_heads, block_size, 2*head_dim]``
+  buffer (viewed as strided K and V, as the reference does) or a stacked
+  ``[2, blocks, block_size, kv_heads, head_dim]`` pair.
+* ``RMSNorm.forward_cuda`` -- rms_norm / fused_add_rms_norm.
+* ``SiluAndMul.forward_cuda`` -- silu_and_mul.
+
+Prefill and mixed batches, quantized KV caches, sliding windows, ALiBi,
+soft-capping, attention sinks, context parallelism, cross/encoder attention and
+graph capture all go to vLLM's implementation
+(reference: decode_kernels/vllm_patch.py:60-99).
+"""
+
+from __future__ import annotations
+
+import importlib
+import logging
+
+import torch
+
+from . import ops as dk_ops
+
+logger = logging.getLogger("decodekernels_amd.vllm")
+
+_STATS = {
+    "attention_kernel_calls": 0,
+    "attention_fallback_calls": 0,
+    "rms_norm_kernel_calls": 0,
+    "rms_norm_fallback_calls": 0,
+    "silu_and_mul_kernel_calls": 0,
+    "silu_and_mul_fallback_calls": 0,
+}
+_APPLIED: set[str] = set()
+_HALF_TYPES = (torch.float16, torch.bfloat16)
+
+# (module, class) of vLLM attention backends whose decode path can be swapped.
+ATTENTION_BACKENDS = (
+    ("vllm.v1.attention.backends.flash_attn", "FlashAttentionImpl"),
+    ("vllm.v1.attention.backends.rocm_attn", "RocmAttentionImpl"),
+    ("vllm.v1.attention.backends.triton_attn", "TritonAttentionImpl"),
+)
+
+
+def stats() -> dict[str, int]:
+    """How often each patched op used the decode kernels vs fell back."""
+    return dict(_STATS)
+
+
+def reset_stats() -> None:
+    for k in _STATS:
+        _STATS[k] = 0
+
+
+# ---------------------------------------------------------------------------
+# Attention
+# ---------------------------------------------------------------------------
+def _decoder_attention_type():
+    """vLLM's AttentionType.DECODER (its value is the string "decoder")."""
+    try:
+        from vllm.v1.attention.backend import AttentionType
+
+        return AttentionType.DECODER
+    except Exception:  # noqa: BLE001  (vLLM absent or moved: compare by value)
+        return "decoder"
+
+
+def split_kv_cache(kv_cache: torch.Tensor, head_size: int):
+    """K and V views [blocks, block_size, kv_heads, head_dim] of vLLM's cache, or None
+    for a layout the kernels do not read."""
+    if kv_cache.dim() == 4 and kv_cache.shape[-1] == 2 * head_size:
+        # [blocks, kv_heads, block_size, 2*D] -> two strided NHD views (reference: vllm_patch.py:121-122).
+        k, v = kv_cache.transpose(1, 2).split(head_size, dim=-1)
+        return k, v
+    if kv_cache.dim() == 5 and kv_cache.shape[0] == 2 and kv_cache.shape[-1] == head_size:
+        return kv_cache[0], kv_cache[1]
+    return None
+
+
+def _attention_eligible(impl, query, kv_cache, attn_metadata, output, output_scale, output_block_scale) -> bool:
+    """The reference's eligibility rules (decode_kernels/vllm_patch.py:60-99), plus a cache-layout check."""
+    if attn_metadata is None or output_scale is not None or output_block_scale is not None:
+        return False
+    if query.is_cuda and torch.cuda.is_current_stream_capturing():
+        # The single-pass / split-K choice depends on the host-side max_seq_len,
+        # which a captured graph would freeze.
+        return False
+    if getattr(impl, "attn_type", _decoder_attention_type()) != _decoder_attention_type():
+        return False
+    if getattr(attn_metadata, "max_query_len", None) != 1:
+        return False
+    if getattr(impl, "dcp_world_size", 1) > 1:
+        return False
+    if str(getattr(impl, "kv_cache_dtype", "auto")) not in ("auto", "float16", "bfloat16") or kv_cache.dtype != query.dtype:
+        return False
+    if query.dtype not in _HALF_TYPES:
+        return False
+    if getattr(impl, "alibi_slopes", None) is not None or getattr(impl, "logits_soft_cap", None):
+        return False
+    if getattr(impl, "sliding_window", None) not in (None, (-1, -1)):
+        return False
+    if getattr(impl, "sinks", None) is not None:
+        return False
+    if impl.head_size not in dk_ops.SUPPORTED_HEAD_DIMS:
+        return False
+    if impl.num_heads % impl.num_kv_heads or impl.num_heads // impl.num_kv_heads > dk_ops.MAX_GQA_GROUP:
+        return False
+    if getattr(attn_metadata, "causal", True) is not True:
+        return False
+    if getattr(attn_metadata, "mm_prefix_query_range_tensor", None) is not None:
+        return False
+    if getattr(attn_metadata, "rswa_prefix_lens", None) is not None:
+        return False
+    n = attn_metadata.num_actual_tokens
+    if attn_metadata.seq_lens.shape[0] < n or attn_metadata.block_table.shape[0] < n:
+        return False
+    if not output.is_contiguous():
+        return False
+    if split_kv_cache(kv_cache, impl.head_size) is None:
+        return False
+    return True
+
+
+def _make_attention_forward(original):
+    def forward(self, layer, query, key, value, kv_cache, attn_metadata, output=None, output_scale=None,
+                output_block_scale=None, *args, **kwargs):
+        if output is not None and not args and not kwargs and _attention_eligible(
+            self, query, kv_cache, attn_metadata, output, output_scale, output_block_scale
+        ):
+            n = attn_metadata.num_actual_tokens
+            key_cache, value_cache = split_kv_cache(kv_cache, self.head_size)
+            q = query[:n].reshape(n, self.num_heads, self.head_size)
+            out = output[:n].view(n, self.num_heads, self.head_size)
+            dk_ops.paged_attention_decode(
+                q,
+                key_cache,
+                value_cache,
+                attn_metadata.block_table,
+                attn_metadata.seq_lens,
+                scale=self.scale,
+                max_seq_len=attn_metadata.max_seq_len,
+                out=out,
+            )
+            _STATS["attention_kernel_calls"] += 1
+            return output
+        _STATS["attention_fallback_calls"] += 1
+        return original(self, layer, query, key, value, kv_cache, attn_metadata, output, output_scale,
+                        output_block_scale, *args, **kwargs)
+
+    forward.__wrapped__ = original  # type: ignore[attr-defined]
+    return forward
+
+
+def _patch_attention() -> None:
+    patched = []
+    for module_name, class_name in ATTENTION_BACKENDS:
+        try:
+            cls = getattr(importlib.import_module(module_name), class_name)
+        except Exception:  # noqa: BLE001  (backend not present in this vLLM build)
+            continue
+        cls.forward = _make_attention_forward(cls.forward)
+        patched.append(class_name)
+    if not patched:
+        raise ImportError("no supported vLLM attention backend found to patch")
+    logger.info("decodekernels_amd: attention patched in %s", patched)
+
+
+# ---------------------------------------------------------------------------
+# RMSNorm and SiluAndMul
+# ---------------------------------------------------------------------------
+def _patch_rms_norm() -> None:
+    import vllm.envs as envs
+    from vllm.model_executor.layers.layernorm import RMSNorm
+
+    original = RMSNorm.forward_cuda
+
+    def forward_cuda(self, x, residual=None):
+        eligible = (
+            not getattr(envs, "VLLM_BATCH_INVARIANT", False)
+            and not torch.compiler.is_compiling()
+            and getattr(self, "variance_size_override", None) is None
+            and getattr(self, "has_weight", True)
+            and x.dtype in _HALF_TYPES
+            and self.weight.dtype == x.dtype
+            and x.shape[-1] == self.hidden_size
+            and x.stride(-1) == 1
+            and (residual is None or (residual.dtype == x.dtype and residual.shape == x.shape))
+        )
+        if not eligible:
+            _STATS["rms_norm_fallback_calls"] += 1
+            return original(self, x, residual)
+        _STATS["rms_norm_kernel_calls"] += 1
+        if residual is None:
+            return dk_ops.rms_norm(x, self.weight.data, self.variance_epsilon)
+        return dk_ops.fused_add_rms_norm(x, residual, self.weight.data, self.variance_epsilon)
+
+    forward_cuda.__wrapped__ = original  # type: ignore[attr-defined]
+    RMSNorm.forward_cuda = forward_cuda
+
+
+def _patch_silu_and_mul() -> None:
+    from vllm.model_executor.layers.activation import SiluAndMul
+
+    original = SiluAndMul.forward_cuda
+
+    def forward_cuda(self, x):
+        if x.dtype in _HALF_TYPES and not torch.compiler.is_compiling() and x.stride(-1) == 1:
+            _STATS["silu_and_mul_kernel_calls"] += 1
+            return dk_ops.silu_and_mul(x)
+        _STATS["silu_and_mul_fallback_calls"] += 1
+        return original(self, x)
+
+    forward_cuda.__wrapped__ = original  # type: ignore[attr-defined]
+    SiluAndMul.forward_cuda = forward_cuda
+
+
+_PATCHERS = {
+    "attention": _patch_attention,
+    "rms_norm": _patch_rms_norm,
+    "silu_and_mul": _patch_silu_and_mul,
+}
+
+
+def apply(ops: list[str] | None = None) -> None:
+    """Install the patches (idempotent) (reference: decode_kernels/vllm_patch.py:200-212)."""
+    if not dk_ops.is_available():
+        logger.warning("decodekernels_amd: HIP extension unavailable; vLLM left unpatched")
+        return
+    for name in ops or list(_PATCHERS):
+        if name not in _PATCHERS:
+            raise ValueError(f"unknown op {name!r}; choose from {sorted(_PATCHERS)}")
+        if name in _APPLIED:
+            continue
+        _PATCHERS[name]()
+        _APPLIED.add(name)
+    logger.info("decodekernels_amd: patched vLLM ops %s", sorted(_APPLIED))
