@@ -20,7 +20,8 @@ sample before anything is reported.
 ``extras``: the other BASELINE configs -- 128K-token split-K decode (fp16,
 batch 1 and 4, HND cache, 1% outlier rows), the head-dim-256 / group-8 stress
 batch, gemm_tn at the decode-layer shapes next to hipBLASLt (``F.linear``),
-and the norm / activation ops -- each timed as the median of cold-cache calls
+the norm / activation ops, and one Llama-3-8B decoder layer's decode step
+end to end (eager and HIP graph) -- each op timed as the median of cold-cache calls
 (a 1 GiB buffer is read before every call, 4x the 256 MB Infinity
 Cache).
 """
@@ -161,11 +162,9 @@ def extras_attention() -> dict:
         res[f"split_k_128k_b{b}_fp16"] = {**t, "GB/s": round(gbs, 1), "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 1),
                                            "MB": round(c["bytes"] / 1e6, 1)}
         del c
-    g = torch.Generator().manual_seed(5)
-    lens = torch.exp(torch.rand(256, generator=g) * math.log(32768)).long().clamp(1, 32768)
-    lens[torch.randperm(256, generator=g)[:8]] = 0
+    lens = c5_seq_lens()
     for dtype, tag in ((torch.float16, "fp16"), (torch.bfloat16, "bf16")):
-        c = attention_case(256, 16, 2, 256, 32, lens.tolist(), dtype, "nhd", seed=20)
+        c = attention_case(256, 16, 2, 256, 32, lens, dtype, "nhd", seed=20)
         t = time_cold(c["run"], iters=20)
         gbs = c["bytes"] / (t["median_us"] * 1e-6) / 1e9
         res[f"d256_g8_stress_{tag}"] = {**t, "GB/s": round(gbs, 1), "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 1),
@@ -178,10 +177,11 @@ def extras_gemm() -> dict:
     torch.backends.cuda.preferred_blas_library("cublaslt")  # hipBLASLt on ROCm
     res = {}
     g = torch.Generator(device="cuda").manual_seed(30)
-    for name, n in (("qkv", 6144), ("o", 4096), ("gate_up", 28672)):
-        w = torch.randn(n, 4096, generator=g, device="cuda", dtype=torch.bfloat16) * 0.02
-        for m in (1, 8, 32, 64, 4096):
-            a = torch.randn(m, 4096, generator=g, device="cuda", dtype=torch.bfloat16) * 0.02
+    for name, n, k, ms in (("qkv", 6144, 4096, (1, 8, 32, 64, 256, 4096)), ("o", 4096, 4096, (1, 8, 32, 64, 256, 4096)),
+                           ("gate_up", 28672, 4096, (1, 8, 32, 64, 256, 4096)), ("down", 4096, 14336, (64, 256, 4096))):
+        w = torch.randn(n, k, generator=g, device="cuda", dtype=torch.bfloat16) * 0.02
+        for m in ms:
+            a = torch.randn(m, k, generator=g, device="cuda", dtype=torch.bfloat16) * 0.02
             out = torch.empty(m, n, device="cuda", dtype=torch.bfloat16)
             torch.ops.decode_kernels.gemm_tn(out, a, w, None)
             ref = F.linear(a, w)
@@ -191,8 +191,8 @@ def extras_gemm() -> dict:
             iters = 10 if m == 4096 else 30
             t_dk = time_cold(lambda: torch.ops.decode_kernels.gemm_tn(out, a, w, None), iters=iters)
             t_bl = time_cold(lambda: F.linear(a, w), iters=iters)
-            flops = 2.0 * m * n * 4096
-            nbytes = (m * 4096 + n * 4096 + m * n) * 2
+            flops = 2.0 * m * n * k
+            nbytes = (m * k + n * k + m * n) * 2
             res[f"{name}_M{m}"] = {
                 "dk_us": t_dk["median_us"], "hipblaslt_us": t_bl["median_us"],
                 "dk_over_hipblaslt": round(t_dk["median_us"] / t_bl["median_us"], 3),
@@ -222,6 +222,102 @@ def extras_norms() -> dict:
     ):
         tm = time_cold(fn, iters=50)
         res[name] = {**tm, "GB/s": round(nbytes / (tm["median_us"] * 1e-6) / 1e9, 1)}
+    return res
+
+
+def c5_seq_lens(num_seqs: int = 256, seed: int = 5) -> list:
+    """Log-uniform lengths in [1, 32768] with 8 zero-length sequences."""
+    g = torch.Generator().manual_seed(seed)
+    lens = torch.exp(torch.rand(num_seqs, generator=g) * math.log(32768)).long().clamp(1, 32768)
+    lens[torch.randperm(num_seqs, generator=g)[:8]] = 0
+    return lens.tolist()
+
+
+def layer_step(num_seqs, hq, hkv, d, bs, seq_lens, dtype, layout, seed, hidden=4096, inter=14336):
+    """One random-init decoder layer's decode step on this path: fused_add_rms_norm
+    -> qkv gemm -> paged attention (q read in place from the qkv output) -> o gemm
+    -> fused_add_rms_norm -> gate_up gemm -> silu_and_mul -> down gemm. Appending
+    the new token's K/V to the cache is the serving engine's job and is not
+    part of it. Returns the per-op callables and the bytes the step must move."""
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    kw = dict(device="cuda", dtype=dtype)
+    nqkv = (hq + 2 * hkv) * d
+    w_qkv = torch.randn(nqkv, hidden, generator=g, **kw) * 0.02
+    w_o = torch.randn(hidden, hq * d, generator=g, **kw) * 0.02
+    w_gu = torch.randn(2 * inter, hidden, generator=g, **kw) * 0.02
+    w_down = torch.randn(hidden, inter, generator=g, **kw) * 0.02
+    ln1 = (1 + 0.1 * torch.randn(hidden, generator=g, device="cuda")).to(dtype)
+    ln2 = (1 + 0.1 * torch.randn(hidden, generator=g, device="cuda")).to(dtype)
+    case = attention_case(num_seqs, hq, hkv, d, bs, seq_lens, dtype, layout, seed=seed + 1)
+    x = torch.randn(num_seqs, hidden, generator=g, **kw)
+    resid = torch.randn(num_seqs, hidden, generator=g, **kw)
+    qkv = torch.empty(num_seqs, nqkv, **kw)
+    attn = torch.empty(num_seqs, hq, d, **kw)
+    o = torch.empty(num_seqs, hidden, **kw)
+    gu = torch.empty(num_seqs, 2 * inter, **kw)
+    act = torch.empty(num_seqs, inter, **kw)
+    down = torch.empty(num_seqs, hidden, **kw)
+    max_len = max(max(seq_lens), 1)
+    ws = dk.alloc_workspace(num_seqs, hq, d, max_len, "cuda")
+    q = qkv[:, : hq * d].view(num_seqs, hq, d)
+    dko = torch.ops.decode_kernels
+    ops = {
+        "fused_add_rms_norm": lambda: dko.fused_add_rms_norm(x, resid, ln1, 1e-5),
+        "qkv_gemm": lambda: dko.gemm_tn(qkv, x, w_qkv, None),
+        "attention": lambda: dk.paged_attention_decode(q, case["k"], case["v"], case["bt"], case["lens"],
+                                                       max_seq_len=max_len, out=attn, workspace=ws),
+        "o_gemm": lambda: dko.gemm_tn(o, attn.view(num_seqs, hq * d), w_o, None),
+        "fused_add_rms_norm_2": lambda: dko.fused_add_rms_norm(o, resid, ln2, 1e-5),
+        "gate_up_gemm": lambda: dko.gemm_tn(gu, o, w_gu, None),
+        "silu_and_mul": lambda: dko.silu_and_mul(act, gu),
+        "down_gemm": lambda: dko.gemm_tn(down, act, w_down, None),
+    }
+    elt = torch.finfo(dtype).bits // 8
+    nbytes = case["bytes"] + elt * (w_qkv.numel() + w_o.numel() + w_gu.numel() + w_down.numel())
+    return ops, nbytes
+
+
+def extras_layer_step() -> dict:
+    """The single-layer decode step timed end to end, eager
+    (back to back) and as one captured HIP graph replayed back to back, next to
+    the sum of its ops timed one by one from cold caches. Hidden 4096 and MLP
+    14336 as Llama-3-8B; attention at the head-dim-256 / group-8 stress shape
+    (256 seqs, qkv N = 5120) and at the Llama-3-8B batch-64 shape."""
+    res = {}
+    cases = (
+        ("d256_g8_b256_bf16", (256, 16, 2, 256, 32, c5_seq_lens(), torch.bfloat16, "nhd")),
+        ("d256_g8_b256_fp16", (256, 16, 2, 256, 32, c5_seq_lens(), torch.float16, "nhd")),
+        ("llama3_8b_b64_bf16", (64, 32, 8, 128, 16, torch.randint(512, 4097, (64,), generator=torch.Generator().manual_seed(0)).tolist(),
+                                torch.bfloat16, "vllm")),
+    )
+    for name, args in cases:
+        ops, nbytes = layer_step(*args, seed=50)
+
+        def step():
+            for fn in ops.values():
+                fn()
+
+        step()
+        torch.cuda.synchronize()
+        per_op = {k: time_cold(fn, iters=20)["median_us"] for k, fn in ops.items()}
+        eager_us = time_back_to_back(step, 20, 3) * 1e3
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            step()
+        torch.cuda.current_stream().wait_stream(side)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            step()
+        graph_us = time_back_to_back(graph.replay, 20, 3) * 1e3
+        res[name] = {
+            "eager_us": round(eager_us, 1), "graph_us": round(graph_us, 1),
+            "sum_of_cold_ops_us": round(sum(per_op.values()), 1), "ops_cold_us": per_op,
+            "weights_plus_kv_MB": round(nbytes / 1e6, 1),
+            "graph_GB/s": round(nbytes / (graph_us * 1e-6) / 1e9, 1),
+        }
+        del ops, graph
+        torch.cuda.empty_cache()
     return res
 
 
@@ -353,7 +449,8 @@ def main() -> int:
     del case
     torch.cuda.empty_cache()
     if not args.no_extras:
-        result["extras"] = {"attention": extras_attention(), "gemm_bf16_K4096": extras_gemm(), "norm_act_bf16": extras_norms()}
+        result["extras"] = {"attention": extras_attention(), "gemm_bf16": extras_gemm(), "norm_act_bf16": extras_norms(),
+                            "decode_layer_step_bf16": extras_layer_step()}
     print(json.dumps(result), flush=True)
     return 0
 

@@ -16,24 +16,17 @@
 //   launch keeps >= 192 workgroups; buffer loads with descriptor bounds make
 //   rows past M/N and columns past K read as zero, and a DEPTH-deep register
 //   ring keeps weight loads in flight across the per-step barrier.
-// * tiled (M > 64, prefill): 128x128 output tile per 256-thread workgroup,
-//   2x2 waves of 64x64, K in 64-column stages double-buffered in LDS (rows
-//   padded by 16 bytes against bank conflicts); the next stage's global loads
-//   are in flight while the current stage is multiplied.
+// * LDS-DMA (M > 64, batched decode and prefill): A and B tiles go from HBM
+//   straight into LDS (buffer_load ... lds), bank-conflict-free XOR-swizzled,
+//   through a multi-stage ring; five tile shapes from 256x256 down to 64x64,
+//   picked per call by a throughput model so that batches of a few hundred
+//   rows still fill all 256 CUs.
 #include "../../include/decodekernels_amd.h"
 #include "dk_device.h"
 #include "dk_host.h"
 
-
-
 namespace dk {
 namespace gemm {
-
-// MFMA operand fragment: 8 consecutive K elements of one row.
-__device__ __forceinline__ u32x4 frag_or_zero(const uint16_t* base, int64_t ld, int row, int rows, int k, int K) {
-  if (row < rows && k < K) return *reinterpret_cast<const u32x4*>(base + row * ld + k);
-  return u32x4{0u, 0u, 0u, 0u};
-}
 
 // ---------------------------------------------------------------------------
 // Skinny kernel
@@ -198,103 +191,210 @@ __global__ __launch_bounds__(WN * WK * kWave) void gemm_skinny_lds_kernel(const 
 }
 
 // ---------------------------------------------------------------------------
-// Tiled kernel (128 x 128 x 64)
+// LDS-DMA kernel (M > 64)
 // ---------------------------------------------------------------------------
-constexpr int kBM = 128;
-constexpr int kBN = 128;
-constexpr int kBK = 64;
-constexpr int kLdsRow = kBK + 8;  // padded LDS row, in elements
-constexpr int kTiledThreads = 256;
+// BM x BN output tile per workgroup of WM x WN waves. K advances in 64-column
+// slices; a slice of A (BM rows) and of B (BN rows) goes from HBM straight into
+// LDS with buffer_load ... lds (16 bytes per lane, one 1 KB instruction per 8
+// rows, no registers), through a STAGES-deep ring: slice t + STAGES - 1 is in
+// flight while slice t is multiplied. A slice row is 128 bytes = 8 chunks of 16
+// bytes, and chunk c of row r is stored at position c ^ (r & 7). gfx950's LDS
+// has 64 banks of 4 bytes and serves a ds_read_b128 in four cycles of 16 lanes:
+// the lanes that share bit 5 and the parity of bits 2..4 of the lane id
+// (measured with SQ_LDS_BANK_CONFLICT on pairs of active lanes). A fragment
+// read (lane l: row l % 16, chunk 2 (l / 32) + (l / 16) % 2 + 4 h) puts 8 rows
+// with chunk c and 8 rows with chunk c ^ 1 in each such group, and the XOR
+// sends those 16 reads to 16 distinct 16-byte bank groups; unswizzled or
+// 16-byte-padded rows conflict 2-way. The load lanes fetch the permuted chunks,
+// so global reads stay whole 128-byte row segments.
+//
+// Tiles are numbered so that each XCD (workgroups go to the 8 XCDs round
+// robin) takes a contiguous run of them, walked in groups of kGroupM tile rows:
+// the ~32 workgroups resident on one XCD share A rows and B rows in its L2.
+constexpr int kDmaBK = 64;
+constexpr int kXcds = 8;
+constexpr int kGroupM = 4;
 
-template <typename E>
-__global__ __launch_bounds__(kTiledThreads) void gemm_tiled_kernel(const uint16_t* __restrict__ A,
+__device__ __forceinline__ int swz(int r) { return r & 7; }
+
+template <int BM, int BN>
+__device__ __forceinline__ void dma_tile_of(int id, int tiles_m, int tiles_n, int& tm, int& tn) {
+  const int total = tiles_m * tiles_n;
+  int pid = id;
+  if (total % kXcds == 0) pid = (id % kXcds) * (total / kXcds) + id / kXcds;
+  const int per_group = kGroupM * tiles_n;
+  const int first_m = (pid / per_group) * kGroupM;
+  const int gm = min(tiles_m - first_m, kGroupM);
+  tm = first_m + (pid % per_group) % gm;
+  tn = (pid % per_group) / gm;
+}
+
+template <typename E, int BM, int BN, int WM, int WN, int STAGES>
+__global__ __launch_bounds__(WM * WN * kWave) void gemm_dma_kernel(const uint16_t* __restrict__ A,
                                                                    const uint16_t* __restrict__ B,
                                                                    const uint16_t* __restrict__ bias,
                                                                    uint16_t* __restrict__ C, int M, int N, int K,
-                                                                   int lda, int ldb, int ldc) {
-  __shared__ uint16_t As[2][kBM * kLdsRow];
-  __shared__ uint16_t Bs[2][kBN * kLdsRow];
-  const int tid = threadIdx.x;
-  const int lane = tid % kWave;
-  const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
-  const int wm = wave / 2;
-  const int wn = wave % 2;
+                                                                   int lda, int ldb, int ldc, int vec_store) {
+  constexpr int NW = WM * WN;
+  constexpr int TM = BM / WM / 16;  // 16-row fragments per wave
+  constexpr int TN = BN / WN / 16;
+  constexpr int LA = BM / 8 / NW;   // 1 KB DMA loads per wave per slice
+  constexpr int LB = BN / 8 / NW;
+  constexpr int kSlice = (BM + BN) * 8;  // u32x4 per slice
+  static_assert(BM % (8 * NW) == 0 && BN % (8 * NW) == 0 && TM >= 1 && TN >= 1, "tile shape");
+  static_assert(STAGES >= 2 && (STAGES - 2) * (LA + LB) < 64, "vmcnt range");
+  __shared__ u32x4 lds[STAGES * kSlice];
+
+  const int lane = threadIdx.x % kWave;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const int wm = wave % WM;
+  const int wn = wave / WM;
   const int l16 = lane % 16;
   const int lg = lane / 16;
-  const int m0 = blockIdx.y * kBM;
-  const int n0 = blockIdx.x * kBN;
 
-  // Global -> register staging: each thread moves 4 A and 4 B vectors per stage.
-  constexpr int kVecPerRow = kBK / 8;                          // 8
-  constexpr int kLoads = kBM * kVecPerRow / kTiledThreads;     // 4
-  u32x4 ra[kLoads], rb[kLoads];
-  auto gload = [&](int k0) {
+  const int tiles_m = (M + BM - 1) / BM;
+  const int tiles_n = (N + BN - 1) / BN;
+  int tm, tn;
+  dma_tile_of<BM, BN>(blockIdx.x, tiles_m, tiles_n, tm, tn);
+  const int m0 = tm * BM;
+  const int n0 = tn * BN;
+  const int rows_a = min(BM, M - m0);
+  const int rows_b = min(BN, N - n0);
+  // Rows past M (N) lie past num_records and read as zero.
+  const __amdgpu_buffer_rsrc_t ra =
+      rsrc(A + static_cast<int64_t>(m0) * lda, (static_cast<int64_t>(rows_a - 1) * lda + K) * 2);
+  const __amdgpu_buffer_rsrc_t rb =
+      rsrc(B + static_cast<int64_t>(n0) * ldb, (static_cast<int64_t>(rows_b - 1) * ldb + K) * 2);
+
+  // DMA lane roles: load j of this wave fills tile rows 8 g .. 8 g + 7 (g = wave + j NW);
+  // lane l writes position l % 8 of row 8 g + l / 8, i.e. chunk (l % 8) ^ swz(row).
+  int offa[LA], ka[LA], offb[LB], kb[LB];
 #pragma unroll
-    for (int j = 0; j < kLoads; ++j) {
-      const int v = tid + j * kTiledThreads;
-      const int row = v / kVecPerRow;
-      const int col = (v % kVecPerRow) * 8;
-      ra[j] = frag_or_zero(A, lda, m0 + row, M, k0 + col, K);
-      rb[j] = frag_or_zero(B, ldb, n0 + row, N, k0 + col, K);
+  for (int j = 0; j < LA; ++j) {
+    const int r = 8 * (wave + j * NW) + lane / 8;
+    const int c = (lane % 8) ^ swz(r);
+    ka[j] = 8 * c;
+    offa[j] = r < rows_a ? r * lda * 2 + 16 * c : kOutOfRange;
+  }
+#pragma unroll
+  for (int j = 0; j < LB; ++j) {
+    const int r = 8 * (wave + j * NW) + lane / 8;
+    const int c = (lane % 8) ^ swz(r);
+    kb[j] = 8 * c;
+    offb[j] = r < rows_b ? r * ldb * 2 + 16 * c : kOutOfRange;
+  }
+  // Issued for every slice index, also past the last one (those lanes are out
+  // of range and move no data), so each wave always has the same count in flight.
+  auto issue = [&](int t, int buf) {
+    const int k0 = t * kDmaBK;
+    u32x4* base = lds + buf * kSlice;
+#pragma unroll
+    for (int j = 0; j < LA; ++j) {
+      const int off = (offa[j] != kOutOfRange && k0 + ka[j] < K) ? offa[j] + 2 * k0 : kOutOfRange;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          ra, (__attribute__((address_space(3))) void*)(base + (wave + j * NW) * 64), 16, off, 0, 0, 0);
+    }
+#pragma unroll
+    for (int j = 0; j < LB; ++j) {
+      const int off = (offb[j] != kOutOfRange && k0 + kb[j] < K) ? offb[j] + 2 * k0 : kOutOfRange;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          rb, (__attribute__((address_space(3))) void*)(base + BM * 8 + (wave + j * NW) * 64), 16, off, 0, 0, 0);
     }
   };
-  auto lstore = [&](int stage) {
-#pragma unroll
-    for (int j = 0; j < kLoads; ++j) {
-      const int v = tid + j * kTiledThreads;
-      const int row = v / kVecPerRow;
-      const int col = (v % kVecPerRow) * 8;
-      *reinterpret_cast<u32x4*>(&As[stage][row * kLdsRow + col]) = ra[j];
-      *reinterpret_cast<u32x4*>(&Bs[stage][row * kLdsRow + col]) = rb[j];
-    }
-  };
 
-  f32x4 acc[4][4];
+  // Fragment read offsets (u32x4) inside a slice, for the two 32-column halves.
+  int ia[TM][2], ib[TN][2];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < TM; ++i) {
+    const int r = wm * (BM / WM) + 16 * i + l16;
+    ia[i][0] = r * 8 + (lg ^ swz(r));
+    ia[i][1] = r * 8 + ((4 + lg) ^ swz(r));
+  }
 #pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-  const int stages = (K + kBK - 1) / kBK;
-  gload(0);
-  lstore(0);
-  __syncthreads();
-  for (int s = 0; s < stages; ++s) {
-    const int cur = s & 1;
-    if (s + 1 < stages) gload((s + 1) * kBK);
-#pragma unroll
-    for (int kk = 0; kk < kBK; kk += 32) {
-      u32x4 af[4], bf[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-        af[i] = *reinterpret_cast<const u32x4*>(&As[cur][(wm * 64 + 16 * i + l16) * kLdsRow + kk + 8 * lg]);
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-        bf[j] = *reinterpret_cast<const u32x4*>(&Bs[cur][(wn * 64 + 16 * j + l16) * kLdsRow + kk + 8 * lg]);
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = E::mfma_16x16x32(af[i], bf[j], acc[i][j]);
-    }
-    if (s + 1 < stages) lstore(cur ^ 1);
-    __syncthreads();
+  for (int j = 0; j < TN; ++j) {
+    const int r = wn * (BN / WN) + 16 * j + l16;
+    ib[j][0] = BM * 8 + r * 8 + (lg ^ swz(r));
+    ib[j][1] = BM * 8 + r * 8 + ((4 + lg) ^ swz(r));
   }
 
-  // Epilogue: acc[i][j] lane l reg r -> C[m0 + wm*64 + 16i + 4*lg + r][n0 + wn*64 + 16j + l16].
+  f32x4 acc[TM][TN];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int n = n0 + wn * 64 + 16 * j + l16;
-    if (n >= N) continue;
-    const float b = bias != nullptr ? E::to_float(bias[n]) : 0.0f;
+  for (int i = 0; i < TM; ++i)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int j = 0; j < TN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  const int ktiles = (K + kDmaBK - 1) / kDmaBK;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int m = m0 + wm * 64 + 16 * i + 4 * lg + r;
-        if (m < M) C[static_cast<int64_t>(m) * ldc + n] = E::from_float(acc[i][j][r] + b);
+  for (int s = 0; s < STAGES - 1; ++s) issue(s, s);
+
+  // vmcnt(n) with expcnt / lgkmcnt left at their maxima (gfx9 encoding).
+  constexpr int kWaitN = (STAGES - 2) * (LA + LB);
+  constexpr int kWaitImm = (kWaitN & 15) | ((kWaitN >> 4) << 14) | (7 << 4) | (15 << 8);
+
+  for (int t0 = 0; t0 < ktiles; t0 += STAGES) {
+#pragma unroll
+    for (int u = 0; u < STAGES; ++u) {
+      if (t0 + u < ktiles) {
+        // This wave's loads of slice t0 + u have landed; the barrier extends that
+        // to every wave and ensures all reads of the buffer refilled next are done.
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_waitcnt(kWaitImm);
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_sched_barrier(0);
+        issue(t0 + u + STAGES - 1, (u + STAGES - 1) % STAGES);
+        const u32x4* sl = lds + u * kSlice;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          u32x4 af[TM], bf[TN];
+#pragma unroll
+          for (int i = 0; i < TM; ++i) af[i] = sl[ia[i][h]];
+#pragma unroll
+          for (int j = 0; j < TN; ++j) bf[j] = sl[ib[j][h]];
+#pragma unroll
+          for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int j = 0; j < TN; ++j) acc[i][j] = E::mfma_16x16x32(bf[j], af[i], acc[i][j]);
+        }
       }
     }
   }
+
+  // The loads issued past the last slice move no data, but none may still be
+  // in flight into this workgroup's LDS when it exits.
+  __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));
+
+  // acc[i][j] lane l, reg r = C[m0 + wm BM/WM + 16 i + l % 16][n0 + wn BN/WN + 16 j + 4 (l / 16) + r].
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+    const int m = m0 + wm * (BM / WM) + 16 * i + l16;
+    if (m >= M) continue;
+    uint16_t* crow = C + static_cast<int64_t>(m) * ldc;
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const int n = n0 + wn * (BN / WN) + 16 * j + 4 * lg;
+      float v[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        v[r] = acc[i][j][r] + (bias != nullptr && n + r < N ? E::to_float(bias[n + r]) : 0.0f);
+      if (vec_store && n + 3 < N) {
+        *reinterpret_cast<u32x2*>(crow + n) = u32x2{pack2<E>(v[0], v[1]), pack2<E>(v[2], v[3])};
+      } else {
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          if (n + r < N) crow[n + r] = E::from_float(v[r]);
+      }
+    }
+  }
+}
+
+template <typename E, int BM, int BN, int WM, int WN, int STAGES>
+hipError_t launch_dma(const uint16_t* A, const uint16_t* B, const uint16_t* bias, uint16_t* C, int M, int N, int K,
+                      int lda, int ldb, int ldc, hipStream_t s) {
+  const int64_t tiles = ceil_div64(M, BM) * ceil_div64(N, BN);
+  const int vec = (ldc % 4 == 0 && aligned_to(C, 8)) ? 1 : 0;
+  hipLaunchKernelGGL((gemm_dma_kernel<E, BM, BN, WM, WN, STAGES>), dim3(static_cast<unsigned>(tiles)),
+                     dim3(WM * WN * kWave), 0, s, A, B, bias, C, M, N, K, lda, ldb, ldc, vec);
+  return hipGetLastError();
 }
 
 template <typename E>
@@ -329,10 +429,34 @@ hipError_t launch(const uint16_t* A, const uint16_t* B, const uint16_t* bias, ui
     }
     return hipGetLastError();
   }
-  if (ceil_div64(M, kBM) > 65535) return hipErrorInvalidValue;
-  const dim3 grid(static_cast<unsigned>(ceil_div64(N, kBN)), static_cast<unsigned>(ceil_div64(M, kBM)));
-  hipLaunchKernelGGL((gemm_tiled_kernel<E>), grid, dim3(kTiledThreads), 0, s, A, B, bias, C, M, N, K, lda, ldb, ldc);
-  return hipGetLastError();
+  // Tile shape by a throughput model fitted to measured bf16 runs at K = 4096
+  // and 14336: time ~ ceil(tiles / 256 CUs) x tile flops / per-CU rate of the
+  // shape (TFLOP/s). Large tiles move fewer bytes per flop through L2 and LDS;
+  // small ones keep all 256 CUs busy when M is a few hundred rows.
+  struct Shape {
+    int bm, bn;
+    double rate;
+    hipError_t (*fn)(const uint16_t*, const uint16_t*, const uint16_t*, uint16_t*, int, int, int, int, int, int,
+                     hipStream_t);
+  };
+  static const Shape shapes[] = {
+      {256, 256, 4.7, launch_dma<E, 256, 256, 4, 2, 2>},
+      {256, 128, 4.2, launch_dma<E, 256, 128, 4, 2, 3>},
+      {128, 128, 3.2, launch_dma<E, 128, 128, 4, 2, 3>},
+      {128, 64, 2.2, launch_dma<E, 128, 64, 2, 2, 4>},
+      {64, 64, 1.4, launch_dma<E, 64, 64, 2, 2, 4>},
+  };
+  const Shape* best = nullptr;
+  double best_t = 0.0;
+  for (const Shape& sh : shapes) {
+    const double rounds = static_cast<double>(ceil_div64(ceil_div64(M, sh.bm) * ceil_div64(N, sh.bn), 256));
+    const double t = rounds * sh.bm * sh.bn / sh.rate;
+    if (best == nullptr || t < best_t) {
+      best = &sh;
+      best_t = t;
+    }
+  }
+  return best->fn(A, B, bias, C, M, N, K, lda, ldb, ldc, s);
 }
 
 }  // namespace gemm
@@ -350,7 +474,9 @@ extern "C" int dk_gemm_tn(int dtype, const void* A, const void* B, const void* b
     return fail("gemm_tn: K and row strides of a/b must be multiples of 8");
   if (!aligned_to(A, 16) || !aligned_to(B, 16)) return fail("gemm_tn: a and b must be 16-byte aligned");
   if (C == nullptr || (K > 0 && (A == nullptr || B == nullptr))) return fail("gemm_tn: pointers must not be NULL");
-  if (M > 64 && ceil_div64(M, gemm::kBM) > 65535) return fail("gemm_tn: M is too large");
+  if (M > 64 && ceil_div64(M, 64) * ceil_div64(N, 64) >= (int64_t{1} << 31)) return fail("gemm_tn: M x N is too large");
+  if (M > 64 && int64_t{256} * std::max(lda, ldb) * 2 >= (int64_t{1} << 31))
+    return fail("gemm_tn: row strides too large for 32-bit buffer offsets");
   if (M <= 64 && (static_cast<int64_t>(M) * lda * 2 >= (int64_t{1} << 31) || int64_t{16} * ldb * 2 >= (int64_t{1} << 31)))
     return fail("gemm_tn: row strides too large for 32-bit buffer offsets");
   hipStream_t s = static_cast<hipStream_t>(stream);

@@ -218,8 +218,13 @@ GEMM_SHAPES = [
     (64, 6144, 4096),
     (65, 512, 256),
     (128, 4096, 4096),
+    (200, 300, 72),  # K tail inside the first slice
+    (256, 4096, 1024),  # 64x64 tiles
     (333, 1024, 1032),
+    (512, 4096, 1032),  # 128x64 tiles
+    (512, 6144, 1032),  # 128x128 tiles
     (512, 11008, 4096),
+    (1000, 1000, 136),
 ]
 
 
@@ -259,6 +264,19 @@ def test_gemm_batched_input_and_strided_rows():
     torch.ops.decode_kernels.gemm_tn(c_wide[:, :80], a2, b, None)
     assert_max_abs(c_wide[:, :80], gemm_f32(a2, b), torch.float16)
     assert torch.count_nonzero(c_wide[:, 80:]) == 0
+
+
+@pytest.mark.parametrize("M", [37, 300])
+def test_gemm_odd_ldc_and_row_strides(M):
+    """C rows of odd stride (no 8-byte stores) and A/B rows padded past K."""
+    g = torch.Generator(device="cuda").manual_seed(M)
+    a_buf = torch.randn(M, 264, generator=g, device="cuda", dtype=torch.bfloat16)
+    b_buf = torch.randn(150, 272, generator=g, device="cuda", dtype=torch.bfloat16) / 16
+    a, b = a_buf[:, :200], b_buf[:, :200]
+    c_buf = torch.full((M, 153), 3.0, device="cuda", dtype=torch.bfloat16)
+    torch.ops.decode_kernels.gemm_tn(c_buf[:, :150], a, b, None)
+    assert_max_abs(c_buf[:, :150], gemm_f32(a, b), torch.bfloat16, f"gemm M={M} ldc=153")
+    assert (c_buf[:, 150:] == 3.0).all()
 
 
 def test_gemm_rejects_unaligned_k():

@@ -1,0 +1,130 @@
+"""GPU test of the ops composed into one decoder layer's decode step.
+
+fused_add_rms_norm -> qkv gemm_tn -> paged_attention_decode (q is a strided
+view of the qkv output, as a serving engine passes it) -> o gemm_tn ->
+fused_add_rms_norm -> gate_up gemm_tn -> silu_and_mul -> down gemm_tn, at the
+head-dim-256 / group-8 attention shape with a reduced MLP width. Each stage is
+checked against the oracle applied to the previous stage's actual output (the
+bar of each op's own parity test), then the whole step is captured in a HIP
+graph and every replay -- with the sequence lengths rewritten on the device
+between replays -- must match an eager run bit for bit.
+"""
+
+import pytest
+import torch
+
+import decodekernels_amd as dk
+from decodekernels_amd.testing import make_paged_kv
+from parity import (
+    assert_max_abs,
+    assert_ulp,
+    attention_f32,
+    fused_add_rms_norm_reference,
+    gemm_f32,
+    silu_and_mul_reference,
+)
+
+pytestmark = pytest.mark.gpu
+
+HQ, HKV, D, BS = 16, 2, 256, 32
+HIDDEN, INTER = HQ * D, 1024
+EPS = 1e-5
+
+
+class Layer:
+    def __init__(self, seq_lens, dtype, seed=0):
+        g = torch.Generator(device="cuda").manual_seed(seed)
+        kw = dict(device="cuda", dtype=dtype)
+        self.dtype = dtype
+        self.n = len(seq_lens)
+        self.w_qkv = torch.randn((HQ + 2 * HKV) * D, HIDDEN, generator=g, **kw) * 0.02
+        self.w_o = torch.randn(HIDDEN, HIDDEN, generator=g, **kw) * 0.02
+        self.w_gu = torch.randn(2 * INTER, HIDDEN, generator=g, **kw) * 0.02
+        self.w_down = torch.randn(HIDDEN, INTER, generator=g, **kw) * 0.02
+        self.ln1 = (1 + 0.1 * torch.randn(HIDDEN, generator=g, device="cuda")).to(dtype)
+        self.ln2 = (1 + 0.1 * torch.randn(HIDDEN, generator=g, device="cuda")).to(dtype)
+        self.kv = make_paged_kv(seq_lens, HKV, D, BS, dtype, "cuda", layout="nhd", seed=seed + 1)
+        self.max_len = max(max(seq_lens), 1)
+        self.x0 = torch.randn(self.n, HIDDEN, generator=g, **kw)
+        self.r0 = torch.randn(self.n, HIDDEN, generator=g, **kw)
+        self.x, self.resid = torch.empty_like(self.x0), torch.empty_like(self.r0)
+        self.qkv = torch.empty(self.n, self.w_qkv.shape[0], **kw)
+        self.attn = torch.empty(self.n, HQ, D, **kw)
+        self.o = torch.empty(self.n, HIDDEN, **kw)
+        self.gu = torch.empty(self.n, 2 * INTER, **kw)
+        self.act = torch.empty(self.n, INTER, **kw)
+        self.down = torch.empty(self.n, HIDDEN, **kw)
+        self.ws = dk.alloc_workspace(self.n, HQ, D, self.max_len, "cuda")
+        self.q = self.qkv[:, : HQ * D].view(self.n, HQ, D)
+        self.saved = {}
+
+    def step(self, keep=False):
+        ops = torch.ops.decode_kernels
+        self.x.copy_(self.x0)
+        self.resid.copy_(self.r0)
+        ops.fused_add_rms_norm(self.x, self.resid, self.ln1, EPS)
+        if keep:
+            self.saved["norm1"] = (self.x.clone(), self.resid.clone())
+        ops.gemm_tn(self.qkv, self.x, self.w_qkv, None)
+        dk.paged_attention_decode(self.q, self.kv.k_cache, self.kv.v_cache, self.kv.block_tables, self.kv.seq_lens,
+                                  max_seq_len=self.max_len, out=self.attn, workspace=self.ws)
+        ops.gemm_tn(self.o, self.attn.view(self.n, HIDDEN), self.w_o, None)
+        if keep:
+            self.saved["o"] = self.o.clone()
+            self.saved["resid1"] = self.resid.clone()
+        ops.fused_add_rms_norm(self.o, self.resid, self.ln2, EPS)
+        ops.gemm_tn(self.gu, self.o, self.w_gu, None)
+        ops.silu_and_mul(self.act, self.gu)
+        ops.gemm_tn(self.down, self.act, self.w_down, None)
+
+    def outputs(self):
+        return [t.clone() for t in (self.qkv, self.attn, self.o, self.resid, self.gu, self.act, self.down)]
+
+
+SEQ_LENS = [0, 1, 600, 1500, 33, 2049, 512, 513]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_layer_step_stages_match_oracle(dtype):
+    L = Layer(SEQ_LENS, dtype)
+    L.step(keep=True)
+    torch.cuda.synchronize()
+    x1, r1 = L.saved["norm1"]
+    want_x, want_r = fused_add_rms_norm_reference(L.x0.cpu(), L.r0.cpu(), L.ln1.cpu(), EPS)
+    assert torch.equal(r1.cpu(), want_r), "residual of the first fused_add_rms_norm is not bit-exact"
+    assert_ulp(x1, want_x, 1, "fused_add_rms_norm")
+    assert_max_abs(L.qkv, gemm_f32(x1, L.w_qkv), dtype, "qkv gemm")
+    ref_attn = attention_f32(L.q, L.kv.k_cache, L.kv.v_cache, L.kv.block_tables, L.kv.seq_lens)
+    assert_max_abs(L.attn, ref_attn, dtype, "attention on the qkv view")
+    assert (L.attn[0] == 0).all(), "zero-length sequence must give zeros"
+    assert_max_abs(L.saved["o"], gemm_f32(L.attn.view(L.n, HIDDEN), L.w_o), dtype, "o gemm")
+    want_o, want_r2 = fused_add_rms_norm_reference(L.saved["o"].cpu(), L.saved["resid1"].cpu(), L.ln2.cpu(), EPS)
+    assert torch.equal(L.resid.cpu(), want_r2)
+    assert_ulp(L.o, want_o, 1, "second fused_add_rms_norm")
+    assert_max_abs(L.gu, gemm_f32(L.o, L.w_gu), dtype, "gate_up gemm")
+    assert_ulp(L.act, silu_and_mul_reference(L.gu.cpu()), 1, "silu_and_mul")
+    assert_max_abs(L.down, gemm_f32(L.act, L.w_down), dtype, "down gemm")
+
+
+def test_layer_step_graph_replays_match_eager():
+    dtype = torch.bfloat16
+    L = Layer(SEQ_LENS, dtype, seed=3)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        L.step()
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        L.step()
+    lens_sets = [SEQ_LENS, [5, 0, 2049, 17, 1024, 1, 700, 2000], SEQ_LENS]
+    for i, lens in enumerate(lens_sets):
+        L.kv.seq_lens.copy_(torch.tensor(lens, dtype=torch.int32))
+        graph.replay()
+        torch.cuda.synchronize()
+        got = L.outputs()
+        L.step()
+        torch.cuda.synchronize()
+        want = L.outputs()
+        for name, a, b in zip(("qkv", "attn", "o", "resid", "gate_up", "act", "down"), got, want):
+            assert torch.equal(a, b), f"replay {i}: {name} differs from the eager step"
