@@ -19,17 +19,22 @@
 //   16-byte load per 32-column step, and the query fragment of head (l % 16)
 //   in the model dtype (exact); the fp32 logits come out as
 //   S[token 4*(l/16)+r][head l%16], r = 0..3.
-// * P·V uses v_mfma_f32_16x16x4_f32, whose A operand (lane l: row l%16,
-//   k = l/16) is exactly register r of the Q·Kᵀ result when the 4-token step
-//   r takes tokens {4q + r}. Its B operand is a V row per lane group read
-//   with one 16-byte load, one MFMA per loaded column, so V never needs a
-//   transpose and P stays in fp32. Accumulators: lane l holds
-//   O[head 4*(l/16)+i][d(r, l%16)].
+// * P·V on v_mfma_f32_16x16x16: V is loaded exactly like K and transposed on
+//   the matrix core -- a 16x16x32 MFMA of a V chunk against an identity
+//   fragment returns it in the B-operand layout (lane l: V[token 4*(l/16)+r]
+//   [column l%16]) -- and P, which leaves Q·Kᵀ already in the A-operand
+//   layout, is split into hi + lo parts in the model dtype: two MFMAs per
+//   16-column block keep the products accurate to ~2^-17 relative.
+//   Accumulators: lane l holds O[head 4*(l/16)+i][column 16n + l%16].
 // * Logits are kept in log2 units (scale * log2 e folded into one multiply)
 //   and exponentiated with v_exp_f32; max_logits are stored in natural-log
 //   units so the workspace means what the reference's does.
 // * K/V tiles are double-buffered in registers: the loads for tile n+1 are
 //   in flight while tile n is multiplied.
+#include <atomic>
+#include <cstdlib>
+#include <cstring>
+
 #include "../../include/decodekernels_amd.h"
 #include "dk_device.h"
 #include "dk_host.h"
@@ -47,6 +52,9 @@ constexpr int kPart = DK_PARTITION_SIZE;  // workspace granularity (tokens)
 #endif
 #ifndef DK_ATTN_DEPTH
 #define DK_ATTN_DEPTH 2  // tiles in flight per wave (head_dim <= 128)
+#endif
+#ifndef DK_ATTN_DEPTH_D256
+#define DK_ATTN_DEPTH_D256 2  // tiles in flight per wave (head_dim 256)
 #endif
 #ifndef DK_ATTN_LOAD_AUX
 #define DK_ATTN_LOAD_AUX 0  // cache-policy bits of the K/V buffer loads
@@ -82,6 +90,8 @@ struct KParams {
   int64_t k_sb, k_st, k_sh, v_sb, v_st, v_sh;
   int64_t bt_stride;
   int num_q_heads, group, block_size, max_partitions;
+  int num_seqs, num_kv_heads, num_slots;  // work-unit grid: num_slots planes of num_seqs x num_kv_heads
+  unsigned* unit_counter;                 // persistent split-K path: next work unit (zeroed before launch)
   int part_tokens;  // tokens per work unit (single pass: 512; split: a multiple of 512)
   float scale_log2;
 };
@@ -139,19 +149,28 @@ constexpr int attn_occupancy() {
   return D >= 256 ? 1 : (D == 128 ? DK_ATTN_OCC_D128 : DK_ATTN_OCC_D64);
 }
 
-// NW waves per workgroup; each wave keeps DEPTH tiles of loads in flight.
-template <typename E, int D, bool SPLIT, bool BS16, int ALIGN, int NW>
-__global__ __launch_bounds__(NW * kWave) __attribute__((amdgpu_waves_per_eu(attn_occupancy<D>(), attn_occupancy<D>())))
-void paged_attention_kernel(const KParams p) {
+// LDS of one work unit: per-wave softmax state and partial outputs, merged at the end.
+template <int D, int NW>
+struct UnitSmem {
+  float m[NW][16];              // reference max per head (log2 units)
+  float t[NW][16];              // true max per head
+  float l[NW][16];              // exp-sum against the reference max
+  float o[NW][kMaxGroup][D];    // partial outputs
+};
+
+// One work unit: the tokens [part * part_tokens, ...) of sequence `seq`
+// (seq_len > that start) for KV head `kv_head` and its query-head group, on
+// NW waves; each wave keeps DEPTH tiles of loads in flight. `before_merge`
+// runs once every wave has consumed its last tile, before the LDS merge.
+template <typename E, int D, bool SPLIT, bool BS16, int ALIGN, int NW, typename Hook>
+__device__ __forceinline__ void attention_unit(const KParams& p, int kv_head, int seq, int part, int seq_len,
+                                               UnitSmem<D, NW>& sm, Hook before_merge) {
   constexpr int CH = D / 32;  // 32-column chunks per row
   constexpr int NB = D / 16;  // 16-column output blocks
-  constexpr int DEPTH = D >= 256 ? 2 : DK_ATTN_DEPTH;
+  constexpr int DEPTH = D >= 256 ? DK_ATTN_DEPTH_D256 : DK_ATTN_DEPTH;
   constexpr int NT = NW * kWave;
   using Tile = TileRegs<CH>;
 
-  const int kv_head = blockIdx.x;
-  const int seq = blockIdx.y;
-  const int part = blockIdx.z;
   const int tid = threadIdx.x;
   const int lane = tid % kWave;
   const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
@@ -159,25 +178,9 @@ void paged_attention_kernel(const KParams p) {
   const int lg = lane / 16;   // lane group 0..3
   const int group = p.group;
 
-  const int seq_len = p.seq_lens[seq];
   const int start = SPLIT ? part * p.part_tokens : 0;
-  if (start >= seq_len) {
-    if (!SPLIT) {
-      for (int idx = tid; idx < group * D; idx += NT) {
-        const int h = idx / D;
-        const int d = idx - h * D;
-        p.out[seq * p.o_ss + (kv_head * group + h) * p.o_sh + d] = 0;
-      }
-    }
-    return;
-  }
   const int end = min(start + p.part_tokens, seq_len);
   const int n_tiles = (end - start + kTile - 1) / kTile;
-
-  __shared__ float sm_m[NW][16];   // reference max per head (log2 units)
-  __shared__ float sm_t[NW][16];   // true max per head
-  __shared__ float sm_l[NW][16];   // exp-sum against the reference max
-  __shared__ float sm_o[NW][kMaxGroup][D];
 
   // Block-table entries of this work unit (lane e holds entry lb0 + e) when
   // every 16-token tile lies inside one cache block.
@@ -347,14 +350,16 @@ void paged_attention_kernel(const KParams p) {
     }
   }
 
+  before_merge();
+
   // Exp-sum of head l16 over all four lane groups.
   float l_tot = l_run + __shfl_xor(l_run, 16, kWave);
   l_tot += __shfl_xor(l_tot, 32, kWave);
 
   if (lane < 16) {
-    sm_m[wave][lane] = m_ref;
-    sm_t[wave][lane] = m_true;
-    sm_l[wave][lane] = l_tot;
+    sm.m[wave][lane] = m_ref;
+    sm.t[wave][lane] = m_true;
+    sm.l[wave][lane] = l_tot;
   }
   // acc[n] lane l: O[head 4*lg + i][column 16n + l16].
 #pragma unroll
@@ -362,7 +367,7 @@ void paged_attention_kernel(const KParams p) {
     const int h = 4 * lg + i;
     if (h < group) {
 #pragma unroll
-      for (int n = 0; n < NB; ++n) sm_o[wave][h][16 * n + l16] = acc[n][i];
+      for (int n = 0; n < NB; ++n) sm.o[wave][h][16 * n + l16] = acc[n][i];
     }
   }
   __syncthreads();
@@ -370,16 +375,16 @@ void paged_attention_kernel(const KParams p) {
   for (int idx = tid; idx < group * D; idx += NT) {
     const int h = idx / D;
     const int d = idx - h * D;
-    float M = sm_m[0][h];
+    float M = sm.m[0][h];
 #pragma unroll
-    for (int w = 1; w < NW; ++w) M = fmaxf(M, sm_m[w][h]);
+    for (int w = 1; w < NW; ++w) M = fmaxf(M, sm.m[w][h]);
     float L = 0.0f;
     float O = 0.0f;
 #pragma unroll
     for (int w = 0; w < NW; ++w) {
-      const float f = __builtin_amdgcn_exp2f(sm_m[w][h] - M);
-      L += f * sm_l[w][h];
-      O += f * sm_o[w][h][d];
+      const float f = __builtin_amdgcn_exp2f(sm.m[w][h] - M);
+      L += f * sm.l[w][h];
+      O += f * sm.o[w][h][d];
     }
     const float res = O / L;
     const int q_head = kv_head * group + h;
@@ -388,9 +393,9 @@ void paged_attention_kernel(const KParams p) {
       p.tmp_out[row * D + d] = res;
       if (d == 0) {
         // Report (max logit, exp-sum) against the partition's true max.
-        float T = sm_t[0][h];
+        float T = sm.t[0][h];
 #pragma unroll
-        for (int w = 1; w < NW; ++w) T = fmaxf(T, sm_t[w][h]);
+        for (int w = 1; w < NW; ++w) T = fmaxf(T, sm.t[w][h]);
         p.max_logits[row] = T * kLn2;
         p.exp_sums[row] = L * __builtin_amdgcn_exp2f(M - T);
       }
@@ -398,6 +403,148 @@ void paged_attention_kernel(const KParams p) {
       p.out[seq * p.o_ss + q_head * p.o_sh + d] = E::from_float(res);
     }
   }
+}
+
+// Grid kernel: one workgroup per work unit. The units of one slot form a
+// plane of num_seqs x num_kv_heads; planes run from the last slot down (full
+// units first, a sequence's short tail unit last), and plane `part` is rotated
+// by `part` positions. Workgroup i runs on XCD i mod 8, so without the
+// rotation every unit of a (sequence, KV head) would land on one XCD and a few
+// long sequences would keep one XCD busy long after the others are idle.
+template <typename E, int D, bool SPLIT, bool BS16, int ALIGN, int NW>
+__global__ __launch_bounds__(NW * kWave) __attribute__((amdgpu_waves_per_eu(attn_occupancy<D>(), attn_occupancy<D>())))
+void paged_attention_kernel(const KParams p) {
+  __shared__ UnitSmem<D, NW> sm;
+  const int per_plane = p.num_seqs * p.num_kv_heads;
+  const int plane = static_cast<int>(blockIdx.x) / per_plane;
+  const int part = SPLIT ? p.num_slots - 1 - plane : 0;
+  const int rot = static_cast<int>(blockIdx.x) - plane * per_plane;
+  const int unit = (rot + per_plane - part % per_plane) % per_plane;
+  const int seq = unit / p.num_kv_heads;
+  const int kv_head = unit - seq * p.num_kv_heads;
+  const int seq_len = p.seq_lens[seq];
+  const int start = SPLIT ? part * p.part_tokens : 0;
+  if (start >= seq_len) {
+    if (!SPLIT) {
+      for (int idx = threadIdx.x; idx < p.group * D; idx += NW * kWave) {
+        const int h = idx / D;
+        const int d = idx - h * D;
+        p.out[seq * p.o_ss + (kv_head * p.group + h) * p.o_sh + d] = 0;
+      }
+    }
+    return;
+  }
+  attention_unit<E, D, SPLIT, BS16, ALIGN, NW>(p, kv_head, seq, part, seq_len, sm, [] {});
+}
+
+// Persistent split-K kernel: a resident-sized grid pulls work units from a
+// counter, so no workgroup is launched for a slot past a sequence's end (at
+// mixed lengths most grid slots are such, and launching them costs the
+// dispatcher more than the work) and the last units are spread over all
+// workgroups. Every workgroup lists the live units itself from seq_lens:
+// the full units of all sequences first, then each sequence's shorter tail
+// unit, KV heads innermost; prefix sums in LDS map a unit index back to its
+// (sequence, slot) by binary search. The first rounds of full units (all the
+// same size) are dealt out in grid order; the rest go through an atomic
+// counter (zeroed before launch). The first counter claim is made when a
+// workgroup starts its last dealt unit, so the claims of all workgroups,
+// which would otherwise arrive together, are served while they work; later
+// claims are made as each unit's partial results are merged.
+constexpr int kMaxPersistSeqs = 2048;
+
+template <typename E, int D, bool BS16, int ALIGN, int NW>
+__global__ __launch_bounds__(NW * kWave) __attribute__((amdgpu_waves_per_eu(attn_occupancy<D>(), attn_occupancy<D>())))
+void paged_attention_persistent_kernel(const KParams p) {
+  constexpr int NT = NW * kWave;
+  __shared__ UnitSmem<D, NW> sm;
+  __shared__ int pf[kMaxPersistSeqs + 1];  // full units of sequences 0 .. s-1
+  __shared__ int pr[kMaxPersistSeqs + 1];  // tail units of sequences 0 .. s-1
+  __shared__ long long scan[NT];
+  __shared__ int next_unit;
+  const int tid = threadIdx.x;
+  const int S = p.num_seqs;
+  const int T = p.part_tokens;
+  const int max_tokens = p.num_slots * T;  // tokens past the workspace are ignored, as in the grid path
+  auto clamped_len = [&](int s) { return min(max(p.seq_lens[s], 0), max_tokens); };
+
+  // Per-thread chunk of sequences -> block-wide exclusive scan of (full, tail) counts.
+  const int per = (S + NT - 1) / NT;
+  const int s0 = min(tid * per, S);
+  const int s1 = min(s0 + per, S);
+  long long cnt = 0;
+  for (int s = s0; s < s1; ++s) {
+    const int len = clamped_len(s);
+    cnt += (static_cast<long long>(len / T) << 32) + (len % T != 0 ? 1 : 0);
+  }
+  scan[tid] = cnt;
+  __syncthreads();
+  for (int off = 1; off < NT; off <<= 1) {
+    const long long add = tid >= off ? scan[tid - off] : 0;
+    __syncthreads();
+    scan[tid] += add;
+    __syncthreads();
+  }
+  long long run = scan[tid] - cnt;
+  for (int s = s0; s < s1; ++s) {
+    pf[s] = static_cast<int>(run >> 32);
+    pr[s] = static_cast<int>(run & 0xffffffff);
+    const int len = clamped_len(s);
+    run += (static_cast<long long>(len / T) << 32) + (len % T != 0 ? 1 : 0);
+  }
+  if (tid == NT - 1) {
+    pf[S] = static_cast<int>(scan[NT - 1] >> 32);
+    pr[S] = static_cast<int>(scan[NT - 1] & 0xffffffff);
+  }
+  __syncthreads();
+
+  const int hkv = p.num_kv_heads;
+  const int total_full = pf[S] * hkv;
+  const int total = total_full + pr[S] * hkv;
+  // Last s with a[s] <= j (a[0] = 0 <= j < a[S]).
+  auto find = [&](const int* a, int j) {
+    int lo = 0, hi = S;
+    while (hi - lo > 1) {
+      const int mid = (lo + hi) >> 1;
+      if (a[mid] <= j) lo = mid;
+      else hi = mid;
+    }
+    return lo;
+  };
+
+  const int G = gridDim.x;
+  const int dealt_rounds = max(1, total_full / G);
+  const int dealt = min(total, dealt_rounds * G);
+  int u = blockIdx.x;
+  int round = 0;
+  while (u < total) {
+    const bool dealt_unit = round < dealt_rounds;
+    const bool last_dealt = round == dealt_rounds - 1;
+    if (last_dealt && tid == 0) {
+      next_unit = dealt < total ? dealt + static_cast<int>(atomicAdd(p.unit_counter, 1u)) : total;
+    }
+    int kv_head, seq, part;
+    if (u < total_full) {
+      kv_head = u % hkv;
+      const int j = u / hkv;
+      seq = find(pf, j);
+      part = j - pf[seq];
+    } else {
+      const int v = u - total_full;
+      kv_head = v % hkv;
+      seq = find(pr, v / hkv);
+      part = clamped_len(seq) / T;
+    }
+    attention_unit<E, D, true, BS16, ALIGN, NW>(p, kv_head, seq, part, clamped_len(seq), sm, [&] {
+      if (!dealt_unit && tid == 0) next_unit = dealt + static_cast<int>(atomicAdd(p.unit_counter, 1u));
+    });
+    u = dealt_unit && !last_dealt ? u + G : next_unit;
+    ++round;
+    __syncthreads();
+  }
+}
+
+__global__ void zero_counter_kernel(unsigned* counter) {
+  if (threadIdx.x == 0) *counter = 0u;
 }
 
 // Log-sum-exp merge of the work units of one (query head, sequence):
@@ -476,43 +623,106 @@ __global__ __launch_bounds__(kReduceWaves * kWave) void paged_attention_reduce_k
   for (int c = 0; c < C; ++c) out[c] = E::from_float(acc[c] * inv);
 }
 
-template <typename E, int D, bool SPLIT, bool BS16>
-hipError_t launch_main_aligned(const KParams& kp, dim3 grid, int align, hipStream_t stream) {
-  constexpr int NW = D >= 256 ? DK_ATTN_WAVES_D256 : kWaves;
-  const dim3 block(NW * kWave);
+constexpr int kMaxDevices = 64;
+
+template <int D>
+constexpr int waves_per_group() {
+  return D >= 256 ? DK_ATTN_WAVES_D256 : kWaves;
+}
+
+// Launches the grid kernel (PERSIST = false, one workgroup per unit slot) or
+// the persistent kernel for KV pointers aligned to ALIGN bytes. With
+// `resident`, only reports how many persistent workgroups fit on the current
+// device at once (0 if unknown), cached per device.
+template <typename E, int D, int ALIGN, bool SPLIT, bool BS16, bool PERSIST>
+hipError_t launch_kernel(const KParams& kp, unsigned grid, hipStream_t stream, int* resident = nullptr) {
+  constexpr int NW = waves_per_group<D>();
+  if constexpr (PERSIST) {
+    const auto kernel = paged_attention_persistent_kernel<E, D, BS16, ALIGN, NW>;
+    if (resident != nullptr) {
+      static std::atomic<int> cache[kMaxDevices];
+      *resident = 0;
+      int dev = 0;
+      if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return hipSuccess;
+      int v = cache[dev].load(std::memory_order_relaxed);
+      if (v <= 0) {
+        int per_cu = 0;
+        int cus = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void*>(kernel), NW * kWave, 0) !=
+                hipSuccess ||
+            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+          return hipSuccess;
+        v = per_cu * cus;
+        cache[dev].store(v, std::memory_order_relaxed);
+      }
+      *resident = v;
+      return hipSuccess;
+    }
+    hipLaunchKernelGGL(kernel, dim3(grid), dim3(NW * kWave), 0, stream, kp);
+  } else {
+    hipLaunchKernelGGL((paged_attention_kernel<E, D, SPLIT, BS16, ALIGN, NW>), dim3(grid), dim3(NW * kWave), 0, stream,
+                       kp);
+  }
+  return hipGetLastError();
+}
+
+template <typename E, int D, bool SPLIT, bool BS16, bool PERSIST>
+hipError_t launch_aligned(const KParams& kp, unsigned grid, int align, hipStream_t stream, int* resident = nullptr) {
   switch (align) {
     case 16:
-      hipLaunchKernelGGL((paged_attention_kernel<E, D, SPLIT, BS16, 16, NW>), grid, block, 0, stream, kp);
-      break;
+      return launch_kernel<E, D, 16, SPLIT, BS16, PERSIST>(kp, grid, stream, resident);
     case 8:
-      if constexpr (D <= 128) {
-        hipLaunchKernelGGL((paged_attention_kernel<E, D, SPLIT, BS16, 8, NW>), grid, block, 0, stream, kp);
-        break;
-      }
+      if constexpr (D <= 128) return launch_kernel<E, D, 8, SPLIT, BS16, PERSIST>(kp, grid, stream, resident);
       return hipErrorInvalidValue;
     case 4:
-      if constexpr (D == 64) {
-        hipLaunchKernelGGL((paged_attention_kernel<E, D, SPLIT, BS16, 4, NW>), grid, block, 0, stream, kp);
-        break;
-      }
+      if constexpr (D == 64) return launch_kernel<E, D, 4, SPLIT, BS16, PERSIST>(kp, grid, stream, resident);
       return hipErrorInvalidValue;
     default:
       return hipErrorInvalidValue;
   }
-  return hipGetLastError();
+}
+
+// DK_ATTN_SCHEDULE=grid|persistent forces the split-K schedule (tests and
+// tuning compare the two on one input); unset or anything else: automatic.
+enum class Schedule { kAuto, kGrid, kPersistent };
+inline Schedule forced_schedule() {
+  const char* v = std::getenv("DK_ATTN_SCHEDULE");
+  if (v == nullptr) return Schedule::kAuto;
+  if (std::strcmp(v, "grid") == 0) return Schedule::kGrid;
+  if (std::strcmp(v, "persistent") == 0) return Schedule::kPersistent;
+  return Schedule::kAuto;
+}
+
+template <typename E, int D, bool BS16>
+hipError_t launch_split(KParams kp, int num_kv_heads, int num_seqs, int num_slots, int align, hipStream_t stream) {
+  const int64_t units_bound = static_cast<int64_t>(num_kv_heads) * num_seqs * num_slots;
+  // The persistent kernel pays a counter reset and a unit-list setup; it wins
+  // when the grid would be mostly slots past their sequence's end, i.e. many
+  // slots per sequence and a grid several times the resident workgroups.
+  const Schedule forced = forced_schedule();
+  int resident = 0;
+  if (num_seqs <= kMaxPersistSeqs && kp.unit_counter != nullptr && forced != Schedule::kGrid &&
+      (num_slots >= 8 || forced == Schedule::kPersistent)) {
+    const hipError_t e = launch_aligned<E, D, true, BS16, true>(kp, 0, align, stream, &resident);
+    if (e != hipSuccess) return e;
+  }
+  if (resident <= 0 || (forced != Schedule::kPersistent && units_bound <= 4 * static_cast<int64_t>(resident)))
+    return launch_aligned<E, D, true, BS16, false>(kp, static_cast<unsigned>(units_bound), align, stream);
+  hipLaunchKernelGGL(zero_counter_kernel, dim3(1), dim3(kWave), 0, stream, kp.unit_counter);
+  const unsigned grid = static_cast<unsigned>(units_bound < resident ? units_bound : resident);
+  return launch_aligned<E, D, true, BS16, true>(kp, grid, align, stream);
 }
 
 template <typename E, int D>
 hipError_t launch(const KParams& kp, int num_kv_heads, int num_seqs, bool split, int num_slots, bool bs16, int align,
                   hipStream_t stream) {
   if (!split) {
-    const dim3 grid(num_kv_heads, num_seqs, 1);
-    return bs16 ? launch_main_aligned<E, D, false, true>(kp, grid, align, stream)
-                : launch_main_aligned<E, D, false, false>(kp, grid, align, stream);
+    const unsigned grid = static_cast<unsigned>(num_kv_heads * num_seqs);
+    return bs16 ? launch_aligned<E, D, false, true, false>(kp, grid, align, stream)
+                : launch_aligned<E, D, false, false, false>(kp, grid, align, stream);
   }
-  const dim3 grid(num_kv_heads, num_seqs, num_slots);
-  hipError_t e = bs16 ? launch_main_aligned<E, D, true, true>(kp, grid, align, stream)
-                      : launch_main_aligned<E, D, true, false>(kp, grid, align, stream);
+  hipError_t e = bs16 ? launch_split<E, D, true>(kp, num_kv_heads, num_seqs, num_slots, align, stream)
+                      : launch_split<E, D, false>(kp, num_kv_heads, num_seqs, num_slots, align, stream);
   if (e != hipSuccess) return e;
   const dim3 rblock(kReduceWaves * kWave);
   if (num_slots <= 16) {
@@ -608,6 +818,16 @@ extern "C" int dk_paged_attention_decode(const dk_paged_attn_params* a, int dtyp
   kp.part_tokens = split ? kPart * DK_ATTN_UNIT_SLOTS : kPart;
   if (split) num_slots = static_cast<int>(ceil_div64(static_cast<int64_t>(a->max_partitions) * kPart, kp.part_tokens));
   kp.scale_log2 = a->scale * kLog2e;
+  if (static_cast<int64_t>(a->num_seqs) * a->num_kv_heads * num_slots >= (int64_t{1} << 31))
+    return fail("paged_attention_decode: num_seqs x num_kv_heads x partitions is too large");
+  kp.num_seqs = a->num_seqs;
+  kp.num_kv_heads = a->num_kv_heads;
+  kp.num_slots = num_slots;
+  // The persistent split-K kernel's unit counter lives in an exp_sums entry
+  // that is never written or read otherwise: work units use slots
+  // 0 .. num_slots - 1 of the max_partitions >= 2 slots, so slot
+  // max_partitions - 1 of (sequence 0, head 0) is free.
+  kp.unit_counter = split ? reinterpret_cast<unsigned*>(a->exp_sums + (a->max_partitions - 1)) : nullptr;
 
   const bool bs16 = a->block_size % kTile == 0;
   hipStream_t s = static_cast<hipStream_t>(stream);

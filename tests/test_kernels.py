@@ -9,6 +9,8 @@ aligned KV strides, the Llama-3-8B decode shape and long split-K contexts.
 These run only on a GPU; the ops raise if the HIP libraries are missing.
 """
 
+import math
+
 import pytest
 import torch
 
@@ -156,9 +158,62 @@ def test_paged_attention_long_context_outlier_rows():
     _check_attention(_q(1, 32, 128, torch.float16), kv, torch.float16)
 
 
-def test_paged_attention_graph_replay():
+def _log_uniform_lens(n, max_len, seed, zeros=4):
+    """Lengths log-uniform in [1, max_len], a few empty, the first at max_len."""
+    g = torch.Generator().manual_seed(seed)
+    lens = torch.exp(torch.rand(n, generator=g) * math.log(max_len)).long().clamp(1, max_len)
+    lens[torch.randperm(n, generator=g)[:zeros]] = 0
+    lens[0] = max_len
+    return lens.tolist()
+
+
+# (head_dim, num_kv_heads, group, block_size, layout, num_seqs, max_len, dtype)
+SCHEDULE_CASES = [
+    (256, 2, 8, 32, "nhd", 48, 16384, torch.bfloat16),  # the head-dim-256 / group-8 stress shape, fewer seqs
+    (128, 8, 4, 16, "vllm", 24, 9000, torch.float16),
+    (64, 4, 2, 16, "hnd", 40, 12000, torch.bfloat16),
+    (128, 2, 4, 24, "nhd", 16, 5000, torch.float16),  # blocks that split 16-token tiles
+]
+
+
+@pytest.mark.parametrize("case", SCHEDULE_CASES, ids=lambda c: f"d{c[0]}_hkv{c[1]}_g{c[2]}_bs{c[3]}_{c[4]}")
+def test_paged_attention_split_k_schedules(case, monkeypatch):
+    """Split-K under both schedules -- one workgroup per unit slot, and resident
+    workgroups pulling the live units from a counter -- against the oracle,
+    and bit-identical to each other."""
+    d, hkv, group, bs, layout, n, max_len, dtype = case
+    lens = _log_uniform_lens(n, max_len, seed=d + bs)
+    kv = make_paged_kv(lens, hkv, d, bs, dtype, "cuda", layout=layout, seed=d + 1)
+    q = _q(n, hkv * group, d, dtype)
+    outs = {}
+    for schedule in ("grid", "persistent"):
+        monkeypatch.setenv("DK_ATTN_SCHEDULE", schedule)
+        outs[schedule] = dk.paged_attention_decode(
+            q, kv.k_cache, kv.v_cache, kv.block_tables, kv.seq_lens, max_seq_len=max_len
+        )
+    torch.cuda.synchronize()
+    ref = attention_f32(q, kv.k_cache, kv.v_cache, kv.block_tables, kv.seq_lens)
+    for schedule, out in outs.items():
+        assert_max_abs(out, ref, dtype, f"{schedule} schedule")
+    assert torch.equal(outs["grid"], outs["persistent"])
+
+
+def test_paged_attention_persistent_schedule_short_sequences(monkeypatch):
+    """A generous max_seq_len with only short sequences: every live unit is a
+    tail unit and most grid slots would be empty."""
+    monkeypatch.setenv("DK_ATTN_SCHEDULE", "persistent")
+    lens = [0, 1, 17, 300, 1023, 1024, 1025, 5]
+    kv = make_paged_kv(lens, 4, 128, 16, torch.bfloat16, "cuda", seed=5)
+    q = _q(len(lens), 16, 128, torch.bfloat16)
+    _check_attention(q, kv, torch.bfloat16, max_seq_len=20000)
+
+
+@pytest.mark.parametrize("schedule", ["auto", "persistent"])
+def test_paged_attention_graph_replay(schedule, monkeypatch):
     """Preallocated buffers make the op capturable; replays track new cache
     contents and lengths (within the captured max_seq_len)."""
+    if schedule != "auto":
+        monkeypatch.setenv("DK_ATTN_SCHEDULE", schedule)
     dtype = torch.float16
     max_seq_len = 2048
     kv = make_paged_kv([max_seq_len] * 3, 2, 128, 16, dtype, "cuda")
