@@ -42,7 +42,8 @@
 namespace dk {
 namespace attn {
 
-constexpr int kPart = DK_PARTITION_SIZE;  // workspace granularity (tokens)
+constexpr int kPart = DK_PARTITION_SIZE;  // workspace slot (tokens), as the reference's partition
+constexpr int kUnit = 2 * kPart;          // split-K work unit: two slots (its block-table entries fit one per lane)
 // Tuning constants of the main kernel (compile-time; defaults are the tuned values).
 #ifndef DK_ATTN_WAVES
 #define DK_ATTN_WAVES 4  // waves per workgroup, head_dim <= 128
@@ -65,11 +66,6 @@ constexpr int kPart = DK_PARTITION_SIZE;  // workspace granularity (tokens)
 #ifndef DK_ATTN_OCC_D64
 #define DK_ATTN_OCC_D64 4  // waves per SIMD targeted at head_dim 64
 #endif
-#ifndef DK_ATTN_UNIT_SLOTS
-#define DK_ATTN_UNIT_SLOTS 2  // 512-token workspace slots per split-K work unit (1 or 2)
-#endif
-static_assert(DK_ATTN_UNIT_SLOTS == 1 || DK_ATTN_UNIT_SLOTS == 2,
-              "a work unit's block-table entries must fit one register per lane");
 constexpr int kWaves = DK_ATTN_WAVES;
 constexpr int kTile = 16;
 constexpr int kMaxGroup = DK_MAX_GQA_GROUP;
@@ -90,9 +86,9 @@ struct KParams {
   int64_t k_sb, k_st, k_sh, v_sb, v_st, v_sh;
   int64_t bt_stride;
   int num_q_heads, group, block_size, max_partitions;
-  int num_seqs, num_kv_heads, num_slots;  // work-unit grid: num_slots planes of num_seqs x num_kv_heads
+  int num_seqs, num_kv_heads;
+  int num_units;  // split-K: unit positions per sequence, ceil(max_partitions / 2)
   unsigned* unit_counter;                 // persistent split-K path: next work unit (zeroed before launch)
-  int part_tokens;  // tokens per work unit (single pass: 512; split: a multiple of 512)
   float scale_log2;
 };
 
@@ -158,13 +154,17 @@ struct UnitSmem {
   float o[NW][kMaxGroup][D];    // partial outputs
 };
 
-// One work unit: the tokens [part * part_tokens, ...) of sequence `seq`
-// (seq_len > that start) for KV head `kv_head` and its query-head group, on
-// NW waves; each wave keeps DEPTH tiles of loads in flight. `before_merge`
-// runs once every wave has consumed its last tile, before the LDS merge.
+// One work unit: tokens [start, min(start + unit_tokens, seq_len)) of sequence
+// `seq` (seq_len > start, at most 1024 tokens) for KV head `kv_head` and its
+// query-head group, on NW waves; each wave keeps DEPTH tiles of loads in
+// flight. Split-K writes the unit's result to workspace slot `slot`, and for a
+// 1024-token unit marks slot + 1 empty (max logit -inf, exp-sum 0) so that the
+// reduce can walk 512-token slots exactly as the reference's partitions.
+// `before_merge` runs once every wave has consumed its last tile, before the
+// LDS merge.
 template <typename E, int D, bool SPLIT, bool BS16, int ALIGN, int NW, typename Hook>
-__device__ __forceinline__ void attention_unit(const KParams& p, int kv_head, int seq, int part, int seq_len,
-                                               UnitSmem<D, NW>& sm, Hook before_merge) {
+__device__ __forceinline__ void attention_unit(const KParams& p, int kv_head, int seq, int start, int unit_tokens,
+                                               int seq_len, int slot, UnitSmem<D, NW>& sm, Hook before_merge) {
   constexpr int CH = D / 32;  // 32-column chunks per row
   constexpr int NB = D / 16;  // 16-column output blocks
   constexpr int DEPTH = D >= 256 ? DK_ATTN_DEPTH_D256 : DK_ATTN_DEPTH;
@@ -178,8 +178,7 @@ __device__ __forceinline__ void attention_unit(const KParams& p, int kv_head, in
   const int lg = lane / 16;   // lane group 0..3
   const int group = p.group;
 
-  const int start = SPLIT ? part * p.part_tokens : 0;
-  const int end = min(start + p.part_tokens, seq_len);
+  const int end = min(start + unit_tokens, seq_len);
   const int n_tiles = (end - start + kTile - 1) / kTile;
 
   // Block-table entries of this work unit (lane e holds entry lb0 + e) when
@@ -389,15 +388,19 @@ __device__ __forceinline__ void attention_unit(const KParams& p, int kv_head, in
     const float res = O / L;
     const int q_head = kv_head * group + h;
     if constexpr (SPLIT) {
-      const int64_t row = (static_cast<int64_t>(seq) * p.num_q_heads + q_head) * p.max_partitions + part;
+      const int64_t row = (static_cast<int64_t>(seq) * p.num_q_heads + q_head) * p.max_partitions + slot;
       p.tmp_out[row * D + d] = res;
       if (d == 0) {
-        // Report (max logit, exp-sum) against the partition's true max.
+        // Report (max logit, exp-sum) against the unit's true max.
         float T = sm.t[0][h];
 #pragma unroll
         for (int w = 1; w < NW; ++w) T = fmaxf(T, sm.t[w][h]);
         p.max_logits[row] = T * kLn2;
         p.exp_sums[row] = L * __builtin_amdgcn_exp2f(M - T);
+        if (unit_tokens > kPart && slot + 1 < p.max_partitions) {
+          p.max_logits[row + 1] = -__builtin_huge_valf();
+          p.exp_sums[row + 1] = 0.0f;
+        }
       }
     } else {
       p.out[seq * p.o_ss + q_head * p.o_sh + d] = E::from_float(res);
@@ -405,25 +408,37 @@ __device__ __forceinline__ void attention_unit(const KParams& p, int kv_head, in
   }
 }
 
-// Grid kernel: one workgroup per work unit. The units of one slot form a
-// plane of num_seqs x num_kv_heads; planes run from the last slot down (full
-// units first, a sequence's short tail unit last), and plane `part` is rotated
-// by `part` positions. Workgroup i runs on XCD i mod 8, so without the
-// rotation every unit of a (sequence, KV head) would land on one XCD and a few
-// long sequences would keep one XCD busy long after the others are idle.
+// Grid kernel: one workgroup per work unit. The units at one token position
+// form a plane of num_seqs x num_kv_heads. Split-K planes run from the last
+// 1024-token position down; the first 1024 tokens of every sequence come last
+// as two planes of 512-token units, so the units still running when the grid
+// drains are short. Plane k is rotated by k positions: workgroup i runs on XCD
+// i mod 8, and without the rotation every unit of a (sequence, KV head) would
+// land on one XCD, where a few long sequences would keep it busy long after
+// the others are idle.
 template <typename E, int D, bool SPLIT, bool BS16, int ALIGN, int NW>
 __global__ __launch_bounds__(NW * kWave) __attribute__((amdgpu_waves_per_eu(attn_occupancy<D>(), attn_occupancy<D>())))
 void paged_attention_kernel(const KParams p) {
   __shared__ UnitSmem<D, NW> sm;
   const int per_plane = p.num_seqs * p.num_kv_heads;
   const int plane = static_cast<int>(blockIdx.x) / per_plane;
-  const int part = SPLIT ? p.num_slots - 1 - plane : 0;
   const int rot = static_cast<int>(blockIdx.x) - plane * per_plane;
-  const int unit = (rot + per_plane - part % per_plane) % per_plane;
+  const int unit = (rot + per_plane - plane % per_plane) % per_plane;
   const int seq = unit / p.num_kv_heads;
   const int kv_head = unit - seq * p.num_kv_heads;
-  const int seq_len = p.seq_lens[seq];
-  const int start = SPLIT ? part * p.part_tokens : 0;
+  int start = 0;
+  int unit_tokens = kPart;
+  int seq_len = p.seq_lens[seq];
+  if constexpr (SPLIT) {
+    const int full_planes = p.num_units - 1;  // positions 1 .. num_units - 1, 1024 tokens each
+    if (plane < full_planes) {
+      start = (full_planes - plane) * kUnit;
+      unit_tokens = kUnit;
+    } else {
+      start = plane == full_planes ? kPart : 0;
+    }
+    seq_len = min(seq_len, p.max_partitions * kPart);  // tokens past the workspace are ignored
+  }
   if (start >= seq_len) {
     if (!SPLIT) {
       for (int idx = threadIdx.x; idx < p.group * D; idx += NW * kWave) {
@@ -434,7 +449,7 @@ void paged_attention_kernel(const KParams p) {
     }
     return;
   }
-  attention_unit<E, D, SPLIT, BS16, ALIGN, NW>(p, kv_head, seq, part, seq_len, sm, [] {});
+  attention_unit<E, D, SPLIT, BS16, ALIGN, NW>(p, kv_head, seq, start, unit_tokens, seq_len, start / kPart, sm, [] {});
 }
 
 // Persistent split-K kernel: a resident-sized grid pulls work units from a
@@ -463,8 +478,8 @@ void paged_attention_persistent_kernel(const KParams p) {
   __shared__ int next_unit;
   const int tid = threadIdx.x;
   const int S = p.num_seqs;
-  const int T = p.part_tokens;
-  const int max_tokens = p.num_slots * T;  // tokens past the workspace are ignored, as in the grid path
+  constexpr int T = kUnit;
+  const int max_tokens = p.max_partitions * kPart;  // tokens past the workspace are ignored, as in the grid path
   auto clamped_len = [&](int s) { return min(max(p.seq_lens[s], 0), max_tokens); };
 
   // Per-thread chunk of sequences -> block-wide exclusive scan of (full, tail) counts.
@@ -534,7 +549,7 @@ void paged_attention_persistent_kernel(const KParams p) {
       seq = find(pr, v / hkv);
       part = clamped_len(seq) / T;
     }
-    attention_unit<E, D, true, BS16, ALIGN, NW>(p, kv_head, seq, part, clamped_len(seq), sm, [&] {
+    attention_unit<E, D, true, BS16, ALIGN, NW>(p, kv_head, seq, part * T, T, clamped_len(seq), 2 * part, sm, [&] {
       if (!dealt_unit && tid == 0) next_unit = dealt + static_cast<int>(atomicAdd(p.unit_counter, 1u));
     });
     u = dealt_unit && !last_dealt ? u + G : next_unit;
@@ -547,7 +562,7 @@ __global__ void zero_counter_kernel(unsigned* counter) {
   if (threadIdx.x == 0) *counter = 0u;
 }
 
-// Log-sum-exp merge of the work units of one (query head, sequence):
+// Log-sum-exp merge of the 512-token slots of one (query head, sequence):
 //   M = max_p m_p,  w_p = s_p * exp(m_p - M),  out = sum_p w_p o_p / sum_p w_p
 // (reference: csrc/paged_attention.cuh:227-269). WPH waves per query head,
 // kReduceWaves waves per workgroup. The (m_p, s_p) pairs are uniform across a
@@ -556,7 +571,7 @@ __global__ void zero_counter_kernel(unsigned* counter) {
 constexpr int kReduceWaves = 4;
 
 template <typename E, int D, int WPH>
-__global__ __launch_bounds__(kReduceWaves * kWave) void paged_attention_reduce_kernel(const KParams p, int num_slots) {
+__global__ __launch_bounds__(kReduceWaves * kWave) void paged_attention_reduce_kernel(const KParams p) {
   constexpr int C = D / kWave;  // columns per lane (1, 2 or 4)
   constexpr int HPW = kReduceWaves / WPH;  // heads per workgroup
   const int wave = static_cast<int>(threadIdx.x) / kWave;
@@ -575,20 +590,31 @@ __global__ __launch_bounds__(kReduceWaves * kWave) void paged_attention_reduce_k
     }
     return;
   }
-  const int n = min((seq_len + p.part_tokens - 1) / p.part_tokens, num_slots);
+  const int n = min((seq_len + kPart - 1) / kPart, p.max_partitions);
   const int64_t row0 = (static_cast<int64_t>(seq) * p.num_q_heads + (active ? q_head : 0)) * p.max_partitions;
   const float* ml = p.max_logits + row0;
   const float* es = p.exp_sums + row0;
   const float* tmp = p.tmp_out + row0 * D + C * lane;
 
+  // Slots holding results: 0, 1 (a 512-token unit in the grid schedule; marked
+  // empty by the persistent schedule, whose unit 0 spans 1024 tokens) and the
+  // even slots >= 2 (1024-token units); odd slots >= 3 are always empty. They
+  // are walked by index so that no load waits on another's value.
+  const int units = 2 + (n - 1) / 2;  // entries j: slot 0, slot 1, then slot 2 (j - 1)
+  const bool slot1 = n > 1 && es[1] != 0.0f;
   float M = -__builtin_huge_valf();
-  for (int i = 0; i < n; ++i) M = fmaxf(M, ml[i]);
+  for (int j = lane; j < units; j += kWave) {
+    if (j != 1 || slot1) M = fmaxf(M, ml[j < 2 ? j : 2 * (j - 1)]);
+  }
+  M = wave_max(M);
   float W = 0.0f;
   float acc[C];
 #pragma unroll
   for (int c = 0; c < C; ++c) acc[c] = 0.0f;
 #pragma unroll 4
-  for (int i = sub; i < n; i += WPH) {
+  for (int j = sub; j < units; j += WPH) {
+    if (j == 1 && !slot1) continue;
+    const int i = j < 2 ? j : 2 * (j - 1);
     const float w = es[i] * __builtin_amdgcn_exp2f((ml[i] - M) * kLog2e);
     W += w;
     const float* t = tmp + static_cast<int64_t>(i) * D;
@@ -694,43 +720,45 @@ inline Schedule forced_schedule() {
 }
 
 template <typename E, int D, bool BS16>
-hipError_t launch_split(KParams kp, int num_kv_heads, int num_seqs, int num_slots, int align, hipStream_t stream) {
-  const int64_t units_bound = static_cast<int64_t>(num_kv_heads) * num_seqs * num_slots;
+hipError_t launch_split(KParams kp, int num_kv_heads, int num_seqs, int align, hipStream_t stream) {
+  const int64_t per_plane = static_cast<int64_t>(num_kv_heads) * num_seqs;
+  const int64_t grid_units = per_plane * (kp.num_units + 1);  // 1024-token planes + two 512-token planes
   // The persistent kernel pays a counter reset and a unit-list setup; it wins
   // when the grid would be mostly slots past their sequence's end, i.e. many
-  // slots per sequence and a grid several times the resident workgroups.
+  // unit positions per sequence and a grid several times the resident workgroups.
   const Schedule forced = forced_schedule();
   int resident = 0;
   if (num_seqs <= kMaxPersistSeqs && kp.unit_counter != nullptr && forced != Schedule::kGrid &&
-      (num_slots >= 8 || forced == Schedule::kPersistent)) {
+      (kp.num_units >= 8 || forced == Schedule::kPersistent)) {
     const hipError_t e = launch_aligned<E, D, true, BS16, true>(kp, 0, align, stream, &resident);
     if (e != hipSuccess) return e;
   }
-  if (resident <= 0 || (forced != Schedule::kPersistent && units_bound <= 4 * static_cast<int64_t>(resident)))
-    return launch_aligned<E, D, true, BS16, false>(kp, static_cast<unsigned>(units_bound), align, stream);
+  if (resident <= 0 || (forced != Schedule::kPersistent && grid_units <= 4 * static_cast<int64_t>(resident)))
+    return launch_aligned<E, D, true, BS16, false>(kp, static_cast<unsigned>(grid_units), align, stream);
   hipLaunchKernelGGL(zero_counter_kernel, dim3(1), dim3(kWave), 0, stream, kp.unit_counter);
+  const int64_t units_bound = per_plane * kp.num_units;
   const unsigned grid = static_cast<unsigned>(units_bound < resident ? units_bound : resident);
   return launch_aligned<E, D, true, BS16, true>(kp, grid, align, stream);
 }
 
 template <typename E, int D>
-hipError_t launch(const KParams& kp, int num_kv_heads, int num_seqs, bool split, int num_slots, bool bs16, int align,
+hipError_t launch(const KParams& kp, int num_kv_heads, int num_seqs, bool split, bool bs16, int align,
                   hipStream_t stream) {
   if (!split) {
     const unsigned grid = static_cast<unsigned>(num_kv_heads * num_seqs);
     return bs16 ? launch_aligned<E, D, false, true, false>(kp, grid, align, stream)
                 : launch_aligned<E, D, false, false, false>(kp, grid, align, stream);
   }
-  hipError_t e = bs16 ? launch_split<E, D, true>(kp, num_kv_heads, num_seqs, num_slots, align, stream)
-                      : launch_split<E, D, false>(kp, num_kv_heads, num_seqs, num_slots, align, stream);
+  hipError_t e = bs16 ? launch_split<E, D, true>(kp, num_kv_heads, num_seqs, align, stream)
+                      : launch_split<E, D, false>(kp, num_kv_heads, num_seqs, align, stream);
   if (e != hipSuccess) return e;
   const dim3 rblock(kReduceWaves * kWave);
-  if (num_slots <= 16) {
+  if (kp.max_partitions <= 32) {
     const dim3 rgrid((kp.num_q_heads + kReduceWaves - 1) / kReduceWaves, num_seqs);
-    hipLaunchKernelGGL((paged_attention_reduce_kernel<E, D, 1>), rgrid, rblock, 0, stream, kp, num_slots);
+    hipLaunchKernelGGL((paged_attention_reduce_kernel<E, D, 1>), rgrid, rblock, 0, stream, kp);
   } else {
     const dim3 rgrid(kp.num_q_heads, num_seqs);
-    hipLaunchKernelGGL((paged_attention_reduce_kernel<E, D, kReduceWaves>), rgrid, rblock, 0, stream, kp, num_slots);
+    hipLaunchKernelGGL((paged_attention_reduce_kernel<E, D, kReduceWaves>), rgrid, rblock, 0, stream, kp);
   }
   return hipGetLastError();
 }
@@ -778,7 +806,6 @@ extern "C" int dk_paged_attention_decode(const dk_paged_attn_params* a, int dtyp
     return fail("paged_attention_decode: num_seqs and head counts must be at most 65535");
 
   const bool split = max_seq_len > kPart;
-  int num_slots = 1;
   if (split) {
     if (a->tmp_out == nullptr || a->max_logits == nullptr || a->exp_sums == nullptr)
       return fail("split-K workspace tensors must be provided when max_seq_len > %d", kPart);
@@ -812,37 +839,36 @@ extern "C" int dk_paged_attention_decode(const dk_paged_attn_params* a, int dtyp
   kp.group = group;
   kp.block_size = a->block_size;
   kp.max_partitions = split ? a->max_partitions : 1;
-  // Split-K work units of DK_ATTN_UNIT_SLOTS x 512 tokens; unit z writes
-  // workspace slot z. Like the reference, the grid covers max_partitions x 512
-  // tokens, so a too-small max_seq_len still bounds every access.
-  kp.part_tokens = split ? kPart * DK_ATTN_UNIT_SLOTS : kPart;
-  if (split) num_slots = static_cast<int>(ceil_div64(static_cast<int64_t>(a->max_partitions) * kPart, kp.part_tokens));
+  // Split-K: workspace slot p holds tokens [512 p, 512 p + 512) as the
+  // reference's partition p; work units cover one or two slots. Like the
+  // reference, only max_partitions x 512 tokens are read, so a too-small
+  // max_seq_len still bounds every access.
+  kp.num_units = split ? static_cast<int>(ceil_div64(a->max_partitions, 2)) : 1;
   kp.scale_log2 = a->scale * kLog2e;
-  if (static_cast<int64_t>(a->num_seqs) * a->num_kv_heads * num_slots >= (int64_t{1} << 31))
+  if (static_cast<int64_t>(a->num_seqs) * a->num_kv_heads * (kp.num_units + 1) >= (int64_t{1} << 31))
     return fail("paged_attention_decode: num_seqs x num_kv_heads x partitions is too large");
   kp.num_seqs = a->num_seqs;
   kp.num_kv_heads = a->num_kv_heads;
-  kp.num_slots = num_slots;
-  // The persistent split-K kernel's unit counter lives in an exp_sums entry
-  // that is never written or read otherwise: work units use slots
-  // 0 .. num_slots - 1 of the max_partitions >= 2 slots, so slot
-  // max_partitions - 1 of (sequence 0, head 0) is free.
-  kp.unit_counter = split ? reinterpret_cast<unsigned*>(a->exp_sums + (a->max_partitions - 1)) : nullptr;
+  // The persistent split-K kernel's unit counter lives in the tmp_out row of
+  // slot 1 of (sequence 0, query head 0): that kernel's 1024-token units write
+  // results to even slots only and mark odd slots empty in exp_sums, so the
+  // row is neither written nor read as data (max_partitions >= 2 here).
+  kp.unit_counter = split ? reinterpret_cast<unsigned*>(a->tmp_out + head_dim) : nullptr;
 
   const bool bs16 = a->block_size % kTile == 0;
   hipStream_t s = static_cast<hipStream_t>(stream);
   hipError_t e;
   if (dtype == DK_BFLOAT16) {
     switch (head_dim) {
-      case 64: e = launch<Bf16, 64>(kp, a->num_kv_heads, a->num_seqs, split, num_slots, bs16, align, s); break;
-      case 128: e = launch<Bf16, 128>(kp, a->num_kv_heads, a->num_seqs, split, num_slots, bs16, align, s); break;
-      default: e = launch<Bf16, 256>(kp, a->num_kv_heads, a->num_seqs, split, num_slots, bs16, align, s); break;
+      case 64: e = launch<Bf16, 64>(kp, a->num_kv_heads, a->num_seqs, split, bs16, align, s); break;
+      case 128: e = launch<Bf16, 128>(kp, a->num_kv_heads, a->num_seqs, split, bs16, align, s); break;
+      default: e = launch<Bf16, 256>(kp, a->num_kv_heads, a->num_seqs, split, bs16, align, s); break;
     }
   } else {
     switch (head_dim) {
-      case 64: e = launch<F16, 64>(kp, a->num_kv_heads, a->num_seqs, split, num_slots, bs16, align, s); break;
-      case 128: e = launch<F16, 128>(kp, a->num_kv_heads, a->num_seqs, split, num_slots, bs16, align, s); break;
-      default: e = launch<F16, 256>(kp, a->num_kv_heads, a->num_seqs, split, num_slots, bs16, align, s); break;
+      case 64: e = launch<F16, 64>(kp, a->num_kv_heads, a->num_seqs, split, bs16, align, s); break;
+      case 128: e = launch<F16, 128>(kp, a->num_kv_heads, a->num_seqs, split, bs16, align, s); break;
+      default: e = launch<F16, 256>(kp, a->num_kv_heads, a->num_seqs, split, bs16, align, s); break;
     }
   }
   return static_cast<int>(e);

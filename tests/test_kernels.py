@@ -18,6 +18,7 @@ import decodekernels_amd as dk
 from decodekernels_amd.testing import make_paged_kv
 from parity import (
     assert_max_abs,
+    half_ulp,
     assert_ulp,
     attention_f32,
     fused_add_rms_norm_reference,
@@ -179,8 +180,10 @@ SCHEDULE_CASES = [
 @pytest.mark.parametrize("case", SCHEDULE_CASES, ids=lambda c: f"d{c[0]}_hkv{c[1]}_g{c[2]}_bs{c[3]}_{c[4]}")
 def test_paged_attention_split_k_schedules(case, monkeypatch):
     """Split-K under both schedules -- one workgroup per unit slot, and resident
-    workgroups pulling the live units from a counter -- against the oracle,
-    and bit-identical to each other."""
+    workgroups pulling the live units from a counter -- against the oracle.
+    The two cut a sequence's first 1024 tokens differently (two 512-token
+    units vs one), so they agree to rounding: within 2 ulp of the model dtype
+    at the reference value (plus 1e-5 near zero)."""
     d, hkv, group, bs, layout, n, max_len, dtype = case
     lens = _log_uniform_lens(n, max_len, seed=d + bs)
     kv = make_paged_kv(lens, hkv, d, bs, dtype, "cuda", layout=layout, seed=d + 1)
@@ -195,7 +198,9 @@ def test_paged_attention_split_k_schedules(case, monkeypatch):
     ref = attention_f32(q, kv.k_cache, kv.v_cache, kv.block_tables, kv.seq_lens)
     for schedule, out in outs.items():
         assert_max_abs(out, ref, dtype, f"{schedule} schedule")
-    assert torch.equal(outs["grid"], outs["persistent"])
+    diff = (outs["grid"].float() - outs["persistent"].float()).abs().cpu()
+    bound = 4 * half_ulp(ref, dtype) + 1e-5
+    assert (diff <= bound).all(), f"grid vs persistent differ by {diff.max().item():.3e}"
 
 
 def test_paged_attention_persistent_schedule_short_sequences(monkeypatch):
