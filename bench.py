@@ -365,6 +365,21 @@ TRAFFIC_PROFILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "prof
 CALIBRATION_BYTES = 256 << 20
 
 
+def pmc_workload_gemm(calls: int = 3) -> None:
+    """What the GEMM counter runs profile: gemm_tn at a prefill shape (M=4096,
+    N=K=4096: 256x256 tiles) and a batched-decode shape (M=256, N=6144,
+    K=4096: 128x64 tiles), `calls` times each."""
+    g = torch.Generator(device="cuda").manual_seed(30)
+    for m, n in ((4096, 4096), (256, 6144)):
+        a = torch.randn(m, 4096, generator=g, device="cuda", dtype=torch.bfloat16) * 0.02
+        w = torch.randn(n, 4096, generator=g, device="cuda", dtype=torch.bfloat16) * 0.02
+        c = torch.empty(m, n, device="cuda", dtype=torch.bfloat16)
+        for _ in range(calls):
+            torch.ops.decode_kernels.gemm_tn(c, a, w, None)
+    torch.cuda.synchronize()
+    print(f"pmc gemm workload done: {calls} calls each at M=4096 N=4096 and M=256 N=6144 (K=4096)", flush=True)
+
+
 def pmc_workload(calls: int = 5) -> None:
     """What the counter runs profile: the headline op `calls` times, then a
     copy of CALIBRATION_BYTES (read once, written once) to scale the counters."""
@@ -398,7 +413,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-extras", action="store_true", help="skip the secondary configs")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline (and its correctness check)")
-    ap.add_argument("--pmc-workload", action="store_true", help="run only what the rocprofv3 --pmc passes profile")
+    ap.add_argument("--pmc-workload", nargs="?", const="attention", choices=["attention", "gemm"],
+                    help="run only what the rocprofv3 --pmc passes profile (default: attention)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: every work unit of this path fits one MI355X and no multi-GPU "
@@ -406,6 +422,9 @@ def main() -> int:
         return 2
     if not dk.is_available():
         raise RuntimeError("decodekernels_amd HIP extension not available (build it with __graft_entry__.build())")
+    if args.pmc_workload == "gemm":
+        pmc_workload_gemm()
+        return 0
     if args.pmc_workload:
         pmc_workload()
         return 0

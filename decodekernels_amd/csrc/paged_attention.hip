@@ -154,46 +154,106 @@ struct UnitSmem {
   float o[NW][kMaxGroup][D];    // partial outputs
 };
 
-// One work unit: tokens [start, min(start + unit_tokens, seq_len)) of sequence
-// `seq` (seq_len > start, at most 1024 tokens) for KV head `kv_head` and its
-// query-head group, on NW waves; each wave keeps DEPTH tiles of loads in
-// flight. Split-K writes the unit's result to workspace slot `slot`, and for a
-// 1024-token unit marks slot + 1 empty (max logit -inf, exp-sum 0) so that the
-// reduce can walk 512-token slots exactly as the reference's partitions.
-// `before_merge` runs once every wave has consumed its last tile, before the
-// LDS merge.
-template <typename E, int D, bool SPLIT, bool BS16, int ALIGN, int NW, typename Hook>
-__device__ __forceinline__ void attention_unit(const KParams& p, int kv_head, int seq, int start, int unit_tokens,
-                                               int seq_len, int slot, UnitSmem<D, NW>& sm, Hook before_merge) {
-  constexpr int CH = D / 32;  // 32-column chunks per row
-  constexpr int NB = D / 16;  // 16-column output blocks
-  constexpr int DEPTH = D >= 256 ? DK_ATTN_DEPTH_D256 : DK_ATTN_DEPTH;
-  constexpr int NT = NW * kWave;
+// A work unit: tokens [start, end) of sequence `seq` (end > start, at most
+// 1024 tokens) for KV head `kv_head` and its query-head group. Split-K writes
+// its result to workspace slot `slot`; a unit of more than 512 tokens marks
+// slot + 1 empty (max logit -inf, exp-sum 0), so the reduce walks 512-token
+// slots exactly as the reference's partitions.
+struct Unit {
+  int kv_head, seq, start, end, slot;
+  bool two_slots;
+};
+
+__device__ __forceinline__ Unit make_unit(int kv_head, int seq, int start, int unit_tokens, int seq_len, int slot) {
+  return Unit{kv_head, seq, start, min(start + unit_tokens, seq_len), slot, unit_tokens > kPart};
+}
+
+// Barrier for data exchanged through LDS only: global loads issued before it
+// stay in flight (a full __syncthreads fence would wait for them).
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// Runs work units on NW waves: wave w takes tiles w, w + NW, ... of a unit,
+// keeps DEPTH tiles of loads in flight and its own online-softmax state; the
+// waves merge through LDS. The steps are separate so that the persistent
+// kernel can issue the next unit's loads before merging the current one.
+template <typename E, int D, bool SPLIT, bool BS16, int ALIGN, int NW>
+struct UnitEngine {
+  static constexpr int CH = D / 32;  // 32-column chunks per row
+  static constexpr int NB = D / 16;  // 16-column output blocks
+  static constexpr int DEPTH = D >= 256 ? DK_ATTN_DEPTH_D256 : DK_ATTN_DEPTH;
+  static constexpr int NT = NW * kWave;
   using Tile = TileRegs<CH>;
 
-  const int tid = threadIdx.x;
-  const int lane = tid % kWave;
-  const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
-  const int l16 = lane % 16;  // K/V row of the tile, head of the logits, output column
-  const int lg = lane / 16;   // lane group 0..3
-  const int group = p.group;
+  const KParams& p;
+  UnitSmem<D, NW>& sm;
+  int tid, lane, wave, l16, lg;
+  u32x4 eye0, eye1;  // identity fragments (see process)
+  u32x4 qf[CH];      // query fragments of the current unit
+  Tile buf[DEPTH];   // tiles in flight
+  f32x4 acc[NB];
+  float m_ref;   // reference max (log2 units) of head l16
+  float m_true;  // exact running max of head l16
+  float l_run;   // this lane's share of the exp-sum against m_ref
 
-  const int end = min(start + unit_tokens, seq_len);
-  const int n_tiles = (end - start + kTile - 1) / kTile;
-
-  // Block-table entries of this work unit (lane e holds entry lb0 + e) when
-  // every 16-token tile lies inside one cache block.
-  const int32_t* bt_row = p.block_tables + seq * p.bt_stride;
-  int lb0 = 0;
-  int bt_lane = 0;
-  if constexpr (BS16) {
-    lb0 = start / p.block_size;
-    const int lb_last = (end - 1) / p.block_size;
-    if (lb0 + lane <= lb_last) bt_lane = bt_row[lb0 + lane];
+  __device__ __forceinline__ UnitEngine(const KParams& params, UnitSmem<D, NW>& smem) : p(params), sm(smem) {
+    tid = threadIdx.x;
+    lane = tid % kWave;
+    wave = __builtin_amdgcn_readfirstlane(tid / kWave);
+    l16 = lane % 16;  // K/V row of the tile, head of the logits, output column
+    lg = lane / 16;   // lane group 0..3
+    // Identity fragments (B operand of a 16x16x32 MFMA): with them, an MFMA
+    // whose A operand is a V chunk returns V transposed into the B-operand
+    // layout of v_mfma_f32_16x16x16 -- lane l: V[token 4*lg + r][column l16 (+16)].
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int k0 = 8 * lg + 2 * e;
+      eye0[e] = (k0 == l16 ? E::kOne : 0u) | ((k0 + 1 == l16 ? E::kOne : 0u) << 16);
+      eye1[e] = (k0 == l16 + 16 ? E::kOne : 0u) | ((k0 + 1 == l16 + 16 ? E::kOne : 0u) << 16);
+    }
+    reset();
   }
 
-  const uint16_t* kbase = p.k + kv_head * p.k_sh;
-  const uint16_t* vbase = p.v + kv_head * p.v_sh;
+  __device__ __forceinline__ void reset() {
+#pragma unroll
+    for (int n = 0; n < NB; ++n) acc[n] = f32x4{0.f, 0.f, 0.f, 0.f};
+    m_ref = -__builtin_huge_valf();
+    m_true = -__builtin_huge_valf();
+    l_run = 0.0f;
+  }
+
+  __device__ __forceinline__ int n_tiles(const Unit& u) const { return (u.end - u.start + kTile - 1) / kTile; }
+
+  // Block-table entries of a unit (lane e holds entry start / block_size + e)
+  // when every 16-token tile lies inside one cache block.
+  __device__ __forceinline__ int load_bt(const Unit& u) const {
+    int v = 0;
+    if constexpr (BS16) {
+      const int lb0 = u.start / p.block_size;
+      const int lb_last = (u.end - 1) / p.block_size;
+      if (lb0 + lane <= lb_last) v = p.block_tables[u.seq * p.bt_stride + lb0 + lane];
+    }
+    return v;
+  }
+
+  // Query fragments (B operand of Q·Kᵀ): head l16, columns 8*lg + 32*c ... +7,
+  // in the model dtype; heads past the group are zero.
+  __device__ __forceinline__ void load_q(const Unit& u) {
+    const uint16_t* qrow = p.q + u.seq * p.q_ss + (u.kv_head * p.group + l16) * p.q_sh;
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+      u32x4 w = {0u, 0u, 0u, 0u};
+      if (l16 < p.group) {
+        const uint16_t* src = qrow + 8 * lg + 32 * c;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) w[e] = static_cast<uint32_t>(src[2 * e]) | (static_cast<uint32_t>(src[2 * e + 1]) << 16);
+      }
+      qf[c] = w;
+    }
+  }
 
   // Issues the loads of one tile. Tiles past the end are still "loaded" so
   // every wave runs the same load sequence (the compiler then waits for
@@ -201,14 +261,17 @@ __device__ __forceinline__ void attention_unit(const KParams& p, int kv_head, in
   // has num_records = 0 and nothing is read; otherwise the last tile is
   // re-read (an L2 hit). Rows past the sequence end are clamped to its last
   // row, so V never contributes uninitialised cache contents.
-  auto load_tile = [&](int tile, Tile& r) {
-    const bool live = tile < n_tiles;
-    const int tt = live ? tile : n_tiles - 1;
-    const int t0 = start + tt * kTile;
-    const int row = min(l16, end - 1 - t0);
+  __device__ __forceinline__ void load_tile(const Unit& u, int bt_lane, int tile, Tile& r) const {
+    const int nt = n_tiles(u);
+    const bool live = tile < nt;
+    const int tt = live ? tile : nt - 1;
+    const int t0 = u.start + tt * kTile;
+    const int row = min(l16, u.end - 1 - t0);
+    const uint16_t* kbase = p.k + u.kv_head * p.k_sh;
+    const uint16_t* vbase = p.v + u.kv_head * p.v_sh;
     if constexpr (BS16) {
       const int lb = t0 / p.block_size;
-      const int phys = __builtin_amdgcn_readlane(bt_lane, lb - lb0);
+      const int phys = __builtin_amdgcn_readlane(bt_lane, lb - u.start / p.block_size);
       const int off = t0 - lb * p.block_size;
       const uint16_t* kt = kbase + static_cast<int64_t>(phys) * p.k_sb + static_cast<int64_t>(off) * p.k_st;
       const uint16_t* vt = vbase + static_cast<int64_t>(phys) * p.v_sb + static_cast<int64_t>(off) * p.v_st;
@@ -224,7 +287,7 @@ __device__ __forceinline__ void attention_unit(const KParams& p, int kv_head, in
     } else {
       const int t = t0 + row;
       const int lb = t / p.block_size;
-      const int64_t phys = bt_row[lb];
+      const int64_t phys = p.block_tables[u.seq * p.bt_stride + lb];
       const int64_t off = t - lb * p.block_size;
       const uint16_t* kp = kbase + phys * p.k_sb + off * p.k_st + 8 * lg;
       const uint16_t* vp = vbase + phys * p.v_sb + off * p.v_st + 8 * lg;
@@ -233,66 +296,32 @@ __device__ __forceinline__ void attention_unit(const KParams& p, int kv_head, in
 #pragma unroll
       for (int c = 0; c < CH; ++c) r.v[c] = load8<ALIGN>(vp + 32 * c);
     }
-  };
+  }
 
-  // Query fragments (B operand of Q·Kᵀ): head l16, columns 8*lg + 32*c ... +7,
-  // in the model dtype; heads past the group are zero. Loaded before the
-  // tiles so that waiting for them never waits for a tile prefetch.
-  u32x4 qf[CH];
-  {
-    const uint16_t* qrow = p.q + seq * p.q_ss + (kv_head * group + l16) * p.q_sh;
+  // The first DEPTH tiles of this wave. The scheduling barriers keep the
+  // tiles' load groups in program order, so the oldest outstanding loads are
+  // always those of the next tile consumed.
+  __device__ __forceinline__ void prologue(const Unit& u, int bt_lane) {
 #pragma unroll
-    for (int c = 0; c < CH; ++c) {
-      u32x4 w = {0u, 0u, 0u, 0u};
-      if (l16 < group) {
-        const uint16_t* src = qrow + 8 * lg + 32 * c;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) w[e] = static_cast<uint32_t>(src[2 * e]) | (static_cast<uint32_t>(src[2 * e + 1]) << 16);
-      }
-      qf[c] = w;
+    for (int i = 0; i < DEPTH; ++i) {
+      load_tile(u, bt_lane, wave + i * NW, buf[i]);
+      __builtin_amdgcn_sched_barrier(0);
     }
   }
 
-  // The scheduling barriers keep the tiles' load groups in program order, so
-  // the oldest outstanding loads are always those of the next tile consumed.
-  Tile buf[DEPTH];
-#pragma unroll
-  for (int i = 0; i < DEPTH; ++i) {
-    load_tile(wave + i * NW, buf[i]);
-    __builtin_amdgcn_sched_barrier(0);
-  }
-
-  // Identity fragments (B operand of a 16x16x32 MFMA): with them, an MFMA
-  // whose A operand is a V chunk returns V transposed into the B-operand
-  // layout of v_mfma_f32_16x16x16 -- lane l: V[token 4*lg + r][column l16 (+16)].
-  u32x4 eye0, eye1;
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    const int k0 = 8 * lg + 2 * e;
-    eye0[e] = (k0 == l16 ? E::kOne : 0u) | ((k0 + 1 == l16 ? E::kOne : 0u) << 16);
-    eye1[e] = (k0 == l16 + 16 ? E::kOne : 0u) | ((k0 + 1 == l16 + 16 ? E::kOne : 0u) << 16);
-  }
-
-  f32x4 acc[NB];
-#pragma unroll
-  for (int n = 0; n < NB; ++n) acc[n] = f32x4{0.f, 0.f, 0.f, 0.f};
-  float m_ref = -__builtin_huge_valf();   // reference max (log2 units) of head l16
-  float m_true = -__builtin_huge_valf();  // exact running max of head l16
-  float l_run = 0.0f;                     // this lane's share of the exp-sum against m_ref
-
   // Online softmax + P·V for one live tile held in `r`.
-  auto process = [&](int tile, const Tile& r) {
+  __device__ __forceinline__ void process(const Unit& u, int tile, const Tile& r) {
     // Q·Kᵀ: S[token 4*lg + i][head l16].
     f32x4 s = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int c = 0; c < CH; ++c) s = E::mfma_16x16x32(r.k[c], qf[c], s);
 
-    const int t0 = start + tile * kTile;
+    const int t0 = u.start + tile * kTile;
     float x[4];
     float tmax = -__builtin_huge_valf();
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const bool valid = t0 + 4 * lg + i < end;
+      const bool valid = t0 + 4 * lg + i < u.end;
       x[i] = valid ? s[i] * p.scale_log2 : -__builtin_huge_valf();
       tmax = fmaxf(tmax, x[i]);
     }
@@ -334,79 +363,85 @@ __device__ __forceinline__ void attention_unit(const KParams& p, int kv_head, in
       acc[2 * c + 1] = E::mfma_16x16x16(p_hi, v_hi, acc[2 * c + 1]);
       acc[2 * c + 1] = E::mfma_16x16x16(p_lo, v_hi, acc[2 * c + 1]);
     }
-  };
+  }
 
   // Steady state: consume the oldest tile, refill its registers DEPTH tiles
   // ahead. Loads are issued on every path, so the wait before each tile is
   // for exactly that tile's loads.
-  for (int base = wave; base < n_tiles; base += DEPTH * NW) {
+  __device__ __forceinline__ void run_tiles(const Unit& u, int bt_lane) {
+    const int nt = n_tiles(u);
+    for (int base = wave; base < nt; base += DEPTH * NW) {
 #pragma unroll
-    for (int i = 0; i < DEPTH; ++i) {
-      const int t = base + i * NW;
-      if (t < n_tiles) process(t, buf[i]);
-      load_tile(t + DEPTH * NW, buf[i]);
-      __builtin_amdgcn_sched_barrier(0);
-    }
-  }
-
-  before_merge();
-
-  // Exp-sum of head l16 over all four lane groups.
-  float l_tot = l_run + __shfl_xor(l_run, 16, kWave);
-  l_tot += __shfl_xor(l_tot, 32, kWave);
-
-  if (lane < 16) {
-    sm.m[wave][lane] = m_ref;
-    sm.t[wave][lane] = m_true;
-    sm.l[wave][lane] = l_tot;
-  }
-  // acc[n] lane l: O[head 4*lg + i][column 16n + l16].
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int h = 4 * lg + i;
-    if (h < group) {
-#pragma unroll
-      for (int n = 0; n < NB; ++n) sm.o[wave][h][16 * n + l16] = acc[n][i];
-    }
-  }
-  __syncthreads();
-
-  for (int idx = tid; idx < group * D; idx += NT) {
-    const int h = idx / D;
-    const int d = idx - h * D;
-    float M = sm.m[0][h];
-#pragma unroll
-    for (int w = 1; w < NW; ++w) M = fmaxf(M, sm.m[w][h]);
-    float L = 0.0f;
-    float O = 0.0f;
-#pragma unroll
-    for (int w = 0; w < NW; ++w) {
-      const float f = __builtin_amdgcn_exp2f(sm.m[w][h] - M);
-      L += f * sm.l[w][h];
-      O += f * sm.o[w][h][d];
-    }
-    const float res = O / L;
-    const int q_head = kv_head * group + h;
-    if constexpr (SPLIT) {
-      const int64_t row = (static_cast<int64_t>(seq) * p.num_q_heads + q_head) * p.max_partitions + slot;
-      p.tmp_out[row * D + d] = res;
-      if (d == 0) {
-        // Report (max logit, exp-sum) against the unit's true max.
-        float T = sm.t[0][h];
-#pragma unroll
-        for (int w = 1; w < NW; ++w) T = fmaxf(T, sm.t[w][h]);
-        p.max_logits[row] = T * kLn2;
-        p.exp_sums[row] = L * __builtin_amdgcn_exp2f(M - T);
-        if (unit_tokens > kPart && slot + 1 < p.max_partitions) {
-          p.max_logits[row + 1] = -__builtin_huge_valf();
-          p.exp_sums[row + 1] = 0.0f;
-        }
+      for (int i = 0; i < DEPTH; ++i) {
+        const int t = base + i * NW;
+        if (t < nt) process(u, t, buf[i]);
+        load_tile(u, bt_lane, t + DEPTH * NW, buf[i]);
+        __builtin_amdgcn_sched_barrier(0);
       }
-    } else {
-      p.out[seq * p.o_ss + q_head * p.o_sh + d] = E::from_float(res);
     }
   }
-}
+
+  // Merges the waves' states through LDS and writes the unit's result; ends
+  // with a barrier, after which the LDS may be reused.
+  __device__ __forceinline__ void merge(const Unit& u) {
+    const int group = p.group;
+    // Exp-sum of head l16 over all four lane groups.
+    float l_tot = l_run + __shfl_xor(l_run, 16, kWave);
+    l_tot += __shfl_xor(l_tot, 32, kWave);
+    if (lane < 16) {
+      sm.m[wave][lane] = m_ref;
+      sm.t[wave][lane] = m_true;
+      sm.l[wave][lane] = l_tot;
+    }
+    // acc[n] lane l: O[head 4*lg + i][column 16n + l16].
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int h = 4 * lg + i;
+      if (h < group) {
+#pragma unroll
+        for (int n = 0; n < NB; ++n) sm.o[wave][h][16 * n + l16] = acc[n][i];
+      }
+    }
+    lds_barrier();
+
+    for (int idx = tid; idx < group * D; idx += NT) {
+      const int h = idx / D;
+      const int d = idx - h * D;
+      float M = sm.m[0][h];
+#pragma unroll
+      for (int w = 1; w < NW; ++w) M = fmaxf(M, sm.m[w][h]);
+      float L = 0.0f;
+      float O = 0.0f;
+#pragma unroll
+      for (int w = 0; w < NW; ++w) {
+        const float f = __builtin_amdgcn_exp2f(sm.m[w][h] - M);
+        L += f * sm.l[w][h];
+        O += f * sm.o[w][h][d];
+      }
+      const float res = O / L;
+      const int q_head = u.kv_head * group + h;
+      if constexpr (SPLIT) {
+        const int64_t row = (static_cast<int64_t>(u.seq) * p.num_q_heads + q_head) * p.max_partitions + u.slot;
+        p.tmp_out[row * D + d] = res;
+        if (d == 0) {
+          // Report (max logit, exp-sum) against the unit's true max.
+          float T = sm.t[0][h];
+#pragma unroll
+          for (int w = 1; w < NW; ++w) T = fmaxf(T, sm.t[w][h]);
+          p.max_logits[row] = T * kLn2;
+          p.exp_sums[row] = L * __builtin_amdgcn_exp2f(M - T);
+          if (u.two_slots && u.slot + 1 < p.max_partitions) {
+            p.max_logits[row + 1] = -__builtin_huge_valf();
+            p.exp_sums[row + 1] = 0.0f;
+          }
+        }
+      } else {
+        p.out[u.seq * p.o_ss + q_head * p.o_sh + d] = E::from_float(res);
+      }
+    }
+    lds_barrier();
+  }
+};
 
 // Grid kernel: one workgroup per work unit. The units at one token position
 // form a plane of num_seqs x num_kv_heads. Split-K planes run from the last
@@ -449,22 +484,31 @@ void paged_attention_kernel(const KParams p) {
     }
     return;
   }
-  attention_unit<E, D, SPLIT, BS16, ALIGN, NW>(p, kv_head, seq, start, unit_tokens, seq_len, start / kPart, sm, [] {});
+  UnitEngine<E, D, SPLIT, BS16, ALIGN, NW> eng(p, sm);
+  const Unit u = make_unit(kv_head, seq, start, unit_tokens, seq_len, start / kPart);
+  const int bt = eng.load_bt(u);
+  eng.load_q(u);
+  eng.prologue(u, bt);
+  eng.run_tiles(u, bt);
+  eng.merge(u);
 }
 
 // Persistent split-K kernel: a resident-sized grid pulls work units from a
-// counter, so no workgroup is launched for a slot past a sequence's end (at
+// list, so no workgroup is launched for a position past a sequence's end (at
 // mixed lengths most grid slots are such, and launching them costs the
-// dispatcher more than the work) and the last units are spread over all
-// workgroups. Every workgroup lists the live units itself from seq_lens:
-// the full units of all sequences first, then each sequence's shorter tail
-// unit, KV heads innermost; prefix sums in LDS map a unit index back to its
-// (sequence, slot) by binary search. The first rounds of full units (all the
-// same size) are dealt out in grid order; the rest go through an atomic
-// counter (zeroed before launch). The first counter claim is made when a
-// workgroup starts its last dealt unit, so the claims of all workgroups,
-// which would otherwise arrive together, are served while they work; later
-// claims are made as each unit's partial results are merged.
+// dispatcher more than the work), and each workgroup starts its next unit's
+// loads while it merges the current one (a unit's start is three dependent
+// round trips -- length, block table, first tiles -- which a grid workgroup
+// waits through every time).
+//
+// Every workgroup lists the live units itself from seq_lens, largest first:
+// the full 1024-token units at positions >= 1, then the shorter last units at
+// positions >= 1, then the two 512-token units covering each sequence's first
+// 1024 tokens (the same cut as the grid kernel, so the results are
+// bit-identical); KV heads innermost. Prefix sums in LDS map a unit index back
+// to its sequence by binary search. Whole rounds of full units are dealt out
+// by grid index (equal sizes, no contention); the rest come from an atomic
+// counter (zeroed before launch).
 constexpr int kMaxPersistSeqs = 2048;
 
 template <typename E, int D, bool BS16, int ALIGN, int NW>
@@ -472,25 +516,29 @@ __global__ __launch_bounds__(NW * kWave) __attribute__((amdgpu_waves_per_eu(attn
 void paged_attention_persistent_kernel(const KParams p) {
   constexpr int NT = NW * kWave;
   __shared__ UnitSmem<D, NW> sm;
-  __shared__ int pf[kMaxPersistSeqs + 1];  // full units of sequences 0 .. s-1
-  __shared__ int pr[kMaxPersistSeqs + 1];  // tail units of sequences 0 .. s-1
+  __shared__ int pf[kMaxPersistSeqs + 1];  // full units at positions >= 1 of sequences 0 .. s-1
+  __shared__ int pr[kMaxPersistSeqs + 1];  // last units at positions >= 1 (shorter than 1024 tokens)
+  __shared__ int ph[kMaxPersistSeqs + 1];  // 512-token units at position 0
   __shared__ long long scan[NT];
-  __shared__ int next_unit;
+  __shared__ int claimed[1];
   const int tid = threadIdx.x;
   const int S = p.num_seqs;
-  constexpr int T = kUnit;
-  const int max_tokens = p.max_partitions * kPart;  // tokens past the workspace are ignored, as in the grid path
+  const int max_tokens = p.max_partitions * kPart;  // tokens past the workspace are ignored
   auto clamped_len = [&](int s) { return min(max(p.seq_lens[s], 0), max_tokens); };
+  // (full, last, half) unit counts of one sequence, packed 32 | 16 | 16 bits.
+  auto counts = [](int len) {
+    const long long full = len / kUnit >= 1 ? len / kUnit - 1 : 0;
+    const long long last = (len > kUnit && len % kUnit != 0) ? 1 : 0;
+    const long long half = (len > 0 ? 1 : 0) + (len > kPart ? 1 : 0);
+    return (full << 32) + (last << 16) + half;
+  };
 
-  // Per-thread chunk of sequences -> block-wide exclusive scan of (full, tail) counts.
+  // Per-thread chunk of sequences -> block-wide exclusive scan of the counts.
   const int per = (S + NT - 1) / NT;
   const int s0 = min(tid * per, S);
   const int s1 = min(s0 + per, S);
   long long cnt = 0;
-  for (int s = s0; s < s1; ++s) {
-    const int len = clamped_len(s);
-    cnt += (static_cast<long long>(len / T) << 32) + (len % T != 0 ? 1 : 0);
-  }
+  for (int s = s0; s < s1; ++s) cnt += counts(clamped_len(s));
   scan[tid] = cnt;
   __syncthreads();
   for (int off = 1; off < NT; off <<= 1) {
@@ -502,19 +550,31 @@ void paged_attention_persistent_kernel(const KParams p) {
   long long run = scan[tid] - cnt;
   for (int s = s0; s < s1; ++s) {
     pf[s] = static_cast<int>(run >> 32);
-    pr[s] = static_cast<int>(run & 0xffffffff);
-    const int len = clamped_len(s);
-    run += (static_cast<long long>(len / T) << 32) + (len % T != 0 ? 1 : 0);
+    pr[s] = static_cast<int>((run >> 16) & 0xffff);
+    ph[s] = static_cast<int>(run & 0xffff);
+    run += counts(clamped_len(s));
   }
   if (tid == NT - 1) {
     pf[S] = static_cast<int>(scan[NT - 1] >> 32);
-    pr[S] = static_cast<int>(scan[NT - 1] & 0xffffffff);
+    pr[S] = static_cast<int>((scan[NT - 1] >> 16) & 0xffff);
+    ph[S] = static_cast<int>(scan[NT - 1] & 0xffff);
   }
   __syncthreads();
 
   const int hkv = p.num_kv_heads;
-  const int total_full = pf[S] * hkv;
-  const int total = total_full + pr[S] * hkv;
+  const int n_full = pf[S] * hkv;
+  const int n_last = pr[S] * hkv;
+  const int total = n_full + n_last + ph[S] * hkv;
+  const int G = gridDim.x;
+  const int w = blockIdx.x;
+  if (w >= total) return;
+  const int dealt_rounds = max(1, n_full / G);
+  const int dealt = min(total, dealt_rounds * G);
+  // Units past the dealt ones come from one counter: a claim's round trip
+  // takes microseconds under contention, so a workgroup must learn that the
+  // list is exhausted from a single claim.
+  auto claim_issue = [&]() { return static_cast<int>(atomicAdd(p.unit_counter, 1u)); };
+  auto claim_finish = [&](int k) { return min(dealt + k, total); };
   // Last s with a[s] <= j (a[0] = 0 <= j < a[S]).
   auto find = [&](const int* a, int j) {
     int lo = 0, hi = S;
@@ -525,36 +585,67 @@ void paged_attention_persistent_kernel(const KParams p) {
     }
     return lo;
   };
+  auto decode = [&](int idx) {
+    if (idx < n_full) {
+      const int j = idx / hkv;
+      const int s = find(pf, j);
+      const int pos = 1 + j - pf[s];
+      return make_unit(idx - j * hkv, s, pos * kUnit, kUnit, clamped_len(s), 2 * pos);
+    }
+    if (idx < n_full + n_last) {
+      const int v = idx - n_full;
+      const int s = find(pr, v / hkv);
+      const int len = clamped_len(s);
+      const int pos = len / kUnit;
+      return make_unit(v % hkv, s, pos * kUnit, kUnit, len, 2 * pos);
+    }
+    const int v = idx - n_full - n_last;
+    const int j = v / hkv;
+    const int s = find(ph, j);
+    const int k = j - ph[s];
+    return make_unit(v - j * hkv, s, k * kPart, kPart, clamped_len(s), k);
+  };
 
-  const int G = gridDim.x;
-  const int dealt_rounds = max(1, total_full / G);
-  const int dealt = min(total, dealt_rounds * G);
-  int u = blockIdx.x;
-  int round = 0;
-  while (u < total) {
-    const bool dealt_unit = round < dealt_rounds;
-    const bool last_dealt = round == dealt_rounds - 1;
-    if (last_dealt && tid == 0) {
-      next_unit = dealt < total ? dealt + static_cast<int>(atomicAdd(p.unit_counter, 1u)) : total;
+  UnitEngine<E, D, true, BS16, ALIGN, NW> eng(p, sm);
+  Unit cu = decode(w);
+  int cu_bt = eng.load_bt(cu);
+  eng.load_q(cu);
+  eng.prologue(cu, cu_bt);
+  for (int k = 0;; ++k) {
+    if (k + 1 < dealt_rounds) {
+      // Next unit known: its block-table entries load while this unit runs,
+      // its query and first tiles before this unit's merge.
+      const Unit nu = decode(w + (k + 1) * G);
+      const int nu_bt = eng.load_bt(nu);
+      eng.run_tiles(cu, cu_bt);
+      eng.load_q(nu);
+      eng.prologue(nu, nu_bt);
+      eng.merge(cu);
+      eng.reset();
+      cu = nu;
+      cu_bt = nu_bt;
+      continue;
     }
-    int kv_head, seq, part;
-    if (u < total_full) {
-      kv_head = u % hkv;
-      const int j = u / hkv;
-      seq = find(pf, j);
-      part = j - pf[seq];
-    } else {
-      const int v = u - total_full;
-      kv_head = v % hkv;
-      seq = find(pr, v / hkv);
-      part = clamped_len(seq) / T;
-    }
-    attention_unit<E, D, true, BS16, ALIGN, NW>(p, kv_head, seq, part * T, T, clamped_len(seq), 2 * part, sm, [&] {
-      if (!dealt_unit && tid == 0) next_unit = dealt + static_cast<int>(atomicAdd(p.unit_counter, 1u));
-    });
-    u = dealt_unit && !last_dealt ? u + G : next_unit;
-    ++round;
-    __syncthreads();
+    // Next unit from the counters. A claim completes in order with the loads
+    // issued before it, so waiting for any later load would wait for the
+    // claim's round trip too: thread 0 issues it after this unit's last tile,
+    // keeps the answer in a register through the merge (LDS only) and
+    // publishes it afterwards.
+    eng.run_tiles(cu, cu_bt);
+    int mine = 0;
+    if (tid == 0) mine = claim_issue();
+    eng.merge(cu);
+    eng.reset();
+    if (tid == 0) claimed[0] = claim_finish(mine);
+    lds_barrier();
+    const int next = claimed[0];
+    if (next >= total) break;
+    const Unit nu = decode(next);
+    const int nu_bt = eng.load_bt(nu);
+    eng.load_q(nu);
+    eng.prologue(nu, nu_bt);
+    cu = nu;
+    cu_bt = nu_bt;
   }
 }
 
@@ -723,13 +814,15 @@ template <typename E, int D, bool BS16>
 hipError_t launch_split(KParams kp, int num_kv_heads, int num_seqs, int align, hipStream_t stream) {
   const int64_t per_plane = static_cast<int64_t>(num_kv_heads) * num_seqs;
   const int64_t grid_units = per_plane * (kp.num_units + 1);  // 1024-token planes + two 512-token planes
-  // The persistent kernel pays a counter reset and a unit-list setup; it wins
-  // when the grid would be mostly slots past their sequence's end, i.e. many
-  // unit positions per sequence and a grid several times the resident workgroups.
+  // The persistent kernel pays a counter reset, a unit-list setup and a
+  // microseconds-long counter round trip per unit; it wins when the grid
+  // would be mostly positions past their sequence's end: many positions per
+  // sequence, enough sequences for their lengths to differ, and a grid several
+  // times the resident workgroups.
   const Schedule forced = forced_schedule();
   int resident = 0;
   if (num_seqs <= kMaxPersistSeqs && kp.unit_counter != nullptr && forced != Schedule::kGrid &&
-      (kp.num_units >= 8 || forced == Schedule::kPersistent)) {
+      ((kp.num_units >= 8 && num_seqs >= 16) || forced == Schedule::kPersistent)) {
     const hipError_t e = launch_aligned<E, D, true, BS16, true>(kp, 0, align, stream, &resident);
     if (e != hipSuccess) return e;
   }
@@ -850,10 +943,10 @@ extern "C" int dk_paged_attention_decode(const dk_paged_attn_params* a, int dtyp
   kp.num_seqs = a->num_seqs;
   kp.num_kv_heads = a->num_kv_heads;
   // The persistent split-K kernel's unit counter lives in the tmp_out row of
-  // slot 1 of (sequence 0, query head 0): that kernel's 1024-token units write
-  // results to even slots only and mark odd slots empty in exp_sums, so the
-  // row is neither written nor read as data (max_partitions >= 2 here).
-  kp.unit_counter = split ? reinterpret_cast<unsigned*>(a->tmp_out + head_dim) : nullptr;
+  // slot 3 of (sequence 0, query head 0): results go to slots 0, 1 and even
+  // slots >= 2, odd slots >= 3 are only ever marked empty in exp_sums, so the
+  // row is neither written nor read as data. Needs max_partitions >= 4.
+  kp.unit_counter = split && a->max_partitions >= 4 ? reinterpret_cast<unsigned*>(a->tmp_out + 3 * head_dim) : nullptr;
 
   const bool bs16 = a->block_size % kTile == 0;
   hipStream_t s = static_cast<hipStream_t>(stream);
