@@ -656,13 +656,19 @@ __global__ void zero_counter_kernel(unsigned* counter) {
 // Log-sum-exp merge of the 512-token slots of one (query head, sequence):
 //   M = max_p m_p,  w_p = s_p * exp(m_p - M),  out = sum_p w_p o_p / sum_p w_p
 // (reference: csrc/paged_attention.cuh:227-269). WPH waves per query head,
-// kReduceWaves waves per workgroup. The (m_p, s_p) pairs are uniform across a
+// max(4, WPH) waves per workgroup. The (m_p, s_p) pairs are uniform across a
 // wave (scalar loads) and each lane accumulates D/64 output columns; with
-// WPH > 1 the waves of a head take every WPH-th unit and merge through LDS.
-constexpr int kReduceWaves = 4;
+// WPH > 1 the waves of a head take every WPH-th slot and merge through LDS.
+// The op is latency-bound: WPH grows with the number of slots a head merges
+// (1 wave up to 8 entries, 4 up to 63, 16 beyond; measured).
+template <int WPH>
+constexpr int reduce_waves() {
+  return WPH > 4 ? WPH : 4;
+}
 
 template <typename E, int D, int WPH>
-__global__ __launch_bounds__(kReduceWaves * kWave) void paged_attention_reduce_kernel(const KParams p) {
+__global__ __launch_bounds__(reduce_waves<WPH>() * kWave) void paged_attention_reduce_kernel(const KParams p) {
+  constexpr int kReduceWaves = reduce_waves<WPH>();
   constexpr int C = D / kWave;  // columns per lane (1, 2 or 4)
   constexpr int HPW = kReduceWaves / WPH;  // heads per workgroup
   const int wave = static_cast<int>(threadIdx.x) / kWave;
@@ -845,13 +851,17 @@ hipError_t launch(const KParams& kp, int num_kv_heads, int num_seqs, bool split,
   hipError_t e = bs16 ? launch_split<E, D, true>(kp, num_kv_heads, num_seqs, align, stream)
                       : launch_split<E, D, false>(kp, num_kv_heads, num_seqs, align, stream);
   if (e != hipSuccess) return e;
-  const dim3 rblock(kReduceWaves * kWave);
-  if (kp.max_partitions <= 32) {
-    const dim3 rgrid((kp.num_q_heads + kReduceWaves - 1) / kReduceWaves, num_seqs);
-    hipLaunchKernelGGL((paged_attention_reduce_kernel<E, D, 1>), rgrid, rblock, 0, stream, kp);
+  // Slot entries a head merges at most: slots 0, 1 and the even slots.
+  const int entries = 2 + (kp.max_partitions - 1) / 2;
+  if (entries <= 8) {
+    const dim3 rgrid((kp.num_q_heads + 3) / 4, num_seqs);
+    hipLaunchKernelGGL((paged_attention_reduce_kernel<E, D, 1>), rgrid, dim3(4 * kWave), 0, stream, kp);
+  } else if (entries < 64) {
+    hipLaunchKernelGGL((paged_attention_reduce_kernel<E, D, 4>), dim3(kp.num_q_heads, num_seqs), dim3(4 * kWave), 0,
+                       stream, kp);
   } else {
-    const dim3 rgrid(kp.num_q_heads, num_seqs);
-    hipLaunchKernelGGL((paged_attention_reduce_kernel<E, D, kReduceWaves>), rgrid, rblock, 0, stream, kp);
+    hipLaunchKernelGGL((paged_attention_reduce_kernel<E, D, 16>), dim3(kp.num_q_heads, num_seqs), dim3(16 * kWave), 0,
+                       stream, kp);
   }
   return hipGetLastError();
 }
