@@ -241,7 +241,7 @@ def layer_step(num_seqs, hq, hkv, d, bs, seq_lens, dtype, layout, seed, hidden=4
     part of it. Returns the per-op callables and the bytes the step must move."""
     g = torch.Generator(device="cuda").manual_seed(seed)
     kw = dict(device="cuda", dtype=dtype)
-    nqkv = (hq + 2 * hkv) * d
+    nqkv = 6144  # Llama-3-8B's fused q|k|v projection; q is its first hq * d columns
     w_qkv = torch.randn(nqkv, hidden, generator=g, **kw) * 0.02
     w_o = torch.randn(hidden, hq * d, generator=g, **kw) * 0.02
     w_gu = torch.randn(2 * inter, hidden, generator=g, **kw) * 0.02
@@ -281,8 +281,9 @@ def extras_layer_step() -> dict:
     """The single-layer decode step timed end to end, eager
     (back to back) and as one captured HIP graph replayed back to back, next to
     the sum of its ops timed one by one from cold caches. Hidden 4096 and MLP
-    14336 as Llama-3-8B; attention at the head-dim-256 / group-8 stress shape
-    (256 seqs, qkv N = 5120) and at the Llama-3-8B batch-64 shape."""
+    14336 and the projections as Llama-3-8B (qkv N = 6144); attention at the
+    head-dim-256 / group-8 stress shape (256 seqs) and at the Llama-3-8B
+    batch-64 shape."""
     res = {}
     cases = (
         ("d256_g8_b256_bf16", (256, 16, 2, 256, 32, c5_seq_lens(), torch.bfloat16, "nhd")),
