@@ -21,7 +21,7 @@ sample before anything is reported.
 batch 1 and 4, HND cache, 1% outlier rows), the head-dim-256 / group-8 stress
 batch, gemm_tn at the decode-layer shapes next to hipBLASLt (``F.linear``),
 the norm / activation ops, and one Llama-3-8B decoder layer's decode step
-end to end (eager and HIP graph) -- each op timed as the median of cold-cache calls
+end to end, RoPE and the cache write included (eager and HIP graph) -- each op timed as the median of cold-cache calls
 (a 1 GiB buffer is read before every call, 4x the 256 MB Infinity
 Cache).
 """
@@ -95,6 +95,13 @@ def attention_case(num_seqs, hq, hkv, d, bs, seq_lens, dtype, layout, seed, q_sc
         dk.paged_attention_decode(q, k, v, bt, lens, max_seq_len=max_len, out=out, workspace=ws)
 
     return dict(q=q, k=k, v=v, bt=bt, lens=lens, out=out, run=run, bytes=nbytes, seq_lens=seq_lens, dtype=dtype)
+
+
+def rope_table(max_position, rot_dim, base=500000.0):
+    """[max_position, rot_dim] float32 cos | sin table, theta_i = base^(-2i / rot_dim)."""
+    inv_freq = base ** (-torch.arange(0, rot_dim, 2, dtype=torch.float64, device="cuda") / rot_dim)
+    ang = torch.arange(max_position, dtype=torch.float64, device="cuda")[:, None] * inv_freq[None, :]
+    return torch.cat([ang.cos(), ang.sin()], dim=1).float()
 
 
 def llama3_8b_decode_case():
@@ -235,10 +242,12 @@ def c5_seq_lens(num_seqs: int = 256, seed: int = 5) -> list:
 
 def layer_step(num_seqs, hq, hkv, d, bs, seq_lens, dtype, layout, seed, hidden=4096, inter=14336):
     """One random-init decoder layer's decode step on this path: fused_add_rms_norm
-    -> qkv gemm -> paged attention (q read in place from the qkv output) -> o gemm
-    -> fused_add_rms_norm -> gate_up gemm -> silu_and_mul -> down gemm. Appending
-    the new token's K/V to the cache is the serving engine's job and is not
-    part of it. Returns the per-op callables and the bytes the step must move."""
+    -> qkv gemm -> rotary embedding of the q and k columns -> the new token's k
+    and v columns written to its cache slot -> paged attention (q read in place
+    from the qkv output) -> o gemm -> fused_add_rms_norm -> gate_up gemm ->
+    silu_and_mul -> down gemm. The new token is the last of each sequence
+    (position len - 1). Returns the per-op callables and the bytes the step
+    must move."""
     g = torch.Generator(device="cuda").manual_seed(seed)
     kw = dict(device="cuda", dtype=dtype)
     nqkv = 6144  # Llama-3-8B's fused q|k|v projection; q is its first hq * d columns
@@ -260,10 +269,18 @@ def layer_step(num_seqs, hq, hkv, d, bs, seq_lens, dtype, layout, seed, hidden=4
     max_len = max(max(seq_lens), 1)
     ws = dk.alloc_workspace(num_seqs, hq, d, max_len, "cuda")
     q = qkv[:, : hq * d].view(num_seqs, hq, d)
+    k_new, v_new = qkv[:, hq * d : (hq + hkv) * d], qkv[:, (hq + hkv) * d : (hq + 2 * hkv) * d]
+    rope = rope_table(max_len, d)
+    bt_host = case["bt"].cpu()
+    positions = torch.tensor([n - 1 for n in seq_lens], device="cuda")
+    slots = torch.tensor([int(bt_host[i, (n - 1) // bs]) * bs + (n - 1) % bs if n > 0 else -1
+                          for i, n in enumerate(seq_lens)], device="cuda")
     dko = torch.ops.decode_kernels
     ops = {
         "fused_add_rms_norm": lambda: dko.fused_add_rms_norm(x, resid, ln1, 1e-5),
         "qkv_gemm": lambda: dko.gemm_tn(qkv, x, w_qkv, None),
+        "rotary_embedding": lambda: dko.rotary_embedding(positions, qkv[:, : hq * d], k_new, d, rope, True),
+        "cache_write": lambda: dko.reshape_and_cache(k_new, v_new, case["k"], case["v"], slots),
         "attention": lambda: dk.paged_attention_decode(q, case["k"], case["v"], case["bt"], case["lens"],
                                                        max_seq_len=max_len, out=attn, workspace=ws),
         "o_gemm": lambda: dko.gemm_tn(o, attn.view(num_seqs, hq * d), w_o, None),
@@ -274,6 +291,7 @@ def layer_step(num_seqs, hq, hkv, d, bs, seq_lens, dtype, layout, seed, hidden=4
     }
     elt = torch.finfo(dtype).bits // 8
     nbytes = case["bytes"] + elt * (w_qkv.numel() + w_o.numel() + w_gu.numel() + w_down.numel())
+    nbytes += num_seqs * (2 * (hq + hkv) * d * elt + d * 4 + 4 * hkv * d * elt)  # rope rows + table row, k/v copy
     return ops, nbytes
 
 

@@ -5,7 +5,9 @@
 
 Same public API as DecodeKernels' ``decode_kernels`` package
 (``decode_kernels/__init__.py:7-27``); the ops are registered under the same
-``torch.ops.decode_kernels.*`` names.
+``torch.ops.decode_kernels.*`` names. ``rotary_embedding`` and
+``reshape_and_cache`` add the two steps around attention that the reference
+leaves to vLLM (vLLM's signatures).
 """
 
 from .ops import (
@@ -18,7 +20,9 @@ from .ops import (
     is_available,
     num_partitions,
     paged_attention_decode,
+    reshape_and_cache,
     rms_norm,
+    rotary_embedding,
     silu_and_mul,
 )
 
@@ -32,7 +36,9 @@ __all__ = [
     "is_available",
     "num_partitions",
     "paged_attention_decode",
+    "reshape_and_cache",
     "rms_norm",
+    "rotary_embedding",
     "silu_and_mul",
 ]
 __version__ = "0.1.0"

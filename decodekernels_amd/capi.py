@@ -21,6 +21,7 @@ HEADER_PATH = Path(__file__).resolve().parent.parent / "include" / "decodekernel
 
 DK_FLOAT16 = 0
 DK_BFLOAT16 = 1
+DK_FLOAT32 = 2
 HIP_ERROR_INVALID_VALUE = 1
 
 
@@ -57,6 +58,57 @@ class PagedAttnParams(ctypes.Structure):
     ]
 
 
+class RotaryParams(ctypes.Structure):
+    """Mirror of ``dk_rotary_params``."""
+
+    _fields_ = [
+        ("positions", ctypes.c_void_p),
+        ("query", ctypes.c_void_p),
+        ("key", ctypes.c_void_p),
+        ("cos_sin_cache", ctypes.c_void_p),
+        ("q_stride_token", ctypes.c_int64),
+        ("q_stride_head", ctypes.c_int64),
+        ("k_stride_token", ctypes.c_int64),
+        ("k_stride_head", ctypes.c_int64),
+        ("cache_stride", ctypes.c_int64),
+        ("num_tokens", ctypes.c_int32),
+        ("num_q_heads", ctypes.c_int32),
+        ("num_kv_heads", ctypes.c_int32),
+        ("head_size", ctypes.c_int32),
+        ("rot_dim", ctypes.c_int32),
+        ("max_position", ctypes.c_int32),
+        ("is_neox", ctypes.c_int32),
+        ("cache_dtype", ctypes.c_int32),
+    ]
+
+
+class CacheWriteParams(ctypes.Structure):
+    """Mirror of ``dk_cache_write_params``."""
+
+    _fields_ = [
+        ("key", ctypes.c_void_p),
+        ("value", ctypes.c_void_p),
+        ("key_cache", ctypes.c_void_p),
+        ("value_cache", ctypes.c_void_p),
+        ("slot_mapping", ctypes.c_void_p),
+        ("k_stride_token", ctypes.c_int64),
+        ("k_stride_head", ctypes.c_int64),
+        ("v_stride_token", ctypes.c_int64),
+        ("v_stride_head", ctypes.c_int64),
+        ("kc_stride_block", ctypes.c_int64),
+        ("kc_stride_token", ctypes.c_int64),
+        ("kc_stride_head", ctypes.c_int64),
+        ("vc_stride_block", ctypes.c_int64),
+        ("vc_stride_token", ctypes.c_int64),
+        ("vc_stride_head", ctypes.c_int64),
+        ("num_tokens", ctypes.c_int32),
+        ("num_kv_heads", ctypes.c_int32),
+        ("head_size", ctypes.c_int32),
+        ("block_size", ctypes.c_int32),
+        ("num_blocks", ctypes.c_int32),
+    ]
+
+
 _LIB: ctypes.CDLL | None = None
 
 _SIGNATURES = {
@@ -84,6 +136,14 @@ _SIGNATURES = {
         ctypes.c_int,
         [ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int64, ctypes.c_int64]
         + [ctypes.c_void_p],
+    ),
+    "dk_rotary_embedding": (
+        ctypes.c_int,
+        [ctypes.POINTER(RotaryParams), ctypes.c_int, ctypes.c_void_p],
+    ),
+    "dk_reshape_and_cache": (
+        ctypes.c_int,
+        [ctypes.POINTER(CacheWriteParams), ctypes.c_int, ctypes.c_void_p],
     ),
     "dk_last_error": (ctypes.c_char_p, []),
     "dk_error_string": (ctypes.c_char_p, [ctypes.c_int]),
@@ -144,4 +204,52 @@ def attn_params(out, q, k_cache, v_cache, block_tables, seq_lens, scale, workspa
     p.num_kv_heads = k_cache.shape[2]
     p.block_size = k_cache.shape[1]
     p.scale = scale
+    return p
+
+
+def _token_head_strides(t, head_size):
+    if t.dim() == 2:
+        return t.stride(0), head_size
+    return t.stride(0), t.stride(1)
+
+
+def _heads(t, head_size):
+    return t.shape[1] // head_size if t.dim() == 2 else t.shape[1]
+
+
+def rotary_params(positions, query, key, head_size, cos_sin_cache, is_neox) -> RotaryParams:
+    """Fills ``dk_rotary_params`` from tensors; ``query`` / ``key`` are
+    [tokens, heads * head_size] or [tokens, heads, head_size]."""
+    p = RotaryParams()
+    p.positions, p.query = positions.data_ptr(), query.data_ptr()
+    p.q_stride_token, p.q_stride_head = _token_head_strides(query, head_size)
+    p.num_q_heads = _heads(query, head_size)
+    if key is not None:
+        p.key = key.data_ptr()
+        p.k_stride_token, p.k_stride_head = _token_head_strides(key, head_size)
+        p.num_kv_heads = _heads(key, head_size)
+    p.cos_sin_cache = cos_sin_cache.data_ptr()
+    p.cache_stride = cos_sin_cache.stride(0)
+    p.num_tokens = positions.numel()
+    p.head_size = head_size
+    p.max_position, p.rot_dim = cos_sin_cache.shape
+    p.is_neox = int(bool(is_neox))
+    p.cache_dtype = DK_FLOAT32 if cos_sin_cache.dtype == torch.float32 else dtype_code(cos_sin_cache.dtype)
+    return p
+
+
+def cache_write_params(key, value, key_cache, value_cache, slot_mapping) -> CacheWriteParams:
+    """Fills ``dk_cache_write_params`` from tensors; the caches are
+    [blocks, block_size, kv_heads, head_size] views."""
+    p = CacheWriteParams()
+    d = key_cache.shape[3]
+    p.key, p.value = key.data_ptr(), value.data_ptr()
+    p.key_cache, p.value_cache = key_cache.data_ptr(), value_cache.data_ptr()
+    p.slot_mapping = slot_mapping.data_ptr()
+    p.k_stride_token, p.k_stride_head = _token_head_strides(key, d)
+    p.v_stride_token, p.v_stride_head = _token_head_strides(value, d)
+    p.kc_stride_block, p.kc_stride_token, p.kc_stride_head = key_cache.stride()[:3]
+    p.vc_stride_block, p.vc_stride_token, p.vc_stride_head = value_cache.stride()[:3]
+    p.num_tokens = slot_mapping.numel()
+    p.num_blocks, p.block_size, p.num_kv_heads, p.head_size = key_cache.shape
     return p

@@ -1,0 +1,280 @@
+// The two steps of a decode layer on either side of paged attention that
+// DecodeKernels leaves to the serving engine (vLLM runs them as its own ops):
+//
+//   rotary_embedding: rotates q and k in place by the token's position,
+//     pairs (x, y) -> (x cos - y sin, y cos + x sin) with cos / sin from a
+//     [max_position, rot_dim] table (cos in the first rot_dim / 2 columns);
+//     NeoX pairing takes x = v[i], y = v[i + rot_dim / 2], GPT-J pairing
+//     x = v[2i], y = v[2i + 1]; columns past rot_dim are left as they are.
+//     fp32 arithmetic with every product and sum rounded on its own (no
+//     fused multiply-add), one rounding to the model dtype per output.
+//   reshape_and_cache: writes each new token's K and V rows into its paged
+//     cache slot (slot_mapping[t] = block * block_size + offset; negative
+//     slots are padding and skipped). The caches are addressed by (block,
+//     token, head) strides exactly as paged_attention_decode reads them, so
+//     NHD, HND and vLLM's interleaved K|V buffers all work.
+//
+// Both are HBM-bound copies with a little arithmetic: one workgroup per
+// token, 16-byte (or 8-byte) vectors where the layout allows, a scalar path
+// otherwise. Positions outside the table and slots outside the cache are
+// skipped rather than read or written out of bounds.
+#include "../../include/decodekernels_amd.h"
+#include "dk_device.h"
+#include "dk_host.h"
+
+namespace dk {
+namespace rope {
+
+constexpr int kThreads = 256;
+
+struct KParams {
+  const int64_t* positions;
+  uint16_t* q;
+  uint16_t* k;
+  const void* cache;
+  int64_t q_st, q_sh, k_st, k_sh, cache_stride;
+  int num_tokens, hq, hkv, rot_dim, max_position;
+};
+
+// Element loader for a cache stored in the model dtype E.
+template <typename E, typename CT>
+__device__ __forceinline__ float table(const void* base, int64_t idx) {
+  if constexpr (sizeof(CT) == 4) {
+    return static_cast<const float*>(base)[idx];
+  } else {
+    return E::to_float(static_cast<const uint16_t*>(base)[idx]);
+  }
+}
+
+// One rotated pair with each product and the sum rounded to fp32 on its own
+// (no fused multiply-add): the same roundings as evaluating the two formulas
+// term by term, so the result does not depend on what the compiler fuses.
+__device__ __forceinline__ void rotate(float x, float y, float c, float s, float& ox, float& oy) {
+#pragma clang fp contract(off)
+  ox = x * c - y * s;
+  oy = y * c + x * s;
+}
+
+// VW pairs per thread step: 4 with vector loads (8 bytes per half for NeoX,
+// 16 bytes for GPT-J), 1 on the scalar path.
+template <typename E, typename CT, bool NEOX, int VW>
+__global__ __launch_bounds__(kThreads) void rotary_kernel(const KParams p) {
+  const int t = blockIdx.x;
+  const int64_t pos = p.positions[t];
+  if (pos < 0 || pos >= p.max_position) return;
+  const int half = p.rot_dim / 2;
+  const int64_t crow = pos * p.cache_stride;
+  const int steps = half / VW;  // per head
+  const int total = (p.hq + p.hkv) * steps;
+  for (int c = threadIdx.x; c < total; c += kThreads) {
+    const int h = c / steps;
+    const int i0 = (c - h * steps) * VW;
+    uint16_t* v = h < p.hq ? p.q + t * p.q_st + h * p.q_sh : p.k + t * p.k_st + (h - p.hq) * p.k_sh;
+    float x[VW], y[VW], cs[VW], sn[VW];
+#pragma unroll
+    for (int j = 0; j < VW; ++j) {
+      cs[j] = table<E, CT>(p.cache, crow + i0 + j);
+      sn[j] = table<E, CT>(p.cache, crow + half + i0 + j);
+    }
+    if constexpr (NEOX) {
+      if constexpr (VW == 4) {
+        const u32x2 a = *reinterpret_cast<const u32x2*>(v + i0);
+        const u32x2 b = *reinterpret_cast<const u32x2*>(v + half + i0);
+        x[0] = E::lo(a[0]), x[1] = E::hi(a[0]), x[2] = E::lo(a[1]), x[3] = E::hi(a[1]);
+        y[0] = E::lo(b[0]), y[1] = E::hi(b[0]), y[2] = E::lo(b[1]), y[3] = E::hi(b[1]);
+      } else {
+        x[0] = E::to_float(v[i0]);
+        y[0] = E::to_float(v[half + i0]);
+      }
+    } else {
+      if constexpr (VW == 4) {
+        const u32x4 a = *reinterpret_cast<const u32x4*>(v + 2 * i0);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) x[j] = E::lo(a[j]), y[j] = E::hi(a[j]);
+      } else {
+        x[0] = E::to_float(v[2 * i0]);
+        y[0] = E::to_float(v[2 * i0 + 1]);
+      }
+    }
+    float ox[VW], oy[VW];
+#pragma unroll
+    for (int j = 0; j < VW; ++j) rotate(x[j], y[j], cs[j], sn[j], ox[j], oy[j]);
+    if constexpr (NEOX) {
+      if constexpr (VW == 4) {
+        *reinterpret_cast<u32x2*>(v + i0) = u32x2{pack2<E>(ox[0], ox[1]), pack2<E>(ox[2], ox[3])};
+        *reinterpret_cast<u32x2*>(v + half + i0) = u32x2{pack2<E>(oy[0], oy[1]), pack2<E>(oy[2], oy[3])};
+      } else {
+        v[i0] = E::from_float(ox[0]);
+        v[half + i0] = E::from_float(oy[0]);
+      }
+    } else {
+      if constexpr (VW == 4) {
+        u32x4 o;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) o[j] = pack2<E>(ox[j], oy[j]);
+        *reinterpret_cast<u32x4*>(v + 2 * i0) = o;
+      } else {
+        v[2 * i0] = E::from_float(ox[0]);
+        v[2 * i0 + 1] = E::from_float(oy[0]);
+      }
+    }
+  }
+}
+
+template <typename E, typename CT>
+hipError_t launch_rotary(const KParams& kp, bool neox, bool vec, hipStream_t s) {
+  const dim3 grid(kp.num_tokens), block(kThreads);
+  if (neox) {
+    if (vec) hipLaunchKernelGGL((rotary_kernel<E, CT, true, 4>), grid, block, 0, s, kp);
+    else hipLaunchKernelGGL((rotary_kernel<E, CT, true, 1>), grid, block, 0, s, kp);
+  } else {
+    if (vec) hipLaunchKernelGGL((rotary_kernel<E, CT, false, 4>), grid, block, 0, s, kp);
+    else hipLaunchKernelGGL((rotary_kernel<E, CT, false, 1>), grid, block, 0, s, kp);
+  }
+  return hipGetLastError();
+}
+
+}  // namespace rope
+
+namespace cache {
+
+constexpr int kThreads = 256;
+
+struct KParams {
+  const uint16_t* key;
+  const uint16_t* value;
+  uint16_t* kc;
+  uint16_t* vc;
+  const int64_t* slots;
+  int64_t k_st, k_sh, v_st, v_sh;
+  int64_t kc_sb, kc_st, kc_sh, vc_sb, vc_st, vc_sh;
+  int num_tokens, hkv, d, block_size, num_blocks;
+};
+
+// VEC elements per copy: 8 (16-byte vectors) or 1.
+template <int VEC>
+__global__ __launch_bounds__(kThreads) void reshape_and_cache_kernel(const KParams p) {
+  const int t = blockIdx.x;
+  const int64_t slot = p.slots[t];
+  if (slot < 0) return;
+  const int64_t blk = slot / p.block_size;
+  const int64_t off = slot - blk * p.block_size;
+  if (blk >= p.num_blocks) return;
+  const int per_head = p.d / VEC;
+  const int n = p.hkv * per_head;
+  for (int c = threadIdx.x; c < 2 * n; c += kThreads) {
+    const bool is_v = c >= n;
+    const int cc = is_v ? c - n : c;
+    const int h = cc / per_head;
+    const int d0 = (cc - h * per_head) * VEC;
+    const uint16_t* src = is_v ? p.value + t * p.v_st + h * p.v_sh + d0 : p.key + t * p.k_st + h * p.k_sh + d0;
+    uint16_t* dst = is_v ? p.vc + blk * p.vc_sb + off * p.vc_st + h * p.vc_sh + d0
+                         : p.kc + blk * p.kc_sb + off * p.kc_st + h * p.kc_sh + d0;
+    if constexpr (VEC == 8) {
+      *reinterpret_cast<u32x4*>(dst) = *reinterpret_cast<const u32x4*>(src);
+    } else {
+      *dst = *src;
+    }
+  }
+}
+
+}  // namespace cache
+}  // namespace dk
+
+extern "C" int dk_rotary_embedding(const dk_rotary_params* a, int dtype, void* stream) {
+  using namespace dk;
+  clear_error();
+  if (a == nullptr) return fail("rotary_embedding: params must not be NULL");
+  if (dtype != DK_FLOAT16 && dtype != DK_BFLOAT16)
+    return fail("rotary_embedding: expected float16 or bfloat16, got dtype code %d", dtype);
+  if (a->cache_dtype != dtype && a->cache_dtype != DK_FLOAT32)
+    return fail("rotary_embedding: cos_sin_cache must be float32 or the query dtype");
+  if (a->num_tokens < 0 || a->num_q_heads < 0 || a->num_kv_heads < 0)
+    return fail("rotary_embedding: sizes must be non-negative");
+  if (a->num_tokens == 0) return hipSuccess;
+  if (a->rot_dim <= 0 || a->rot_dim % 2 != 0 || a->rot_dim > a->head_size)
+    return fail("rotary_embedding: rot_dim must be even and at most head_size");
+  if (a->positions == nullptr || a->query == nullptr || a->cos_sin_cache == nullptr)
+    return fail("rotary_embedding: positions, query and cos_sin_cache must not be NULL");
+  if (a->num_tokens > 0x7fffffff / 2) return fail("rotary_embedding: too many tokens");
+  rope::KParams kp{};
+  kp.positions = a->positions;
+  kp.q = static_cast<uint16_t*>(a->query);
+  kp.k = static_cast<uint16_t*>(a->key);
+  kp.cache = a->cos_sin_cache;
+  kp.q_st = a->q_stride_token;
+  kp.q_sh = a->q_stride_head;
+  kp.k_st = a->k_stride_token;
+  kp.k_sh = a->k_stride_head;
+  kp.cache_stride = a->cache_stride;
+  kp.num_tokens = a->num_tokens;
+  kp.hq = a->num_q_heads;
+  kp.hkv = a->key != nullptr ? a->num_kv_heads : 0;
+  kp.rot_dim = a->rot_dim;
+  kp.max_position = a->max_position;
+  const bool neox = a->is_neox != 0;
+  // Vector path: 4 pairs per step, every row start aligned to the vector.
+  const int half = a->rot_dim / 2;
+  const int vbytes = neox ? 8 : 16;
+  const int velems = vbytes / 2;
+  bool vec = half % 4 == 0 && aligned_to(a->query, vbytes) && a->q_stride_token % velems == 0 &&
+             a->q_stride_head % velems == 0 && (!neox || half % velems == 0);
+  if (kp.hkv > 0)
+    vec = vec && aligned_to(a->key, vbytes) && a->k_stride_token % velems == 0 && a->k_stride_head % velems == 0;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  hipError_t e;
+  if (a->cache_dtype == DK_FLOAT32) {
+    e = dtype == DK_BFLOAT16 ? rope::launch_rotary<Bf16, float>(kp, neox, vec, s)
+                             : rope::launch_rotary<F16, float>(kp, neox, vec, s);
+  } else {
+    e = dtype == DK_BFLOAT16 ? rope::launch_rotary<Bf16, uint16_t>(kp, neox, vec, s)
+                             : rope::launch_rotary<F16, uint16_t>(kp, neox, vec, s);
+  }
+  return static_cast<int>(e);
+}
+
+extern "C" int dk_reshape_and_cache(const dk_cache_write_params* a, int dtype, void* stream) {
+  using namespace dk;
+  clear_error();
+  if (a == nullptr) return fail("reshape_and_cache: params must not be NULL");
+  if (dtype != DK_FLOAT16 && dtype != DK_BFLOAT16)
+    return fail("reshape_and_cache: expected float16 or bfloat16, got dtype code %d", dtype);
+  if (a->num_tokens < 0 || a->num_kv_heads <= 0 || a->head_size <= 0 || a->block_size <= 0 || a->num_blocks < 0)
+    return fail("reshape_and_cache: sizes must be positive");
+  if (a->num_tokens == 0) return hipSuccess;
+  if (a->key == nullptr || a->value == nullptr || a->key_cache == nullptr || a->value_cache == nullptr ||
+      a->slot_mapping == nullptr)
+    return fail("reshape_and_cache: pointers must not be NULL");
+  cache::KParams kp{};
+  kp.key = static_cast<const uint16_t*>(a->key);
+  kp.value = static_cast<const uint16_t*>(a->value);
+  kp.kc = static_cast<uint16_t*>(a->key_cache);
+  kp.vc = static_cast<uint16_t*>(a->value_cache);
+  kp.slots = a->slot_mapping;
+  kp.k_st = a->k_stride_token;
+  kp.k_sh = a->k_stride_head;
+  kp.v_st = a->v_stride_token;
+  kp.v_sh = a->v_stride_head;
+  kp.kc_sb = a->kc_stride_block;
+  kp.kc_st = a->kc_stride_token;
+  kp.kc_sh = a->kc_stride_head;
+  kp.vc_sb = a->vc_stride_block;
+  kp.vc_st = a->vc_stride_token;
+  kp.vc_sh = a->vc_stride_head;
+  kp.num_tokens = a->num_tokens;
+  kp.hkv = a->num_kv_heads;
+  kp.d = a->head_size;
+  kp.block_size = a->block_size;
+  kp.num_blocks = a->num_blocks;
+  const bool vec = a->head_size % 8 == 0 && aligned_to(a->key, 16) && aligned_to(a->value, 16) &&
+                   aligned_to(a->key_cache, 16) && aligned_to(a->value_cache, 16) &&
+                   a->k_stride_token % 8 == 0 && a->k_stride_head % 8 == 0 && a->v_stride_token % 8 == 0 &&
+                   a->v_stride_head % 8 == 0 && a->kc_stride_block % 8 == 0 && a->kc_stride_token % 8 == 0 &&
+                   a->kc_stride_head % 8 == 0 && a->vc_stride_block % 8 == 0 && a->vc_stride_token % 8 == 0 &&
+                   a->vc_stride_head % 8 == 0;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const dim3 grid(a->num_tokens), block(cache::kThreads);
+  if (vec) hipLaunchKernelGGL((cache::reshape_and_cache_kernel<8>), grid, block, 0, s, kp);
+  else hipLaunchKernelGGL((cache::reshape_and_cache_kernel<1>), grid, block, 0, s, kp);
+  return static_cast<int>(hipGetLastError());
+}

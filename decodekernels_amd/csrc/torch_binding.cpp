@@ -3,7 +3,9 @@
 // The five schemas, the dispatch key (CUDA, which is where PyTorch-ROCm puts
 // HIP tensors) and the argument-check messages are DecodeKernels' interface
 // (csrc/ops.cu:44-286), kept identical so callers and tests written against
-// the reference see the same ops and the same errors. Each impl checks tensor
+// the reference see the same ops and the same errors. Two more ops,
+// rotary_embedding and reshape_and_cache, cover the steps around attention
+// that the reference leaves to vLLM, with vLLM's schemas. Each impl checks tensor
 // metadata, fills the C-ABI arguments and enqueues the HIP kernels on the
 // current stream of the input's device; nothing here allocates memory, so the
 // ops can be captured in a graph.
@@ -19,6 +21,8 @@
 
 #include <algorithm>
 #include <optional>
+#include <tuple>
+#include <utility>
 
 #include "decodekernels_amd.h"
 
@@ -249,6 +253,117 @@ void silu_and_mul(at::Tensor& out, const at::Tensor& input) {
 }
 
 // ---------------------------------------------------------------------------
+// rotary_embedding / reshape_and_cache: the steps either side of attention
+// that DecodeKernels leaves to the serving engine; the schemas are vLLM's ops
+// of the same names (query / key as [tokens, heads * head_size] or
+// [tokens, heads, head_size]; caches as the [blocks, block_size, kv_heads,
+// head_size] views paged_attention_decode takes).
+// ---------------------------------------------------------------------------
+namespace {
+
+// (token stride, head stride) of a [T, H * D] or [T, H, D] tensor.
+std::pair<int64_t, int64_t> token_head_strides(const at::Tensor& t, int64_t head_size, const char* name) {
+  TORCH_CHECK(t.stride(-1) == 1, name, ": last dimension must be contiguous");
+  if (t.dim() == 2) {
+    TORCH_CHECK(t.size(1) % head_size == 0, name, ": last dimension must be a multiple of head_size");
+    return {t.stride(0), head_size};
+  }
+  TORCH_CHECK(t.dim() == 3 && t.size(2) == head_size, name, ": expected [tokens, heads * head_size] or [tokens, heads, head_size]");
+  return {t.stride(0), t.stride(1)};
+}
+
+int64_t heads_of(const at::Tensor& t, int64_t head_size) { return t.dim() == 2 ? t.size(1) / head_size : t.size(1); }
+
+}  // namespace
+
+void rotary_embedding(const at::Tensor& positions, at::Tensor& query, const std::optional<at::Tensor>& key,
+                      int64_t head_size, const at::Tensor& cos_sin_cache, bool is_neox) {
+  TORCH_CHECK(query.is_cuda(), "rotary_embedding: query must be on CUDA");
+  TORCH_CHECK(positions.scalar_type() == at::ScalarType::Long && positions.is_contiguous(),
+              "rotary_embedding: positions must be contiguous int64");
+  TORCH_CHECK(head_size > 0, "rotary_embedding: head_size must be positive");
+  const int64_t T = positions.numel();
+  TORCH_CHECK(query.size(0) == T, "rotary_embedding: query must have one row per position");
+  TORCH_CHECK(cos_sin_cache.dim() == 2 && cos_sin_cache.stride(1) == 1,
+              "rotary_embedding: cos_sin_cache must be [max_position, rot_dim] with contiguous rows");
+  TORCH_CHECK(cos_sin_cache.device() == query.device() && positions.device() == query.device(),
+              "rotary_embedding: tensors must be on the same device");
+  const int dt = dtype_code(query.scalar_type(), "rotary_embedding");
+  int cache_dt;
+  if (cos_sin_cache.scalar_type() == at::ScalarType::Float) {
+    cache_dt = DK_FLOAT32;
+  } else {
+    TORCH_CHECK(cos_sin_cache.scalar_type() == query.scalar_type(),
+                "rotary_embedding: cos_sin_cache must be float32 or the query dtype");
+    cache_dt = dt;
+  }
+  dk_rotary_params p{};
+  p.positions = positions.data_ptr<int64_t>();
+  p.query = query.data_ptr();
+  std::tie(p.q_stride_token, p.q_stride_head) = token_head_strides(query, head_size, "rotary_embedding(query)");
+  p.num_q_heads = static_cast<int32_t>(heads_of(query, head_size));
+  if (key.has_value()) {
+    check_same(query, *key, "query/key");
+    TORCH_CHECK(key->size(0) == T, "rotary_embedding: key must have one row per position");
+    p.key = key->data_ptr();
+    std::tie(p.k_stride_token, p.k_stride_head) = token_head_strides(*key, head_size, "rotary_embedding(key)");
+    p.num_kv_heads = static_cast<int32_t>(heads_of(*key, head_size));
+  }
+  p.cos_sin_cache = cos_sin_cache.data_ptr();
+  p.cache_stride = cos_sin_cache.stride(0);
+  p.num_tokens = static_cast<int32_t>(T);
+  p.head_size = static_cast<int32_t>(head_size);
+  p.rot_dim = static_cast<int32_t>(cos_sin_cache.size(1));
+  p.max_position = static_cast<int32_t>(cos_sin_cache.size(0));
+  p.is_neox = is_neox ? 1 : 0;
+  p.cache_dtype = cache_dt;
+  const DeviceGuard guard(query.device());
+  check_status(dk_rotary_embedding(&p, dt, stream_of(query)), "rotary_embedding");
+}
+
+void reshape_and_cache(const at::Tensor& key, const at::Tensor& value, at::Tensor& key_cache, at::Tensor& value_cache,
+                       const at::Tensor& slot_mapping) {
+  TORCH_CHECK(key.is_cuda(), "reshape_and_cache: key must be on CUDA");
+  check_same(key, value, "key/value");
+  check_same(key, key_cache, "key/key_cache");
+  check_same(key, value_cache, "key/value_cache");
+  TORCH_CHECK(slot_mapping.scalar_type() == at::ScalarType::Long && slot_mapping.is_contiguous() &&
+                  slot_mapping.device() == key.device(),
+              "reshape_and_cache: slot_mapping must be contiguous int64 on the key's device");
+  TORCH_CHECK(key_cache.dim() == 4 && value_cache.dim() == 4 && key_cache.sizes() == value_cache.sizes() &&
+                  key_cache.stride(3) == 1 && value_cache.stride(3) == 1,
+              "reshape_and_cache: caches must be [num_blocks, block_size, num_kv_heads, head_size] views with "
+              "contiguous head_size");
+  const int64_t D = key_cache.size(3);
+  const int64_t T = slot_mapping.numel();
+  TORCH_CHECK(key.size(0) == T && value.size(0) == T, "reshape_and_cache: one key / value row per slot");
+  TORCH_CHECK(heads_of(key, D) == key_cache.size(2) && heads_of(value, D) == key_cache.size(2),
+              "reshape_and_cache: key / value heads must match the cache");
+  dk_cache_write_params p{};
+  p.key = key.data_ptr();
+  p.value = value.data_ptr();
+  p.key_cache = key_cache.data_ptr();
+  p.value_cache = value_cache.data_ptr();
+  p.slot_mapping = slot_mapping.data_ptr<int64_t>();
+  std::tie(p.k_stride_token, p.k_stride_head) = token_head_strides(key, D, "reshape_and_cache(key)");
+  std::tie(p.v_stride_token, p.v_stride_head) = token_head_strides(value, D, "reshape_and_cache(value)");
+  p.kc_stride_block = key_cache.stride(0);
+  p.kc_stride_token = key_cache.stride(1);
+  p.kc_stride_head = key_cache.stride(2);
+  p.vc_stride_block = value_cache.stride(0);
+  p.vc_stride_token = value_cache.stride(1);
+  p.vc_stride_head = value_cache.stride(2);
+  p.num_tokens = static_cast<int32_t>(T);
+  p.num_kv_heads = static_cast<int32_t>(key_cache.size(2));
+  p.head_size = static_cast<int32_t>(D);
+  p.block_size = static_cast<int32_t>(key_cache.size(1));
+  p.num_blocks = static_cast<int32_t>(key_cache.size(0));
+  const int dt = dtype_code(key.scalar_type(), "reshape_and_cache");
+  const DeviceGuard guard(key.device());
+  check_status(dk_reshape_and_cache(&p, dt, stream_of(key)), "reshape_and_cache");
+}
+
+// ---------------------------------------------------------------------------
 // Registration (csrc/ops.cu:270-286)
 // ---------------------------------------------------------------------------
 TORCH_LIBRARY(decode_kernels, m) {
@@ -259,6 +374,10 @@ TORCH_LIBRARY(decode_kernels, m) {
   m.def("rms_norm(Tensor! out, Tensor input, Tensor weight, float eps) -> ()");
   m.def("fused_add_rms_norm(Tensor! input, Tensor! residual, Tensor weight, float eps) -> ()");
   m.def("silu_and_mul(Tensor! out, Tensor input) -> ()");
+  m.def(
+      "rotary_embedding(Tensor positions, Tensor! query, Tensor!? key, int head_size, Tensor cos_sin_cache, "
+      "bool is_neox) -> ()");
+  m.def("reshape_and_cache(Tensor key, Tensor value, Tensor! key_cache, Tensor! value_cache, Tensor slot_mapping) -> ()");
 }
 
 TORCH_LIBRARY_IMPL(decode_kernels, CUDA, m) {
@@ -267,6 +386,8 @@ TORCH_LIBRARY_IMPL(decode_kernels, CUDA, m) {
   m.impl("rms_norm", &rms_norm);
   m.impl("fused_add_rms_norm", &fused_add_rms_norm);
   m.impl("silu_and_mul", &silu_and_mul);
+  m.impl("rotary_embedding", &rotary_embedding);
+  m.impl("reshape_and_cache", &reshape_and_cache);
 }
 
 // Python module entry point: an empty module; importing it loads this

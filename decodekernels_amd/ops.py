@@ -64,6 +64,14 @@ if _AVAILABLE:
     def _(out, input):
         return None
 
+    @torch.library.register_fake("decode_kernels::rotary_embedding")
+    def _(positions, query, key, head_size, cos_sin_cache, is_neox):
+        return None
+
+    @torch.library.register_fake("decode_kernels::reshape_and_cache")
+    def _(key, value, key_cache, value_cache, slot_mapping):
+        return None
+
 
 # ---------------------------------------------------------------------------
 # Paged attention
@@ -167,3 +175,40 @@ def silu_and_mul(x: torch.Tensor, out: torch.Tensor | None = None):
         out = torch.empty(*x.shape[:-1], d, dtype=x.dtype, device=x.device)
     torch.ops.decode_kernels.silu_and_mul(out, x)
     return out
+
+
+# ---------------------------------------------------------------------------
+# The steps around attention (vLLM's ops of the same names; not part of
+# DecodeKernels, which leaves them to the serving engine)
+# ---------------------------------------------------------------------------
+def rotary_embedding(
+    positions: torch.Tensor,
+    query: torch.Tensor,
+    key: torch.Tensor | None,
+    head_size: int,
+    cos_sin_cache: torch.Tensor,
+    is_neox: bool = True,
+):
+    """In place: rotates the first ``cos_sin_cache.shape[1]`` columns of every
+    head of ``query`` (and ``key``) by the token's position. ``query`` /
+    ``key`` are [tokens, heads * head_size] or [tokens, heads, head_size];
+    ``cos_sin_cache`` is [max_position, rot_dim] (cos columns, then sin), in
+    float32 or the query dtype. Returns (query, key)."""
+    _require()
+    torch.ops.decode_kernels.rotary_embedding(positions, query, key, int(head_size), cos_sin_cache, bool(is_neox))
+    return query, key
+
+
+def reshape_and_cache(
+    key: torch.Tensor,
+    value: torch.Tensor,
+    key_cache: torch.Tensor,
+    value_cache: torch.Tensor,
+    slot_mapping: torch.Tensor,
+) -> None:
+    """Writes key[t] / value[t] ([tokens, kv_heads, head_size]) into cache slot
+    ``slot_mapping[t]`` (int64; negative = skip) of the
+    [num_blocks, block_size, kv_heads, head_size] cache views -- the same views
+    paged_attention_decode reads (NHD, HND or vLLM's interleaved buffer)."""
+    _require()
+    torch.ops.decode_kernels.reshape_and_cache(key, value, key_cache, value_cache, slot_mapping)

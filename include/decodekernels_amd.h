@@ -23,10 +23,12 @@
 extern "C" {
 #endif
 
-/* Element type of every 16-bit tensor argument. */
+/* Element type of every 16-bit tensor argument (DK_FLOAT32: the rotary
+ * cos / sin table only). */
 enum dk_dtype {
   DK_FLOAT16 = 0,
   DK_BFLOAT16 = 1,
+  DK_FLOAT32 = 2,
 };
 
 /* Tokens per split-K partition of the workspace contract (reference:
@@ -106,6 +108,62 @@ int dk_fused_add_rms_norm(int dtype, void* input, void* residual, const void* we
  */
 int dk_silu_and_mul(int dtype, void* out, const void* input, int rows, int d, int64_t in_stride, int64_t out_stride,
                     void* stream);
+
+/*
+ * Rotary position embedding, in place on q and k: for the first rot_dim
+ * columns of every head, pairs (x, y) <- (x cos - y sin, y cos + x sin) with
+ * cos = cos_sin_cache[position][i], sin = cos_sin_cache[position][rot_dim/2 + i];
+ * NeoX pairing x = v[i], y = v[i + rot_dim/2]; GPT-J pairing x = v[2i],
+ * y = v[2i + 1]. fp32 arithmetic, one rounding per output.
+ *   positions      [num_tokens] int64; a position outside [0, max_position)
+ *                  leaves its token unchanged
+ *   query          [num_tokens, num_q_heads, head_size], strides in elements
+ *   key            [num_tokens, num_kv_heads, head_size] or NULL
+ *   cos_sin_cache  [max_position, rot_dim], row stride cache_stride, float32
+ *                  (cache_dtype DK_FLOAT32) or the query dtype
+ * No counterpart in DecodeKernels, which leaves this step to the serving
+ * engine: it is vLLM's rotary_embedding op (positions, query, key, head_size,
+ * cos_sin_cache, is_neox), run before paged attention in every decode step.
+ */
+typedef struct dk_rotary_params {
+  const int64_t* positions;
+  void* query;
+  void* key;
+  const void* cos_sin_cache;
+  int64_t q_stride_token, q_stride_head;
+  int64_t k_stride_token, k_stride_head;
+  int64_t cache_stride;
+  int32_t num_tokens, num_q_heads, num_kv_heads, head_size, rot_dim, max_position, is_neox, cache_dtype;
+} dk_rotary_params;
+
+int dk_rotary_embedding(const dk_rotary_params* p, int dtype, void* stream);
+
+/*
+ * Writes new tokens' K and V rows into the paged cache:
+ *   key_cache[slot / block_size, slot % block_size, h, :] = key[t, h, :],
+ *   value_cache likewise, with slot = slot_mapping[t] (int64). Negative slots
+ *   (padding) and slots at or past num_blocks * block_size are skipped.
+ * key / value [num_tokens, num_kv_heads, head_size]; the caches use the
+ * (block, token, head) strides of dk_paged_attn_params, so NHD, HND and
+ * vLLM's interleaved K|V buffer all work. A bit-exact copy.
+ * No counterpart in DecodeKernels, which leaves this step to the serving
+ * engine: it is vLLM's reshape_and_cache_flash op, which fills the cache that
+ * paged attention then reads.
+ */
+typedef struct dk_cache_write_params {
+  const void* key;
+  const void* value;
+  void* key_cache;
+  void* value_cache;
+  const int64_t* slot_mapping;
+  int64_t k_stride_token, k_stride_head;
+  int64_t v_stride_token, v_stride_head;
+  int64_t kc_stride_block, kc_stride_token, kc_stride_head;
+  int64_t vc_stride_block, vc_stride_token, vc_stride_head;
+  int32_t num_tokens, num_kv_heads, head_size, block_size, num_blocks;
+} dk_cache_write_params;
+
+int dk_reshape_and_cache(const dk_cache_write_params* p, int dtype, void* stream);
 
 /* Description of the last argument error raised on this thread ("" if none).
  * The reference reports these through TORCH_CHECK messages (csrc/ops.cu). */

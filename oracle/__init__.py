@@ -12,6 +12,11 @@ imports it and has no CPU fallback: without the HIP libraries its ops raise.
   written from the definitions (softmax attention with GQA head mapping
   ``kv_head = q_head // group``, the log-sum-exp merge, ``A·Bᵀ``, RMSNorm,
   SiLU), used to pin ``oracle.reference``.
+* ``oracle.rope_cache`` -- rotary embedding and the paged cache write, the
+  two steps around attention that DecodeKernels leaves to vLLM, restated from
+  their published definitions; pinned in ``tests/test_oracle_rope_cache.py``
+  (complex-multiplication route, rotation invariants, ``index_put_`` scatter,
+  planted mistakes).
 
 Pins (see ``tests/test_oracle.py``): every function of ``oracle.reference`` is
 checked against ``oracle.brute`` and against a torch library routine or

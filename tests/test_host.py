@@ -21,6 +21,8 @@ def test_library_exports_every_declared_symbol():
         "dk_rms_norm",
         "dk_fused_add_rms_norm",
         "dk_silu_and_mul",
+        "dk_rotary_embedding",
+        "dk_reshape_and_cache",
         "dk_last_error",
         "dk_error_string",
         "dk_version",
@@ -37,6 +39,12 @@ def test_library_exports_every_declared_symbol():
 def test_params_struct_matches_header_layout():
     # 9 pointers, 11 int64 strides, 5 int32 and a float: 9*8 + 11*8 + 5*4 + 4 = 184 bytes.
     assert ctypes.sizeof(capi.PagedAttnParams) == 184
+    # 4 pointers, 5 int64 strides, 8 int32: 32 + 40 + 32 = 104 bytes.
+    assert ctypes.sizeof(capi.RotaryParams) == 104
+    # 5 pointers, 10 int64 strides, 5 int32 = 140, padded to 8: 144 bytes.
+    assert ctypes.sizeof(capi.CacheWriteParams) == 144
+    assert capi.RotaryParams.cache_dtype.offset == 100
+    assert capi.CacheWriteParams.num_blocks.offset == 136
 
 
 def _attn_params(num_q_heads=8, num_kv_heads=2, block_size=16, max_partitions=1):
@@ -116,6 +124,88 @@ def test_capi_norm_validation():
     assert capi.lib().dk_error_string(1)
 
 
+def _rotary_params(**kw):
+    p = capi.RotaryParams()
+    p.positions = p.query = p.key = p.cos_sin_cache = 0x10000  # never dereferenced
+    p.q_stride_token, p.q_stride_head = 4 * 128, 128
+    p.k_stride_token, p.k_stride_head = 2 * 128, 128
+    p.cache_stride = 128
+    p.num_tokens, p.num_q_heads, p.num_kv_heads, p.head_size = 3, 4, 2, 128
+    p.rot_dim, p.max_position, p.is_neox, p.cache_dtype = 128, 4096, 1, capi.DK_FLOAT32
+    for k, v in kw.items():
+        setattr(p, k, v)
+    return p
+
+
+@pytest.mark.parametrize(
+    "kwargs,dtype,message",
+    [
+        (dict(), 3, "float16 or bfloat16"),
+        (dict(cache_dtype=capi.DK_FLOAT16), capi.DK_BFLOAT16, "float32 or the query dtype"),
+        (dict(rot_dim=130), capi.DK_BFLOAT16, "rot_dim"),
+        (dict(rot_dim=63, head_size=64), capi.DK_BFLOAT16, "rot_dim"),
+        (dict(rot_dim=0), capi.DK_FLOAT16, "rot_dim"),
+        (dict(num_q_heads=-1), capi.DK_FLOAT16, "non-negative"),
+        (dict(query=None), capi.DK_FLOAT16, "NULL"),
+    ],
+)
+def test_capi_rotary_validation(kwargs, dtype, message):
+    p = _rotary_params(**kwargs)
+    rc = capi.lib().dk_rotary_embedding(ctypes.byref(p), dtype, None)
+    assert rc == capi.HIP_ERROR_INVALID_VALUE
+    assert message in capi.last_error()
+
+
+def test_capi_rotary_and_cache_write_no_tokens_are_no_ops():
+    L = capi.lib()
+    assert L.dk_rotary_embedding(ctypes.byref(_rotary_params(num_tokens=0)), capi.DK_BFLOAT16, None) == 0
+    assert L.dk_rotary_embedding(None, capi.DK_BFLOAT16, None) == capi.HIP_ERROR_INVALID_VALUE
+    c = capi.CacheWriteParams()
+    c.num_tokens, c.num_kv_heads, c.head_size, c.block_size, c.num_blocks = 0, 2, 128, 16, 4
+    assert L.dk_reshape_and_cache(ctypes.byref(c), capi.DK_FLOAT16, None) == 0
+    assert capi.last_error() == ""
+
+
+@pytest.mark.parametrize(
+    "field,value,dtype,message",
+    [
+        (None, None, 4, "float16 or bfloat16"),
+        ("block_size", 0, capi.DK_FLOAT16, "positive"),
+        ("num_kv_heads", 0, capi.DK_FLOAT16, "positive"),
+        ("value", None, capi.DK_BFLOAT16, "NULL"),
+        ("slot_mapping", None, capi.DK_BFLOAT16, "NULL"),
+    ],
+)
+def test_capi_cache_write_validation(field, value, dtype, message):
+    c = capi.CacheWriteParams()
+    c.key = c.value = c.key_cache = c.value_cache = c.slot_mapping = 0x10000
+    c.num_tokens, c.num_kv_heads, c.head_size, c.block_size, c.num_blocks = 2, 2, 128, 16, 4
+    if field is not None:
+        setattr(c, field, value)
+    rc = capi.lib().dk_reshape_and_cache(ctypes.byref(c), dtype, None)
+    assert rc == capi.HIP_ERROR_INVALID_VALUE
+    assert message in capi.last_error()
+
+
+def test_capi_fill_helpers_read_tensor_layouts():
+    pos = torch.arange(5)
+    q = torch.zeros(5, 3 * 64, dtype=torch.bfloat16)
+    k = torch.zeros(5, 2, 8, 64, dtype=torch.bfloat16)[:, :, 3]  # strided [T, H, D]
+    cache = torch.zeros(100, 32)
+    p = capi.rotary_params(pos, q, k, 64, cache, False)
+    assert (p.q_stride_token, p.q_stride_head, p.num_q_heads) == (192, 64, 3)
+    assert (p.k_stride_token, p.k_stride_head, p.num_kv_heads) == (1024, 512, 2)
+    assert (p.rot_dim, p.max_position, p.cache_stride, p.is_neox, p.cache_dtype) == (32, 100, 32, 0, capi.DK_FLOAT32)
+    kv = torch.zeros(6, 2, 16, 2 * 64, dtype=torch.float16)
+    kc, vc = kv.transpose(1, 2).split(64, dim=-1)
+    key = torch.zeros(4, 2 * 64, dtype=torch.float16)
+    c = capi.cache_write_params(key, key.view(4, 2, 64), kc, vc, torch.arange(4))
+    assert (c.kc_stride_block, c.kc_stride_token, c.kc_stride_head) == (2 * 16 * 128, 128, 16 * 128)
+    assert c.value_cache - c.key_cache == 64 * 2
+    assert (c.k_stride_token, c.k_stride_head, c.v_stride_token, c.v_stride_head) == (128, 64, 128, 64)
+    assert (c.num_blocks, c.block_size, c.num_kv_heads, c.head_size, c.num_tokens) == (6, 16, 2, 64, 4)
+
+
 # ---------------------------------------------------------------------------
 # Python wrappers (host logic only)
 # ---------------------------------------------------------------------------
@@ -142,6 +232,10 @@ def test_ops_are_registered_with_reference_schemas():
         "rms_norm": "rms_norm(Tensor(a0!) out, Tensor input, Tensor weight, float eps) -> ()",
         "fused_add_rms_norm": "fused_add_rms_norm(Tensor(a0!) input, Tensor(a1!) residual, Tensor weight, float eps) -> ()",
         "silu_and_mul": "silu_and_mul(Tensor(a0!) out, Tensor input) -> ()",
+        "rotary_embedding": "rotary_embedding(Tensor positions, Tensor(a0!) query, Tensor(a1!)? key, int head_size, "
+        "Tensor cos_sin_cache, bool is_neox) -> ()",
+        "reshape_and_cache": "reshape_and_cache(Tensor key, Tensor value, Tensor(a0!) key_cache, "
+        "Tensor(a1!) value_cache, Tensor slot_mapping) -> ()",
     }
     for name, schema in schemas.items():
         got = str(getattr(torch.ops.decode_kernels, name).default._schema).replace("decode_kernels::", "")
@@ -171,6 +265,9 @@ def test_wrappers_fail_loudly_without_extension(monkeypatch):
         lambda: ops.rms_norm(torch.zeros(2, 8), torch.ones(8)),
         lambda: ops.fused_add_rms_norm(torch.zeros(2, 8), torch.zeros(2, 8), torch.ones(8)),
         lambda: ops.silu_and_mul(torch.zeros(2, 8)),
+        lambda: ops.rotary_embedding(torch.zeros(2, dtype=torch.long), torch.zeros(2, 8), None, 8, torch.zeros(4, 8)),
+        lambda: ops.reshape_and_cache(torch.zeros(2, 1, 8), torch.zeros(2, 1, 8), torch.zeros(1, 4, 1, 8),
+                                      torch.zeros(1, 4, 1, 8), torch.zeros(2, dtype=torch.long)),
     ):
         with pytest.raises(RuntimeError, match="not built"):
             call()

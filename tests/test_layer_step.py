@@ -1,13 +1,17 @@
 """GPU test of the ops composed into one decoder layer's decode step.
 
-fused_add_rms_norm -> qkv gemm_tn -> paged_attention_decode (q is a strided
-view of the qkv output, as a serving engine passes it) -> o gemm_tn ->
-fused_add_rms_norm -> gate_up gemm_tn -> silu_and_mul -> down gemm_tn, at the
-head-dim-256 / group-8 attention shape with a reduced MLP width. Each stage is
-checked against the oracle applied to the previous stage's actual output (the
-bar of each op's own parity test), then the whole step is captured in a HIP
-graph and every replay -- with the sequence lengths rewritten on the device
-between replays -- must match an eager run bit for bit.
+fused_add_rms_norm -> qkv gemm_tn -> rotary_embedding on the q and k columns
+of the qkv output -> reshape_and_cache of the new token's k and v columns ->
+paged_attention_decode (q is a strided view of the qkv output, as a serving
+engine passes it) -> o gemm_tn -> fused_add_rms_norm -> gate_up gemm_tn ->
+silu_and_mul -> down gemm_tn, at the head-dim-256 / group-8 attention shape
+with a reduced MLP width. ``seq_lens`` counts the new token, which sits at
+position len - 1; an empty sequence is a padding row (position and slot -1).
+Each stage is checked against the oracle applied to the previous stage's
+actual output (the bar of each op's own parity test), then the whole step is
+captured in a HIP graph and every replay -- with the sequence lengths,
+positions and slots rewritten on the device between replays -- must match an
+eager run bit for bit.
 """
 
 import pytest
@@ -15,6 +19,7 @@ import torch
 
 import decodekernels_amd as dk
 from decodekernels_amd.testing import make_paged_kv
+from oracle.rope_cache import reshape_and_cache_reference, rope_cos_sin_cache, rotary_embedding_reference
 from parity import (
     assert_max_abs,
     assert_ulp,
@@ -56,7 +61,23 @@ class Layer:
         self.down = torch.empty(self.n, HIDDEN, **kw)
         self.ws = dk.alloc_workspace(self.n, HQ, D, self.max_len, "cuda")
         self.q = self.qkv[:, : HQ * D].view(self.n, HQ, D)
+        self.k_new = self.qkv[:, HQ * D : (HQ + HKV) * D]
+        self.v_new = self.qkv[:, (HQ + HKV) * D :]
+        self.rope = rope_cos_sin_cache(4096, D, base=1e6).cuda()
+        self.positions = torch.empty(self.n, dtype=torch.long, device="cuda")
+        self.slots = torch.empty(self.n, dtype=torch.long, device="cuda")
+        self.set_lens(seq_lens)
         self.saved = {}
+
+    def set_lens(self, lens):
+        """Lengths, positions and cache slots of a step whose new token is the
+        last of each sequence (written in place: a captured graph follows)."""
+        bt = self.kv.block_tables.cpu()
+        pos = [n - 1 for n in lens]
+        slots = [int(bt[s, p // BS]) * BS + p % BS if p >= 0 else -1 for s, p in enumerate(pos)]
+        self.kv.seq_lens.copy_(torch.tensor(lens, dtype=torch.int32))
+        self.positions.copy_(torch.tensor(pos))
+        self.slots.copy_(torch.tensor(slots))
 
     def step(self, keep=False):
         ops = torch.ops.decode_kernels
@@ -66,6 +87,13 @@ class Layer:
         if keep:
             self.saved["norm1"] = (self.x.clone(), self.resid.clone())
         ops.gemm_tn(self.qkv, self.x, self.w_qkv, None)
+        if keep:
+            self.saved["qkv"] = self.qkv.clone()
+        ops.rotary_embedding(self.positions, self.qkv[:, : HQ * D], self.k_new, D, self.rope, True)
+        if keep:
+            self.saved["k_cache"] = self.kv.k_cache.clone()
+            self.saved["v_cache"] = self.kv.v_cache.clone()
+        ops.reshape_and_cache(self.k_new, self.v_new, self.kv.k_cache, self.kv.v_cache, self.slots)
         dk.paged_attention_decode(self.q, self.kv.k_cache, self.kv.v_cache, self.kv.block_tables, self.kv.seq_lens,
                                   max_seq_len=self.max_len, out=self.attn, workspace=self.ws)
         ops.gemm_tn(self.o, self.attn.view(self.n, HIDDEN), self.w_o, None)
@@ -78,7 +106,8 @@ class Layer:
         ops.gemm_tn(self.down, self.act, self.w_down, None)
 
     def outputs(self):
-        return [t.clone() for t in (self.qkv, self.attn, self.o, self.resid, self.gu, self.act, self.down)]
+        return [t.clone() for t in (self.qkv, self.kv.k_cache, self.kv.v_cache, self.attn, self.o, self.resid, self.gu,
+                                    self.act, self.down)]
 
 
 SEQ_LENS = [0, 1, 600, 1500, 33, 2049, 512, 513]
@@ -93,7 +122,17 @@ def test_layer_step_stages_match_oracle(dtype):
     want_x, want_r = fused_add_rms_norm_reference(L.x0.cpu(), L.r0.cpu(), L.ln1.cpu(), EPS)
     assert torch.equal(r1.cpu(), want_r), "residual of the first fused_add_rms_norm is not bit-exact"
     assert_ulp(x1, want_x, 1, "fused_add_rms_norm")
-    assert_max_abs(L.qkv, gemm_f32(x1, L.w_qkv), dtype, "qkv gemm")
+    qkv = L.saved["qkv"]
+    assert_max_abs(qkv, gemm_f32(x1, L.w_qkv), dtype, "qkv gemm")
+    hq_d, kv_d = HQ * D, (HQ + HKV) * D
+    want_q, want_k = rotary_embedding_reference(L.positions.cpu(), qkv[:, :hq_d].cpu(), qkv[:, hq_d:kv_d].cpu(), D,
+                                                L.rope.cpu(), True)
+    assert_ulp(L.qkv[:, :hq_d], want_q, 0, "rotary_embedding(q)")
+    assert_ulp(L.qkv[:, hq_d:kv_d], want_k, 0, "rotary_embedding(k)")
+    assert torch.equal(L.qkv[:, kv_d:], qkv[:, kv_d:]), "v columns must pass through RoPE untouched"
+    want_kc, want_vc = reshape_and_cache_reference(L.k_new.cpu(), L.v_new.cpu(), L.saved["k_cache"].cpu(),
+                                                   L.saved["v_cache"].cpu(), L.slots.cpu())
+    assert torch.equal(L.kv.k_cache.cpu(), want_kc) and torch.equal(L.kv.v_cache.cpu(), want_vc)
     ref_attn = attention_f32(L.q, L.kv.k_cache, L.kv.v_cache, L.kv.block_tables, L.kv.seq_lens)
     assert_max_abs(L.attn, ref_attn, dtype, "attention on the qkv view")
     assert (L.attn[0] == 0).all(), "zero-length sequence must give zeros"
@@ -119,12 +158,13 @@ def test_layer_step_graph_replays_match_eager():
         L.step()
     lens_sets = [SEQ_LENS, [5, 0, 2049, 17, 1024, 1, 700, 2000], SEQ_LENS]
     for i, lens in enumerate(lens_sets):
-        L.kv.seq_lens.copy_(torch.tensor(lens, dtype=torch.int32))
+        L.set_lens(lens)
         graph.replay()
         torch.cuda.synchronize()
         got = L.outputs()
         L.step()
         torch.cuda.synchronize()
         want = L.outputs()
-        for name, a, b in zip(("qkv", "attn", "o", "resid", "gate_up", "act", "down"), got, want):
+        names = ("qkv", "k_cache", "v_cache", "attn", "o", "resid", "gate_up", "act", "down")
+        for name, a, b in zip(names, got, want):
             assert torch.equal(a, b), f"replay {i}: {name} differs from the eager step"

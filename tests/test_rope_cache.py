@@ -1,0 +1,255 @@
+"""GPU parity tests of rotary_embedding and reshape_and_cache against
+``oracle/rope_cache.py``.
+
+Rotary embedding: bit-exact against the oracle (both round each fp32 product
+and sum on its own, then once to the model dtype; the kernel is built without
+fused multiply-adds for this), including columns past rot_dim and tokens
+whose position is outside the table, which stay as they were. Cache write:
+bit-exact. Cases: NeoX and GPT-J pairing, partial rot_dim, float32 and
+model-dtype tables, flat / 3-D / strided q and k (the vector and the scalar
+paths), key None, the three cache layouts paged attention reads, padding and
+out-of-range slots, and a decode step that appends a token through
+reshape_and_cache and attends over it.
+"""
+
+import ctypes
+
+import pytest
+import torch
+
+import decodekernels_amd as dk
+from decodekernels_amd import capi
+from decodekernels_amd.testing import make_paged_kv
+from oracle.rope_cache import reshape_and_cache_reference, rope_cos_sin_cache, rotary_embedding_reference
+from parity import assert_max_abs, assert_ulp, attention_f32
+
+pytestmark = pytest.mark.gpu
+
+DTYPES = [torch.float16, torch.bfloat16]
+
+
+def _stream():
+    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def _qkv(t, hq, hkv, d, dtype, seed, pad=0):
+    """Query and key as the column slices of a fused qkv projection output
+    ([t, (hq + 2 hkv) d + pad]), the layout a decode step hands to RoPE."""
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    width = (hq + 2 * hkv) * d + pad
+    qkv = torch.randn(t, width, generator=g, device="cuda", dtype=dtype)
+    return qkv, qkv[:, : hq * d], qkv[:, hq * d : (hq + hkv) * d]
+
+
+def _positions(t, max_position, seed, out_of_range=True):
+    g = torch.Generator(device="cpu").manual_seed(seed)
+    pos = torch.randint(0, max_position, (t,), generator=g)
+    if out_of_range and t >= 3:
+        pos[0], pos[t // 2], pos[-1] = -1, max_position, 0
+    return pos.cuda()
+
+
+def _check_rope(pos, q, k, head_size, cache, is_neox):
+    want_q, want_k = rotary_embedding_reference(
+        pos.cpu(), q.cpu(), None if k is None else k.cpu(), head_size, cache.cpu(), is_neox
+    )
+    q0 = q.clone()
+    dk.rotary_embedding(pos, q, k, head_size, cache, is_neox)
+    torch.cuda.synchronize()
+    assert_ulp(q, want_q, 0, "rotary_embedding(query)")
+    rot = cache.shape[1]
+    t = q.shape[0]
+    assert torch.equal(q.reshape(t, -1, head_size)[..., rot:], q0.reshape(t, -1, head_size)[..., rot:])
+    bad = (pos < 0) | (pos >= cache.shape[0])
+    assert torch.equal(q[bad], q0[bad])
+    if k is not None:
+        assert_ulp(k, want_k, 0, "rotary_embedding(key)")
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("is_neox", [True, False])
+@pytest.mark.parametrize("head_size,rot_dim", [(64, 64), (128, 128), (256, 256), (128, 64), (128, 32)])
+def test_rope_fused_qkv_slices(dtype, is_neox, head_size, rot_dim):
+    t, hq, hkv = 37, 8, 2
+    cache = rope_cos_sin_cache(4096, rot_dim).cuda()
+    qkv, q, k = _qkv(t, hq, hkv, head_size, dtype, seed=head_size + rot_dim + is_neox)
+    v0 = qkv[:, (hq + hkv) * head_size :].clone()
+    _check_rope(_positions(t, 4096, 1), q, k, head_size, cache, is_neox)
+    assert torch.equal(qkv[:, (hq + hkv) * head_size :], v0), "value columns must be untouched"
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("is_neox", [True, False])
+def test_rope_model_dtype_table_and_3d_views(dtype, is_neox):
+    t, hq, hkv, d = 64, 32, 8, 128
+    cache = rope_cos_sin_cache(8192, d, base=500000.0, dtype=dtype).cuda()
+    g = torch.Generator(device="cuda").manual_seed(5)
+    q = torch.randn(t, hq, d, generator=g, device="cuda", dtype=dtype)
+    k = torch.randn(t, hkv, 2, d, generator=g, device="cuda", dtype=dtype)[:, :, 1]  # head stride 2d
+    _check_rope(_positions(t, 8192, 2), q, k, d, cache, is_neox)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("is_neox", [True, False])
+@pytest.mark.parametrize("case", ["odd_stride", "rot_dim_20", "head_size_80"])
+def test_rope_scalar_path(dtype, is_neox, case):
+    """Layouts the vector path cannot take: token strides not a multiple of
+    the vector, rot_dim / 2 not a multiple of 4."""
+    t, hq, hkv = 19, 4, 2
+    if case == "odd_stride":
+        d, rot, pad = 128, 128, 2
+    elif case == "rot_dim_20":
+        d, rot, pad = 64, 20, 0
+    else:
+        d, rot, pad = 80, 40, 0
+    cache = rope_cos_sin_cache(1000, rot).cuda()
+    _, q, k = _qkv(t, hq, hkv, d, dtype, seed=7, pad=pad)
+    _check_rope(_positions(t, 1000, 3), q, k, d, cache, is_neox)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_rope_without_key_and_large_batch(dtype):
+    t, hq, d = 4096, 32, 128
+    cache = rope_cos_sin_cache(131072, d, base=500000.0).cuda()
+    g = torch.Generator(device="cuda").manual_seed(9)
+    q = torch.randn(t, hq * d, generator=g, device="cuda", dtype=dtype)
+    _check_rope(_positions(t, 131072, 4), q, None, d, cache, True)
+
+
+def test_rope_no_tokens_is_a_no_op():
+    q = torch.empty(0, 128, device="cuda", dtype=torch.bfloat16)
+    dk.rotary_embedding(torch.empty(0, dtype=torch.long, device="cuda"), q, None, 128, torch.zeros(8, 128, device="cuda"))
+    torch.cuda.synchronize()
+
+
+def test_rope_rejects_bad_arguments():
+    q = torch.zeros(4, 256, device="cuda", dtype=torch.bfloat16)
+    pos = torch.zeros(4, dtype=torch.long, device="cuda")
+    with pytest.raises(RuntimeError, match="rot_dim"):
+        dk.rotary_embedding(pos, q, None, 128, torch.zeros(8, 130, device="cuda"))
+    with pytest.raises(RuntimeError, match="float32 or the query dtype"):
+        dk.rotary_embedding(pos, q, None, 128, torch.zeros(8, 128, device="cuda", dtype=torch.float16))
+    with pytest.raises(RuntimeError, match="int64"):
+        dk.rotary_embedding(pos.int(), q, None, 128, torch.zeros(8, 128, device="cuda"))
+    with pytest.raises(RuntimeError, match="multiple of head_size"):
+        dk.rotary_embedding(pos, q, None, 96, torch.zeros(8, 96, device="cuda"))
+
+
+@pytest.mark.parametrize("is_neox", [True, False])
+def test_rope_capi_matches_torch_op(is_neox):
+    dtype = torch.bfloat16
+    t, hq, hkv, d = 33, 8, 2, 128
+    cache = rope_cos_sin_cache(2048, d).cuda()
+    _, q, k = _qkv(t, hq, hkv, d, dtype, seed=11)
+    q2, k2 = q.clone(), k.clone()
+    pos = _positions(t, 2048, 5)
+    p = capi.rotary_params(pos, q2, k2, d, cache, is_neox)
+    rc = capi.lib().dk_rotary_embedding(ctypes.byref(p), capi.dtype_code(dtype), _stream())
+    assert rc == 0, capi.last_error()
+    dk.rotary_embedding(pos, q, k, d, cache, is_neox)
+    torch.cuda.synchronize()
+    assert torch.equal(q, q2) and torch.equal(k, k2)
+
+
+# ---------------------------------------------------------------------------
+# reshape_and_cache
+# ---------------------------------------------------------------------------
+def _slots(num_blocks, block_size, t, seed):
+    g = torch.Generator(device="cpu").manual_seed(seed)
+    slots = torch.randperm(num_blocks * block_size, generator=g)[:t].clone()
+    if t >= 4:
+        slots[1] = -1  # padding token
+        slots[t // 2] = num_blocks * block_size + 3  # past the cache: skipped
+    return slots.cuda()
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("layout", ["nhd", "hnd", "vllm"])
+@pytest.mark.parametrize("head_dim,block_size", [(64, 16), (128, 16), (128, 32), (256, 16)])
+def test_cache_write_layouts(dtype, layout, head_dim, block_size):
+    hkv, t = 4, 150
+    kv = make_paged_kv([700, 300], hkv, head_dim, block_size, dtype, "cuda", layout=layout, seed=head_dim)
+    g = torch.Generator(device="cuda").manual_seed(12)
+    key = torch.randn(t, hkv, head_dim, generator=g, device="cuda", dtype=dtype)
+    value = torch.randn(t, hkv * head_dim, generator=g, device="cuda", dtype=dtype)
+    slots = _slots(kv.k_cache.shape[0], block_size, t, 13)
+    want_k, want_v = reshape_and_cache_reference(key.cpu(), value.cpu(), kv.k_cache.cpu(), kv.v_cache.cpu(), slots.cpu())
+    dk.reshape_and_cache(key, value, kv.k_cache, kv.v_cache, slots)
+    torch.cuda.synchronize()
+    assert torch.equal(kv.k_cache.cpu(), want_k)
+    assert torch.equal(kv.v_cache.cpu(), want_v)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("case", ["misaligned_rows", "head_size_36"])
+def test_cache_write_scalar_path(dtype, case):
+    hkv, t, bs, nb = 2, 40, 16, 8
+    d = 36 if case == "head_size_36" else 64
+    g = torch.Generator(device="cuda").manual_seed(14)
+    kc = torch.randn(nb, bs, hkv, d, generator=g, device="cuda", dtype=dtype)
+    vc = torch.randn(nb, bs, hkv, d, generator=g, device="cuda", dtype=dtype)
+    buf = torch.randn(t, 2 * hkv * d + 1, generator=g, device="cuda", dtype=dtype)
+    off = 1 if case == "misaligned_rows" else 0
+    key = buf[:, off : off + hkv * d]
+    value = buf[:, off + hkv * d : off + 2 * hkv * d]
+    slots = _slots(nb, bs, t, 15)
+    want_k, want_v = reshape_and_cache_reference(key.cpu(), value.cpu(), kc.cpu(), vc.cpu(), slots.cpu())
+    dk.reshape_and_cache(key, value, kc, vc, slots)
+    torch.cuda.synchronize()
+    assert torch.equal(kc.cpu(), want_k) and torch.equal(vc.cpu(), want_v)
+
+
+def test_cache_write_capi_matches_torch_op():
+    dtype = torch.float16
+    kv = make_paged_kv([900], 8, 128, 16, dtype, "cuda", layout="vllm", seed=3)
+    kc2, vc2 = kv.k_cache.clone(), kv.v_cache.clone()
+    g = torch.Generator(device="cuda").manual_seed(16)
+    key = torch.randn(64, 8, 128, generator=g, device="cuda", dtype=dtype)
+    value = torch.randn(64, 8, 128, generator=g, device="cuda", dtype=dtype)
+    slots = _slots(kv.k_cache.shape[0], 16, 64, 17)
+    p = capi.cache_write_params(key, value, kc2, vc2, slots)
+    rc = capi.lib().dk_reshape_and_cache(ctypes.byref(p), capi.dtype_code(dtype), _stream())
+    assert rc == 0, capi.last_error()
+    dk.reshape_and_cache(key, value, kv.k_cache, kv.v_cache, slots)
+    torch.cuda.synchronize()
+    assert torch.equal(kv.k_cache, kc2) and torch.equal(kv.v_cache, vc2)
+
+
+def test_cache_write_rejects_bad_arguments():
+    kc = torch.zeros(4, 16, 2, 64, device="cuda", dtype=torch.bfloat16)
+    key = torch.zeros(3, 2, 64, device="cuda", dtype=torch.bfloat16)
+    slots = torch.zeros(3, dtype=torch.long, device="cuda")
+    with pytest.raises(RuntimeError, match="int64"):
+        dk.reshape_and_cache(key, key, kc, kc.clone(), slots.int())
+    with pytest.raises(RuntimeError, match="heads"):
+        dk.reshape_and_cache(torch.zeros(3, 4, 64, device="cuda", dtype=torch.bfloat16), key, kc, kc.clone(), slots)
+    with pytest.raises(RuntimeError, match="one key / value row"):
+        dk.reshape_and_cache(key, key, kc, kc.clone(), slots[:2])
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("layout", ["nhd", "vllm"])
+def test_decode_step_appends_and_attends(dtype, layout):
+    """One decode step: RoPE on the new token's q / k, the k / v row written at
+    the next slot of each sequence, then attention over the grown cache."""
+    hq, hkv, d, bs = 16, 4, 128, 16
+    lens = [5, 300, 1100, 47]  # none a multiple of the block size: room in the last block
+    kv = make_paged_kv(lens, hkv, d, bs, dtype, "cuda", layout=layout, seed=18)
+    n = len(lens)
+    qkv, q, k = _qkv(n, hq, hkv, d, dtype, seed=19)
+    v = qkv[:, (hq + hkv) * d :]
+    cache = rope_cos_sin_cache(4096, d).cuda()
+    pos = torch.tensor(lens, device="cuda")  # the new token's position
+    want_q, want_k = rotary_embedding_reference(pos.cpu(), q.cpu(), k.cpu(), d, cache.cpu(), True)
+    dk.rotary_embedding(pos, q, k, d, cache, True)
+    bt = kv.block_tables.cpu()
+    slots = torch.tensor([int(bt[s, lens[s] // bs]) * bs + lens[s] % bs for s in range(n)], device="cuda")
+    dk.reshape_and_cache(k, v, kv.k_cache, kv.v_cache, slots)
+    new_lens = (kv.seq_lens + 1).contiguous()
+    q3 = q.reshape(n, hq, d)
+    out = dk.paged_attention_decode(q3, kv.k_cache, kv.v_cache, kv.block_tables, new_lens)
+    torch.cuda.synchronize()
+    assert_ulp(q, want_q, 0, "rotary_embedding(query)")
+    assert_ulp(k, want_k, 0, "rotary_embedding(key)")
+    ref = attention_f32(q3, kv.k_cache, kv.v_cache, kv.block_tables, new_lens)
+    assert_max_abs(out, ref, dtype, "paged_attention_decode after the cache write")
