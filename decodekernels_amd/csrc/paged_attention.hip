@@ -87,8 +87,7 @@ struct KParams {
   int64_t bt_stride;
   int num_q_heads, group, block_size, max_partitions;
   int num_seqs, num_kv_heads;
-  int num_units;  // split-K: unit positions per sequence, ceil(max_partitions / 2)
-  unsigned* unit_counter;                 // persistent split-K path: next work unit (zeroed before launch)
+  int num_units;  // split-K grid: unit positions per sequence, ceil(max_partitions / 2)
   float scale_log2;
 };
 
@@ -178,7 +177,7 @@ __device__ __forceinline__ void lds_barrier() {
 
 // Runs work units on NW waves: wave w takes tiles w, w + NW, ... of a unit,
 // keeps DEPTH tiles of loads in flight and its own online-softmax state; the
-// waves merge through LDS. The steps are separate so that the persistent
+// waves merge through LDS. The steps are separate so that the balanced
 // kernel can issue the next unit's loads before merging the current one.
 template <typename E, int D, bool SPLIT, bool BS16, int ALIGN, int NW>
 struct UnitEngine {
@@ -493,180 +492,207 @@ void paged_attention_kernel(const KParams p) {
   eng.merge(u);
 }
 
-// Persistent split-K kernel: a resident-sized grid pulls work units from a
-// list, so no workgroup is launched for a position past a sequence's end (at
-// mixed lengths most grid slots are such, and launching them costs the
-// dispatcher more than the work), and each workgroup starts its next unit's
-// loads while it merges the current one (a unit's start is three dependent
-// round trips -- length, block table, first tiles -- which a grid workgroup
-// waits through every time).
+// Balanced split-K kernel: a resident-sized grid in which every workgroup
+// gets an equal share of the work, known up front.
 //
-// Every workgroup lists the live units itself from seq_lens, largest first:
-// the full 1024-token units at positions >= 1, then the shorter last units at
-// positions >= 1, then the two 512-token units covering each sequence's first
-// 1024 tokens (the same cut as the grid kernel, so the results are
-// bit-identical); KV heads innermost. Prefix sums in LDS map a unit index back
-// to its sequence by binary search. Whole rounds of full units are dealt out
-// by grid index (equal sizes, no contention); the rest come from an atomic
-// counter (zeroed before launch).
-constexpr int kMaxPersistSeqs = 2048;
+// Per-workgroup bandwidth is latency-bound (each workgroup moves ~1/500 of
+// the chip's bandwidth), so a 1024-token unit takes tens of microseconds and a
+// grid of whole units ends with a long tail of the last ones. Here the
+// (sequence, KV head) streams are laid end to end (sequences in order, KV
+// heads innermost) on a line where each stream costs its 16-token tiles plus
+// a fixed overhead (its query load and partial-result merge, counted as
+// kStreamCost tiles), and workgroup w takes cost range [w s, w s + s),
+// s = max(64, ceil(total / grid)). Since a workgroup knows its whole list, the
+// next piece's block-table entries, query and first tiles load while the
+// current one finishes: no piece start waits on a round trip, no atomics.
+//
+// A piece is one stream's tiles inside a workgroup's share (run as sub-units
+// of at most 64 tiles sharing one softmax state). Its partial result goes to
+// workspace row (w - workgroup of the stream's first tile) of the stream's
+// query heads: rows are numbered by piece, not by token position. A stream of
+// n tiles meets at most ceil(n / 64) + 1 shares, which is at most
+// max(2, ceil(L / 512)) <= max_partitions rows; the workgroup holding a
+// stream's last tile marks the row after its piece empty (exp-sum 0), and the
+// reduce reads rows up to the first empty one.
+constexpr int kMaxBalancedSeqs = 2048;
+constexpr int kMinShareTiles = 64;
+#ifndef DK_ATTN_STREAM_COST
+#define DK_ATTN_STREAM_COST 8  // per-stream overhead, in tiles, of the share balance
+#endif
+constexpr int kStreamCost = DK_ATTN_STREAM_COST;
 
 template <typename E, int D, bool BS16, int ALIGN, int NW>
 __global__ __launch_bounds__(NW * kWave) __attribute__((amdgpu_waves_per_eu(attn_occupancy<D>(), attn_occupancy<D>())))
-void paged_attention_persistent_kernel(const KParams p) {
+void paged_attention_balanced_kernel(const KParams p) {
   constexpr int NT = NW * kWave;
   __shared__ UnitSmem<D, NW> sm;
-  __shared__ int pf[kMaxPersistSeqs + 1];  // full units at positions >= 1 of sequences 0 .. s-1
-  __shared__ int pr[kMaxPersistSeqs + 1];  // last units at positions >= 1 (shorter than 1024 tokens)
-  __shared__ int ph[kMaxPersistSeqs + 1];  // 512-token units at position 0
-  __shared__ long long scan[NT];
-  __shared__ int claimed[1];
+  __shared__ int pre[kMaxBalancedSeqs + 1];  // cost per KV head of sequences 0 .. s-1
+  __shared__ int len[kMaxBalancedSeqs];      // lengths, clamped to the workspace
+  __shared__ int scan[NT];
   const int tid = threadIdx.x;
   const int S = p.num_seqs;
-  const int max_tokens = p.max_partitions * kPart;  // tokens past the workspace are ignored
-  auto clamped_len = [&](int s) { return min(max(p.seq_lens[s], 0), max_tokens); };
-  // (full, last, half) unit counts of one sequence, packed 32 | 16 | 16 bits.
-  auto counts = [](int len) {
-    const long long full = len / kUnit >= 1 ? len / kUnit - 1 : 0;
-    const long long last = (len > kUnit && len % kUnit != 0) ? 1 : 0;
-    const long long half = (len > 0 ? 1 : 0) + (len > kPart ? 1 : 0);
-    return (full << 32) + (last << 16) + half;
-  };
+  const int P = p.max_partitions;
+  const int max_tokens = P * kPart;  // tokens past the workspace are ignored
+  auto tiles_of = [&](int s) { return (len[s] + kTile - 1) / kTile; };
+  auto cost_of_len = [](int l) { return l > 0 ? (l + kTile - 1) / kTile + kStreamCost : 0; };
 
-  // Per-thread chunk of sequences -> block-wide exclusive scan of the counts.
+  // Per-thread chunk of sequences -> block-wide inclusive scan of stream costs.
   const int per = (S + NT - 1) / NT;
   const int s0 = min(tid * per, S);
   const int s1 = min(s0 + per, S);
-  long long cnt = 0;
-  for (int s = s0; s < s1; ++s) cnt += counts(clamped_len(s));
+  int cnt = 0;
+  for (int s = s0; s < s1; ++s) {
+    const int l = min(max(p.seq_lens[s], 0), max_tokens);
+    len[s] = l;
+    cnt += cost_of_len(l);
+  }
   scan[tid] = cnt;
   __syncthreads();
   for (int off = 1; off < NT; off <<= 1) {
-    const long long add = tid >= off ? scan[tid - off] : 0;
+    const int add = tid >= off ? scan[tid - off] : 0;
     __syncthreads();
     scan[tid] += add;
     __syncthreads();
   }
-  long long run = scan[tid] - cnt;
+  int run = scan[tid] - cnt;
   for (int s = s0; s < s1; ++s) {
-    pf[s] = static_cast<int>(run >> 32);
-    pr[s] = static_cast<int>((run >> 16) & 0xffff);
-    ph[s] = static_cast<int>(run & 0xffff);
-    run += counts(clamped_len(s));
+    pre[s] = run;
+    run += cost_of_len(len[s]);
   }
-  if (tid == NT - 1) {
-    pf[S] = static_cast<int>(scan[NT - 1] >> 32);
-    pr[S] = static_cast<int>((scan[NT - 1] >> 16) & 0xffff);
-    ph[S] = static_cast<int>(scan[NT - 1] & 0xffff);
-  }
+  if (tid == NT - 1) pre[S] = scan[NT - 1];
   __syncthreads();
 
   const int hkv = p.num_kv_heads;
-  const int n_full = pf[S] * hkv;
-  const int n_last = pr[S] * hkv;
-  const int total = n_full + n_last + ph[S] * hkv;
+  const int total = pre[S] * hkv;  // < 2^31 (checked by the host)
   const int G = gridDim.x;
+  const int share = max(kMinShareTiles, (total + G - 1) / G);
   const int w = blockIdx.x;
-  if (w >= total) return;
-  const int dealt_rounds = max(1, n_full / G);
-  const int dealt = min(total, dealt_rounds * G);
-  // Units past the dealt ones come from one counter: a claim's round trip
-  // takes microseconds under contention, so a workgroup must learn that the
-  // list is exhausted from a single claim.
-  auto claim_issue = [&]() { return static_cast<int>(atomicAdd(p.unit_counter, 1u)); };
-  auto claim_finish = [&](int k) { return min(dealt + k, total); };
-  // Last s with a[s] <= j (a[0] = 0 <= j < a[S]).
-  auto find = [&](const int* a, int j) {
+  const int a = w * share;
+  if (a >= total) return;
+  const int b = min(a + share, total);
+  auto cost_of = [&](int s) { return pre[s + 1] - pre[s]; };
+
+  // Stream holding cost position a: the last sequence whose first position
+  // is <= a (it has tiles, since pre[S] * hkv > a), then the KV head.
+  int seq = 0;
+  {
     int lo = 0, hi = S;
     while (hi - lo > 1) {
       const int mid = (lo + hi) >> 1;
-      if (a[mid] <= j) lo = mid;
+      if (pre[mid] * hkv <= a) lo = mid;
       else hi = mid;
     }
-    return lo;
+    seq = lo;
+  }
+  int kv = (a - pre[seq] * hkv) / cost_of(seq);
+
+  // Walk the streams that meet [a, b): each contributes the tiles
+  // [lo, hi) of its own (local) numbering that lie inside the share.
+  int u = 0, hi = 0, row = 0;
+  bool last_tile_here = false;  // this share holds the stream's last tile
+  auto advance = [&]() {        // to the next stream with tiles; false if none
+    if (++kv < hkv) return true;
+    kv = 0;
+    for (;;) {
+      if (++seq >= S) return false;
+      if (cost_of(seq) > 0) return true;
+    }
   };
-  auto decode = [&](int idx) {
-    if (idx < n_full) {
-      const int j = idx / hkv;
-      const int s = find(pf, j);
-      const int pos = 1 + j - pf[s];
-      return make_unit(idx - j * hkv, s, pos * kUnit, kUnit, clamped_len(s), 2 * pos);
+  auto enter_stream = [&]() {  // false once the streams start past the share
+    for (;;) {
+      const int first = pre[seq] * hkv + kv * cost_of(seq) + kStreamCost;  // position of tile 0
+      const int n = tiles_of(seq);
+      if (first >= b) return false;
+      const int lo = max(a, first) - first;
+      hi = min(b, first + n) - first;
+      if (lo < hi) {
+        u = lo;
+        row = w - first / share;
+        last_tile_here = hi == n;
+        return true;
+      }
+      if (!advance()) return false;  // the share covers only this stream's overhead
     }
-    if (idx < n_full + n_last) {
-      const int v = idx - n_full;
-      const int s = find(pr, v / hkv);
-      const int len = clamped_len(s);
-      const int pos = len / kUnit;
-      return make_unit(v % hkv, s, pos * kUnit, kUnit, len, 2 * pos);
-    }
-    const int v = idx - n_full - n_last;
-    const int j = v / hkv;
-    const int s = find(ph, j);
-    const int k = j - ph[s];
-    return make_unit(v - j * hkv, s, k * kPart, kPart, clamped_len(s), k);
+  };
+  auto next_stream = [&]() { return advance() && enter_stream(); };
+
+  struct Sub {
+    Unit unit;
+    int tiles;
+    bool piece_end, stream_end;
+  };
+  auto make_sub = [&]() {
+    const int m = min(kMinShareTiles, hi - u);
+    Sub r;
+    r.unit = Unit{kv, seq, u * kTile, min((u + m) * kTile, len[seq]), row, false};
+    r.tiles = m;
+    r.piece_end = u + m == hi;
+    r.stream_end = r.piece_end && last_tile_here;
+    return r;
   };
 
+  if (!enter_stream()) return;
   UnitEngine<E, D, true, BS16, ALIGN, NW> eng(p, sm);
-  Unit cu = decode(w);
-  int cu_bt = eng.load_bt(cu);
-  eng.load_q(cu);
-  eng.prologue(cu, cu_bt);
-  for (int k = 0;; ++k) {
-    if (k + 1 < dealt_rounds) {
-      // Next unit known: its block-table entries load while this unit runs,
-      // its query and first tiles before this unit's merge.
-      const Unit nu = decode(w + (k + 1) * G);
-      const int nu_bt = eng.load_bt(nu);
-      eng.run_tiles(cu, cu_bt);
-      eng.load_q(nu);
-      eng.prologue(nu, nu_bt);
-      eng.merge(cu);
-      eng.reset();
-      cu = nu;
-      cu_bt = nu_bt;
-      continue;
+  Sub cur = make_sub();
+  int cur_bt = eng.load_bt(cur.unit);
+  eng.load_q(cur.unit);
+  eng.prologue(cur.unit, cur_bt);
+  for (;;) {
+    u += cur.tiles;
+    bool more = true;
+    bool new_stream = false;
+    if (cur.piece_end) {
+      more = next_stream();
+      new_stream = true;
     }
-    // Next unit from the counters. A claim completes in order with the loads
-    // issued before it, so waiting for any later load would wait for the
-    // claim's round trip too: thread 0 issues it after this unit's last tile,
-    // keeps the answer in a register through the merge (LDS only) and
-    // publishes it afterwards.
-    eng.run_tiles(cu, cu_bt);
-    int mine = 0;
-    if (tid == 0) mine = claim_issue();
-    eng.merge(cu);
-    eng.reset();
-    if (tid == 0) claimed[0] = claim_finish(mine);
-    lds_barrier();
-    const int next = claimed[0];
-    if (next >= total) break;
-    const Unit nu = decode(next);
-    const int nu_bt = eng.load_bt(nu);
-    eng.load_q(nu);
-    eng.prologue(nu, nu_bt);
-    cu = nu;
-    cu_bt = nu_bt;
+    Sub nxt{};
+    int nxt_bt = 0;
+    if (more) {
+      nxt = make_sub();
+      nxt_bt = eng.load_bt(nxt.unit);  // in flight while this sub-unit runs
+    }
+    eng.run_tiles(cur.unit, cur_bt);
+    if (more) {
+      if (new_stream) eng.load_q(nxt.unit);
+      eng.prologue(nxt.unit, nxt_bt);
+    }
+    if (cur.piece_end) {
+      eng.merge(cur.unit);
+      eng.reset();
+      const int next_row = cur.unit.slot + 1;
+      if (cur.stream_end && next_row < P && tid < p.group) {
+        const int64_t r =
+            (static_cast<int64_t>(cur.unit.seq) * p.num_q_heads + cur.unit.kv_head * p.group + tid) * P + next_row;
+        p.max_logits[r] = -__builtin_huge_valf();
+        p.exp_sums[r] = 0.0f;
+      }
+    }
+    if (!more) break;
+    cur = nxt;
+    cur_bt = nxt_bt;
   }
 }
 
-__global__ void zero_counter_kernel(unsigned* counter) {
-  if (threadIdx.x == 0) *counter = 0u;
-}
-
-// Log-sum-exp merge of the 512-token slots of one (query head, sequence):
+// Log-sum-exp merge of the partial results of one (query head, sequence):
 //   M = max_p m_p,  w_p = s_p * exp(m_p - M),  out = sum_p w_p o_p / sum_p w_p
-// (reference: csrc/paged_attention.cuh:227-269). WPH waves per query head,
-// max(4, WPH) waves per workgroup. The (m_p, s_p) pairs are uniform across a
-// wave (scalar loads) and each lane accumulates D/64 output columns; with
-// WPH > 1 the waves of a head take every WPH-th slot and merge through LDS.
-// The op is latency-bound: WPH grows with the number of slots a head merges
-// (1 wave up to 8 entries, 4 up to 63, 16 beyond; measured).
+// (reference: csrc/paged_attention.cuh:227-269). Two row layouts:
+//   PIECES = false (grid schedule): row p = tokens [512 p, 512 p + 512);
+//     results in rows 0, 1 and the even rows >= 2 (1024-token units), odd rows
+//     >= 3 hold no result. Rows are walked by index so no load waits on another.
+//   PIECES = true (balanced schedule): rows 0 .. n-1 hold the stream's pieces,
+//     row n (if < max_partitions) is marked empty (exp-sum 0); n is found with
+//     one lane-parallel pass over the exp-sums.
+// WPH waves per query head, max(4, WPH) waves per workgroup. The (m_p, s_p)
+// pairs are uniform across a wave and each lane accumulates D/64 output
+// columns; with WPH > 1 the waves of a head take every WPH-th row and merge
+// through LDS. The op is latency-bound: WPH grows with the number of rows a
+// head merges (1 wave up to 8, 4 up to 63, 16 beyond; measured).
 template <int WPH>
 constexpr int reduce_waves() {
   return WPH > 4 ? WPH : 4;
 }
 
-template <typename E, int D, int WPH>
+template <typename E, int D, int WPH, bool PIECES>
 __global__ __launch_bounds__(reduce_waves<WPH>() * kWave) void paged_attention_reduce_kernel(const KParams p) {
   constexpr int kReduceWaves = reduce_waves<WPH>();
   constexpr int C = D / kWave;  // columns per lane (1, 2 or 4)
@@ -687,21 +713,37 @@ __global__ __launch_bounds__(reduce_waves<WPH>() * kWave) void paged_attention_r
     }
     return;
   }
-  const int n = min((seq_len + kPart - 1) / kPart, p.max_partitions);
   const int64_t row0 = (static_cast<int64_t>(seq) * p.num_q_heads + (active ? q_head : 0)) * p.max_partitions;
   const float* ml = p.max_logits + row0;
   const float* es = p.exp_sums + row0;
   const float* tmp = p.tmp_out + row0 * D + C * lane;
 
-  // Slots holding results: 0, 1 (a 512-token unit in the grid schedule; marked
-  // empty by the persistent schedule, whose unit 0 spans 1024 tokens) and the
-  // even slots >= 2 (1024-token units); odd slots >= 3 are always empty. They
-  // are walked by index so that no load waits on another's value.
-  const int units = 2 + (n - 1) / 2;  // entries j: slot 0, slot 1, then slot 2 (j - 1)
-  const bool slot1 = n > 1 && es[1] != 0.0f;
+  int entries;  // entries j map to rows row_of(j)
+  bool slot1 = true;
   float M = -__builtin_huge_valf();
-  for (int j = lane; j < units; j += kWave) {
-    if (j != 1 || slot1) M = fmaxf(M, ml[j < 2 ? j : 2 * (j - 1)]);
+  if constexpr (PIECES) {
+    const int P = p.max_partitions;
+    entries = P;
+    for (int base = 0; base < P; base += kWave) {
+      const int j = base + lane;
+      const bool in = j < P;
+      const float e = in ? es[j] : 0.0f;
+      const float m = in ? ml[j] : -__builtin_huge_valf();
+      const unsigned long long z = __ballot(e == 0.0f);
+      const int t = z != 0 ? __ffsll(static_cast<long long>(z)) - 1 : kWave;
+      if (lane < t) M = fmaxf(M, m);
+      if (z != 0) {
+        entries = base + t;
+        break;
+      }
+    }
+  } else {
+    const int n = min((seq_len + kPart - 1) / kPart, p.max_partitions);
+    entries = 2 + (n - 1) / 2;  // slot 0, slot 1, then slot 2 (j - 1)
+    slot1 = n > 1 && es[1] != 0.0f;
+    for (int j = lane; j < entries; j += kWave) {
+      if (j != 1 || slot1) M = fmaxf(M, ml[j < 2 ? j : 2 * (j - 1)]);
+    }
   }
   M = wave_max(M);
   float W = 0.0f;
@@ -709,9 +751,9 @@ __global__ __launch_bounds__(reduce_waves<WPH>() * kWave) void paged_attention_r
 #pragma unroll
   for (int c = 0; c < C; ++c) acc[c] = 0.0f;
 #pragma unroll 4
-  for (int j = sub; j < units; j += WPH) {
-    if (j == 1 && !slot1) continue;
-    const int i = j < 2 ? j : 2 * (j - 1);
+  for (int j = sub; j < entries; j += WPH) {
+    if (!PIECES && j == 1 && !slot1) continue;
+    const int i = PIECES ? j : (j < 2 ? j : 2 * (j - 1));
     const float w = es[i] * __builtin_amdgcn_exp2f((ml[i] - M) * kLog2e);
     W += w;
     const float* t = tmp + static_cast<int64_t>(i) * D;
@@ -753,15 +795,15 @@ constexpr int waves_per_group() {
   return D >= 256 ? DK_ATTN_WAVES_D256 : kWaves;
 }
 
-// Launches the grid kernel (PERSIST = false, one workgroup per unit slot) or
-// the persistent kernel for KV pointers aligned to ALIGN bytes. With
-// `resident`, only reports how many persistent workgroups fit on the current
-// device at once (0 if unknown), cached per device.
-template <typename E, int D, int ALIGN, bool SPLIT, bool BS16, bool PERSIST>
+// Launches the grid kernel (BALANCED = false, one workgroup per unit slot) or
+// the balanced kernel for KV pointers aligned to ALIGN bytes. With
+// `resident`, only reports how many balanced-kernel workgroups fit on the
+// current device at once (0 if unknown), cached per device.
+template <typename E, int D, int ALIGN, bool SPLIT, bool BS16, bool BALANCED>
 hipError_t launch_kernel(const KParams& kp, unsigned grid, hipStream_t stream, int* resident = nullptr) {
   constexpr int NW = waves_per_group<D>();
-  if constexpr (PERSIST) {
-    const auto kernel = paged_attention_persistent_kernel<E, D, BS16, ALIGN, NW>;
+  if constexpr (BALANCED) {
+    const auto kernel = paged_attention_balanced_kernel<E, D, BS16, ALIGN, NW>;
     if (resident != nullptr) {
       static std::atomic<int> cache[kMaxDevices];
       *resident = 0;
@@ -789,55 +831,75 @@ hipError_t launch_kernel(const KParams& kp, unsigned grid, hipStream_t stream, i
   return hipGetLastError();
 }
 
-template <typename E, int D, bool SPLIT, bool BS16, bool PERSIST>
+template <typename E, int D, bool SPLIT, bool BS16, bool BALANCED>
 hipError_t launch_aligned(const KParams& kp, unsigned grid, int align, hipStream_t stream, int* resident = nullptr) {
   switch (align) {
     case 16:
-      return launch_kernel<E, D, 16, SPLIT, BS16, PERSIST>(kp, grid, stream, resident);
+      return launch_kernel<E, D, 16, SPLIT, BS16, BALANCED>(kp, grid, stream, resident);
     case 8:
-      if constexpr (D <= 128) return launch_kernel<E, D, 8, SPLIT, BS16, PERSIST>(kp, grid, stream, resident);
+      if constexpr (D <= 128) return launch_kernel<E, D, 8, SPLIT, BS16, BALANCED>(kp, grid, stream, resident);
       return hipErrorInvalidValue;
     case 4:
-      if constexpr (D == 64) return launch_kernel<E, D, 4, SPLIT, BS16, PERSIST>(kp, grid, stream, resident);
+      if constexpr (D == 64) return launch_kernel<E, D, 4, SPLIT, BS16, BALANCED>(kp, grid, stream, resident);
       return hipErrorInvalidValue;
     default:
       return hipErrorInvalidValue;
   }
 }
 
-// DK_ATTN_SCHEDULE=grid|persistent forces the split-K schedule (tests and
+// DK_ATTN_SCHEDULE=grid|balanced forces the split-K schedule (tests and
 // tuning compare the two on one input); unset or anything else: automatic.
-enum class Schedule { kAuto, kGrid, kPersistent };
+enum class Schedule { kAuto, kGrid, kBalanced };
 inline Schedule forced_schedule() {
   const char* v = std::getenv("DK_ATTN_SCHEDULE");
   if (v == nullptr) return Schedule::kAuto;
   if (std::strcmp(v, "grid") == 0) return Schedule::kGrid;
-  if (std::strcmp(v, "persistent") == 0) return Schedule::kPersistent;
+  if (std::strcmp(v, "balanced") == 0) return Schedule::kBalanced;
   return Schedule::kAuto;
+}
+
+template <int D, int WPH, bool PIECES, typename E>
+void launch_reduce(const KParams& kp, int num_seqs, hipStream_t stream) {
+  constexpr int HPW = reduce_waves<WPH>() / WPH;
+  const dim3 grid((kp.num_q_heads + HPW - 1) / HPW, num_seqs);
+  hipLaunchKernelGGL((paged_attention_reduce_kernel<E, D, WPH, PIECES>), grid, dim3(reduce_waves<WPH>() * kWave), 0,
+                     stream, kp);
+}
+
+template <typename E, int D, bool PIECES>
+void launch_reduce_sized(const KParams& kp, int num_seqs, hipStream_t stream) {
+  // Rows a head merges at most.
+  const int entries = PIECES ? kp.max_partitions : 2 + (kp.max_partitions - 1) / 2;
+  if (entries <= 8) launch_reduce<D, 1, PIECES, E>(kp, num_seqs, stream);
+  else if (entries < 64) launch_reduce<D, 4, PIECES, E>(kp, num_seqs, stream);
+  else launch_reduce<D, 16, PIECES, E>(kp, num_seqs, stream);
 }
 
 template <typename E, int D, bool BS16>
 hipError_t launch_split(KParams kp, int num_kv_heads, int num_seqs, int align, hipStream_t stream) {
   const int64_t per_plane = static_cast<int64_t>(num_kv_heads) * num_seqs;
   const int64_t grid_units = per_plane * (kp.num_units + 1);  // 1024-token planes + two 512-token planes
-  // The persistent kernel pays a counter reset, a unit-list setup and a
-  // microseconds-long counter round trip per unit; it wins when the grid
-  // would be mostly positions past their sequence's end: many positions per
-  // sequence, enough sequences for their lengths to differ, and a grid several
-  // times the resident workgroups.
+  // The balanced kernel needs the whole length list in LDS and tile counts
+  // below 2^31; it pays a short set-up (a scan of the lengths) and wins once
+  // the grid would be more than one round of resident workgroups.
   const Schedule forced = forced_schedule();
+  const int64_t tile_bound = per_plane * kp.max_partitions * (kPart / kTile);
   int resident = 0;
-  if (num_seqs <= kMaxPersistSeqs && kp.unit_counter != nullptr && forced != Schedule::kGrid &&
-      ((kp.num_units >= 8 && num_seqs >= 16) || forced == Schedule::kPersistent)) {
+  if (num_seqs <= kMaxBalancedSeqs && tile_bound < (int64_t{1} << 30) && forced != Schedule::kGrid) {
     const hipError_t e = launch_aligned<E, D, true, BS16, true>(kp, 0, align, stream, &resident);
     if (e != hipSuccess) return e;
   }
-  if (resident <= 0 || (forced != Schedule::kPersistent && grid_units <= 4 * static_cast<int64_t>(resident)))
-    return launch_aligned<E, D, true, BS16, false>(kp, static_cast<unsigned>(grid_units), align, stream);
-  hipLaunchKernelGGL(zero_counter_kernel, dim3(1), dim3(kWave), 0, stream, kp.unit_counter);
-  const int64_t units_bound = per_plane * kp.num_units;
-  const unsigned grid = static_cast<unsigned>(units_bound < resident ? units_bound : resident);
-  return launch_aligned<E, D, true, BS16, true>(kp, grid, align, stream);
+  hipError_t e;
+  const bool balanced = resident > 0 && (forced == Schedule::kBalanced || grid_units > resident);
+  if (balanced) {
+    e = launch_aligned<E, D, true, BS16, true>(kp, static_cast<unsigned>(resident), align, stream);
+  } else {
+    e = launch_aligned<E, D, true, BS16, false>(kp, static_cast<unsigned>(grid_units), align, stream);
+  }
+  if (e != hipSuccess) return e;
+  if (balanced) launch_reduce_sized<E, D, true>(kp, num_seqs, stream);
+  else launch_reduce_sized<E, D, false>(kp, num_seqs, stream);
+  return hipGetLastError();
 }
 
 template <typename E, int D>
@@ -848,22 +910,8 @@ hipError_t launch(const KParams& kp, int num_kv_heads, int num_seqs, bool split,
     return bs16 ? launch_aligned<E, D, false, true, false>(kp, grid, align, stream)
                 : launch_aligned<E, D, false, false, false>(kp, grid, align, stream);
   }
-  hipError_t e = bs16 ? launch_split<E, D, true>(kp, num_kv_heads, num_seqs, align, stream)
-                      : launch_split<E, D, false>(kp, num_kv_heads, num_seqs, align, stream);
-  if (e != hipSuccess) return e;
-  // Slot entries a head merges at most: slots 0, 1 and the even slots.
-  const int entries = 2 + (kp.max_partitions - 1) / 2;
-  if (entries <= 8) {
-    const dim3 rgrid((kp.num_q_heads + 3) / 4, num_seqs);
-    hipLaunchKernelGGL((paged_attention_reduce_kernel<E, D, 1>), rgrid, dim3(4 * kWave), 0, stream, kp);
-  } else if (entries < 64) {
-    hipLaunchKernelGGL((paged_attention_reduce_kernel<E, D, 4>), dim3(kp.num_q_heads, num_seqs), dim3(4 * kWave), 0,
-                       stream, kp);
-  } else {
-    hipLaunchKernelGGL((paged_attention_reduce_kernel<E, D, 16>), dim3(kp.num_q_heads, num_seqs), dim3(16 * kWave), 0,
-                       stream, kp);
-  }
-  return hipGetLastError();
+  return bs16 ? launch_split<E, D, true>(kp, num_kv_heads, num_seqs, align, stream)
+              : launch_split<E, D, false>(kp, num_kv_heads, num_seqs, align, stream);
 }
 
 // Largest of 16/8/4 bytes that every K/V row start is aligned to.
@@ -942,21 +990,17 @@ extern "C" int dk_paged_attention_decode(const dk_paged_attn_params* a, int dtyp
   kp.group = group;
   kp.block_size = a->block_size;
   kp.max_partitions = split ? a->max_partitions : 1;
-  // Split-K: workspace slot p holds tokens [512 p, 512 p + 512) as the
-  // reference's partition p; work units cover one or two slots. Like the
-  // reference, only max_partitions x 512 tokens are read, so a too-small
-  // max_seq_len still bounds every access.
+  // Split-K: the workspace has the reference's shape; its rows hold partial
+  // results either per 512-token slot (grid schedule, as the reference's
+  // partitions) or per piece (balanced schedule). Like the reference, only
+  // max_partitions x 512 tokens are read, so a too-small max_seq_len still
+  // bounds every access.
   kp.num_units = split ? static_cast<int>(ceil_div64(a->max_partitions, 2)) : 1;
   kp.scale_log2 = a->scale * kLog2e;
   if (static_cast<int64_t>(a->num_seqs) * a->num_kv_heads * (kp.num_units + 1) >= (int64_t{1} << 31))
     return fail("paged_attention_decode: num_seqs x num_kv_heads x partitions is too large");
   kp.num_seqs = a->num_seqs;
   kp.num_kv_heads = a->num_kv_heads;
-  // The persistent split-K kernel's unit counter lives in the tmp_out row of
-  // slot 3 of (sequence 0, query head 0): results go to slots 0, 1 and even
-  // slots >= 2, odd slots >= 3 are only ever marked empty in exp_sums, so the
-  // row is neither written nor read as data. Needs max_partitions >= 4.
-  kp.unit_counter = split && a->max_partitions >= 4 ? reinterpret_cast<unsigned*>(a->tmp_out + 3 * head_dim) : nullptr;
 
   const bool bs16 = a->block_size % kTile == 0;
   hipStream_t s = static_cast<hipStream_t>(stream);

@@ -179,36 +179,50 @@ SCHEDULE_CASES = [
 @pytest.mark.parametrize("case", SCHEDULE_CASES, ids=lambda c: f"d{c[0]}_hkv{c[1]}_g{c[2]}_bs{c[3]}_{c[4]}")
 def test_paged_attention_split_k_schedules(case, monkeypatch):
     """Split-K under both schedules -- one workgroup per unit slot, and resident
-    workgroups pulling the live units from a counter -- against the oracle.
-    Both cut the sequences into the same units, so they agree bit for bit."""
+    workgroups with equal tile shares of all sequences -- against the oracle.
+    The two cut the sequences differently (so they may differ in the last
+    bits); each is deterministic from call to call."""
     d, hkv, group, bs, layout, n, max_len, dtype = case
     lens = _log_uniform_lens(n, max_len, seed=d + bs)
     kv = make_paged_kv(lens, hkv, d, bs, dtype, "cuda", layout=layout, seed=d + 1)
     q = _q(n, hkv * group, d, dtype)
-    outs = {}
-    for schedule in ("grid", "persistent"):
+    ref = attention_f32(q, kv.k_cache, kv.v_cache, kv.block_tables, kv.seq_lens)
+    for schedule in ("grid", "balanced"):
         monkeypatch.setenv("DK_ATTN_SCHEDULE", schedule)
-        outs[schedule] = dk.paged_attention_decode(
+        run = lambda: dk.paged_attention_decode(  # noqa: E731
             q, kv.k_cache, kv.v_cache, kv.block_tables, kv.seq_lens, max_seq_len=max_len
         )
-    torch.cuda.synchronize()
-    ref = attention_f32(q, kv.k_cache, kv.v_cache, kv.block_tables, kv.seq_lens)
-    for schedule, out in outs.items():
+        out = run()
+        again = run()
+        torch.cuda.synchronize()
         assert_max_abs(out, ref, dtype, f"{schedule} schedule")
-    assert torch.equal(outs["grid"], outs["persistent"])
+        assert torch.equal(out, again), f"{schedule} schedule is not deterministic"
 
 
-def test_paged_attention_persistent_schedule_short_sequences(monkeypatch):
-    """A generous max_seq_len with only short sequences: every live unit is a
-    tail unit and most grid slots would be empty."""
-    monkeypatch.setenv("DK_ATTN_SCHEDULE", "persistent")
-    lens = [0, 1, 17, 300, 1023, 1024, 1025, 5]
-    kv = make_paged_kv(lens, 4, 128, 16, torch.bfloat16, "cuda", seed=5)
-    q = _q(len(lens), 16, 128, torch.bfloat16)
-    _check_attention(q, kv, torch.bfloat16, max_seq_len=20000)
+# (lens, num_kv_heads, max_seq_len): shapes whose tile shares end inside short
+# streams, a single long stream, a two-row workspace and mostly-empty batches.
+BALANCED_CASES = [
+    ([0, 1, 17, 300, 1023, 1024, 1025, 5], 4, 20000),
+    ([513, 600, 1000, 1024, 700, 520, 999, 1001] * 8, 8, 1024),
+    ([40000], 8, 40000),
+    ([0] * 30 + [3000] + [0] * 30, 2, 3000),
+    ([511, 512, 513] * 40, 1, 600),
+    ([16, 32, 48, 64, 80, 96] * 50, 8, 4096),
+]
 
 
-@pytest.mark.parametrize("schedule", ["auto", "persistent"])
+@pytest.mark.parametrize("case", BALANCED_CASES, ids=lambda c: f"n{len(c[0])}_hkv{c[1]}_max{c[2]}")
+def test_paged_attention_balanced_schedule_edge_shapes(case, monkeypatch):
+    monkeypatch.setenv("DK_ATTN_SCHEDULE", "balanced")
+    lens, hkv, max_len = case
+    kv = make_paged_kv(lens, hkv, 128, 16, torch.bfloat16, "cuda", seed=len(lens))
+    q = _q(len(lens), 4 * hkv, 128, torch.bfloat16)
+    out = _check_attention(q, kv, torch.bfloat16, max_seq_len=max_len)
+    if 0 in lens:
+        assert (out[torch.tensor(lens) == 0] == 0).all()
+
+
+@pytest.mark.parametrize("schedule", ["auto", "grid", "balanced"])
 def test_paged_attention_graph_replay(schedule, monkeypatch):
     """Preallocated buffers make the op capturable; replays track new cache
     contents and lengths (within the captured max_seq_len)."""
