@@ -56,16 +56,22 @@ def paged_cache_on_device(seq_lens, num_kv_heads, head_dim, block_size, dtype, l
     g = torch.Generator(device=dev).manual_seed(seed)
     nblk = [-(-n // block_size) for n in seq_lens]
     num_blocks = sum(nblk) + 3
+    fp8 = dtype == torch.float8_e4m3fn
+
+    def randn(*shape):  # fp8: N(0, 1) drawn in fp16, rounded to e4m3fn
+        x = torch.randn(*shape, generator=g, device=dev, dtype=torch.float16 if fp8 else dtype)
+        return x.to(dtype) if fp8 else x
+
     if layout == "vllm":
-        kv = torch.randn(num_blocks, num_kv_heads, block_size, 2 * head_dim, generator=g, device=dev, dtype=dtype)
+        kv = randn(num_blocks, num_kv_heads, block_size, 2 * head_dim)
         k, v = kv.transpose(1, 2).split(head_dim, dim=-1)
     elif layout == "hnd":
-        k = torch.randn(num_blocks, num_kv_heads, block_size, head_dim, generator=g, device=dev, dtype=dtype).transpose(1, 2)
-        v = torch.randn(num_blocks, num_kv_heads, block_size, head_dim, generator=g, device=dev, dtype=dtype).transpose(1, 2)
+        k = randn(num_blocks, num_kv_heads, block_size, head_dim).transpose(1, 2)
+        v = randn(num_blocks, num_kv_heads, block_size, head_dim).transpose(1, 2)
     else:
-        k = torch.randn(num_blocks, block_size, num_kv_heads, head_dim, generator=g, device=dev, dtype=dtype)
-        v = torch.randn(num_blocks, block_size, num_kv_heads, head_dim, generator=g, device=dev, dtype=dtype)
-    if outlier_frac > 0:
+        k = randn(num_blocks, block_size, num_kv_heads, head_dim)
+        v = randn(num_blocks, block_size, num_kv_heads, head_dim)
+    if outlier_frac > 0 and not fp8:
         rows = torch.rand(num_blocks, block_size, num_kv_heads, 1, generator=g, device=dev) < outlier_frac
         scale = torch.where(rows, 8.0, 1.0).to(dtype)
         k.mul_(scale)
@@ -81,18 +87,24 @@ def paged_cache_on_device(seq_lens, num_kv_heads, head_dim, block_size, dtype, l
     return k, v, bt, lens
 
 
-def attention_case(num_seqs, hq, hkv, d, bs, seq_lens, dtype, layout, seed, q_scale=1.0, outlier_frac=0.0):
-    k, v, bt, lens = paged_cache_on_device(seq_lens, hkv, d, bs, dtype, layout, seed, outlier_frac)
+def attention_case(num_seqs, hq, hkv, d, bs, seq_lens, dtype, layout, seed, q_scale=1.0, outlier_frac=0.0,
+                   kv_dtype=None, k_scale=1.0, v_scale=1.0):
+    """kv_dtype: the cache's element type (default: dtype); torch.float8_e4m3fn
+    runs the fp8-cache op with the given scales."""
+    kv_dtype = kv_dtype or dtype
+    k, v, bt, lens = paged_cache_on_device(seq_lens, hkv, d, bs, kv_dtype, layout, seed, outlier_frac)
     g = torch.Generator(device="cuda").manual_seed(seed + 1)
     q = torch.randn(num_seqs, hq, d, generator=g, device="cuda", dtype=dtype) * q_scale
     max_len = max(seq_lens)
     out = torch.empty_like(q)
     ws = dk.alloc_workspace(num_seqs, hq, d, max_len, "cuda")
     elt = torch.finfo(dtype).bits // 8
-    nbytes = sum(seq_lens) * 2 * hkv * d * elt + 2 * q.numel() * elt
+    kv_elt = torch.finfo(kv_dtype).bits // 8
+    nbytes = sum(seq_lens) * 2 * hkv * d * kv_elt + 2 * q.numel() * elt
+    scales = dict(k_scale=k_scale, v_scale=v_scale) if kv_dtype == torch.float8_e4m3fn else {}
 
     def run():
-        dk.paged_attention_decode(q, k, v, bt, lens, max_seq_len=max_len, out=out, workspace=ws)
+        dk.paged_attention_decode(q, k, v, bt, lens, max_seq_len=max_len, out=out, workspace=ws, **scales)
 
     return dict(q=q, k=k, v=v, bt=bt, lens=lens, out=out, run=run, bytes=nbytes, seq_lens=seq_lens, dtype=dtype)
 
@@ -176,6 +188,17 @@ def extras_attention() -> dict:
         gbs = c["bytes"] / (t["median_us"] * 1e-6) / 1e9
         res[f"d256_g8_stress_{tag}"] = {**t, "GB/s": round(gbs, 1), "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 1),
                                         "MB": round(c["bytes"] / 1e6, 1)}
+        del c
+    # fp8 (e4m3fn) KV cache, bf16 queries: the headline batch and 128K batch 1
+    # (half the bytes of the 16-bit cache; GB/s counts the fp8 bytes).
+    llama_lens = torch.randint(512, 4097, (64,), generator=torch.Generator().manual_seed(0)).tolist()
+    for name, args in (("fp8_kv_llama3_8b_b64", (64, 32, 8, 128, 16, llama_lens, torch.bfloat16, "vllm")),
+                       ("fp8_kv_128k_b1", (1, 32, 8, 128, 16, [131072], torch.bfloat16, "hnd"))):
+        c = attention_case(*args, seed=60, q_scale=128**-0.5, kv_dtype=torch.float8_e4m3fn, k_scale=0.5, v_scale=0.5)
+        t = time_cold(c["run"], iters=20)
+        gbs = c["bytes"] / (t["median_us"] * 1e-6) / 1e9
+        res[name] = {**t, "GB/s": round(gbs, 1), "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 1),
+                     "MB": round(c["bytes"] / 1e6, 1)}
         del c
     return res
 

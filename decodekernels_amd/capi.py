@@ -116,6 +116,11 @@ _SIGNATURES = {
         ctypes.c_int,
         [ctypes.POINTER(PagedAttnParams), ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p],
     ),
+    "dk_paged_attention_decode_fp8": (
+        ctypes.c_int,
+        [ctypes.POINTER(PagedAttnParams), ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_float, ctypes.c_float]
+        + [ctypes.c_void_p],
+    ),
     "dk_gemm_tn": (
         ctypes.c_int,
         [ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p]

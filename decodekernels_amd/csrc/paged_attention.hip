@@ -34,6 +34,7 @@
 #include <atomic>
 #include <cstdlib>
 #include <cstring>
+#include <type_traits>
 
 #include "../../include/decodekernels_amd.h"
 #include "dk_device.h"
@@ -56,6 +57,15 @@ constexpr int kUnit = 2 * kPart;          // split-K work unit: two slots (its b
 #endif
 #ifndef DK_ATTN_DEPTH_D256
 #define DK_ATTN_DEPTH_D256 2  // tiles in flight per wave (head_dim 256)
+#endif
+#ifndef DK_ATTN_DEPTH_FP8
+#define DK_ATTN_DEPTH_FP8 2  // tiles in flight per wave with an fp8 cache
+#endif
+#ifndef DK_ATTN_OCC_FP8_D128
+#define DK_ATTN_OCC_FP8_D128 3  // waves per SIMD targeted at head_dim 128 with an fp8 cache
+#endif
+#ifndef DK_ATTN_OCC_FP8_D256
+#define DK_ATTN_OCC_FP8_D256 1  // waves per SIMD targeted at head_dim 256 with an fp8 cache
 #endif
 #ifndef DK_ATTN_LOAD_AUX
 #define DK_ATTN_LOAD_AUX 0  // cache-policy bits of the K/V buffer loads
@@ -88,7 +98,8 @@ struct KParams {
   int num_q_heads, group, block_size, max_partitions;
   int num_seqs, num_kv_heads;
   int num_units;  // split-K grid: unit positions per sequence, ceil(max_partitions / 2)
-  float scale_log2;
+  float scale_log2;  // softmax scale x log2(e) (x k_scale for an fp8 cache)
+  float v_scale;     // multiplies the output (fp8 cache's v_scale; 1 otherwise)
 };
 
 
@@ -125,11 +136,30 @@ __device__ __forceinline__ u32x2 bload4(__amdgpu_buffer_rsrc_t r, int off) {
 // One 16-token tile in registers: lane l holds 8 consecutive elements
 // (columns 8*(l/16) + 32*c ...) of K row l%16 and of V row l%16, for every
 // 32-column chunk c -- the A-operand layout of v_mfma_f32_16x16x32.
-template <int CHUNKS>
+template <int CHUNKS, bool KV8>
 struct TileRegs {
   u32x4 k[CHUNKS];
   u32x4 v[CHUNKS];
 };
+
+// An fp8 (e4m3fn) cache tile: lane l holds the same 8 columns as raw bytes.
+template <int CHUNKS>
+struct TileRegs<CHUNKS, true> {
+  u32x2 k[CHUNKS];
+  u32x2 v[CHUNKS];
+};
+
+// 8 e4m3fn bytes -> 8 elements of E, exactly (every e4m3fn value is a bf16
+// and an fp16 value); v_cvt_pk_f32_fp8 matches torch.float8_e4m3fn on all
+// 256 encodings (checked on the device).
+template <typename E>
+__device__ __forceinline__ u32x4 fp8x8_to(u32x2 w) {
+  const auto a = __builtin_amdgcn_cvt_pk_f32_fp8(w[0], false);
+  const auto b = __builtin_amdgcn_cvt_pk_f32_fp8(w[0], true);
+  const auto c = __builtin_amdgcn_cvt_pk_f32_fp8(w[1], false);
+  const auto d = __builtin_amdgcn_cvt_pk_f32_fp8(w[1], true);
+  return u32x4{pack2<E>(a[0], a[1]), pack2<E>(b[0], b[1]), pack2<E>(c[0], c[1]), pack2<E>(d[0], d[1])};
+}
 
 // Log2-units headroom of the lazy running max: exponentials are taken
 // against a reference max that only moves when a tile exceeds it by more
@@ -139,8 +169,9 @@ constexpr float kLazyMax = 8.0f;
 // Waves per SIMD the register allocation targets: head_dim 64 fits four and
 // head_dim 128 three without spilling; head_dim 256 keeps its natural
 // allocation (one wave, no spills).
-template <int D>
+template <int D, bool KV8 = false>
 constexpr int attn_occupancy() {
+  if constexpr (KV8) return D >= 256 ? DK_ATTN_OCC_FP8_D256 : (D == 128 ? DK_ATTN_OCC_FP8_D128 : DK_ATTN_OCC_D64);
   return D >= 256 ? 1 : (D == 128 ? DK_ATTN_OCC_D128 : DK_ATTN_OCC_D64);
 }
 
@@ -179,13 +210,13 @@ __device__ __forceinline__ void lds_barrier() {
 // keeps DEPTH tiles of loads in flight and its own online-softmax state; the
 // waves merge through LDS. The steps are separate so that the balanced
 // kernel can issue the next unit's loads before merging the current one.
-template <typename E, int D, bool SPLIT, bool BS16, int ALIGN, int NW>
+template <typename E, int D, bool SPLIT, bool BS16, int ALIGN, int NW, bool KV8>
 struct UnitEngine {
   static constexpr int CH = D / 32;  // 32-column chunks per row
   static constexpr int NB = D / 16;  // 16-column output blocks
-  static constexpr int DEPTH = D >= 256 ? DK_ATTN_DEPTH_D256 : DK_ATTN_DEPTH;
+  static constexpr int DEPTH = KV8 ? DK_ATTN_DEPTH_FP8 : (D >= 256 ? DK_ATTN_DEPTH_D256 : DK_ATTN_DEPTH);
   static constexpr int NT = NW * kWave;
-  using Tile = TileRegs<CH>;
+  using Tile = TileRegs<CH, KV8>;
 
   const KParams& p;
   UnitSmem<D, NW>& sm;
@@ -266,36 +297,57 @@ struct UnitEngine {
     const int tt = live ? tile : nt - 1;
     const int t0 = u.start + tt * kTile;
     const int row = min(l16, u.end - 1 - t0);
-    const uint16_t* kbase = p.k + u.kv_head * p.k_sh;
-    const uint16_t* vbase = p.v + u.kv_head * p.v_sh;
+    // Element pointers of the K / V cache (bytes for fp8, 16-bit otherwise).
+    using KvT = typename std::conditional<KV8, uint8_t, uint16_t>::type;
+    constexpr int kElt = sizeof(KvT);
+    const KvT* kbase = reinterpret_cast<const KvT*>(p.k) + u.kv_head * p.k_sh;
+    const KvT* vbase = reinterpret_cast<const KvT*>(p.v) + u.kv_head * p.v_sh;
     if constexpr (BS16) {
       const int lb = t0 / p.block_size;
       const int phys = __builtin_amdgcn_readlane(bt_lane, lb - u.start / p.block_size);
       const int off = t0 - lb * p.block_size;
-      const uint16_t* kt = kbase + static_cast<int64_t>(phys) * p.k_sb + static_cast<int64_t>(off) * p.k_st;
-      const uint16_t* vt = vbase + static_cast<int64_t>(phys) * p.v_sb + static_cast<int64_t>(off) * p.v_st;
+      const KvT* kt = kbase + static_cast<int64_t>(phys) * p.k_sb + static_cast<int64_t>(off) * p.k_st;
+      const KvT* vt = vbase + static_cast<int64_t>(phys) * p.v_sb + static_cast<int64_t>(off) * p.v_st;
       const int nrec = live ? 0x7fffffff : 0;
-      const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(kt), 0, nrec, kRsrcWord3);
-      const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(vt), 0, nrec, kRsrcWord3);
-      const int koff = 2 * (row * static_cast<int>(p.k_st) + 8 * lg);
-      const int voff = 2 * (row * static_cast<int>(p.v_st) + 8 * lg);
+      const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(const_cast<KvT*>(kt), 0, nrec, kRsrcWord3);
+      const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(const_cast<KvT*>(vt), 0, nrec, kRsrcWord3);
+      const int koff = kElt * (row * static_cast<int>(p.k_st) + 8 * lg);
+      const int voff = kElt * (row * static_cast<int>(p.v_st) + 8 * lg);
+      if constexpr (KV8) {
 #pragma unroll
-      for (int c = 0; c < CH; ++c) r.k[c] = bload8<ALIGN>(rk, koff + 64 * c);
+        for (int c = 0; c < CH; ++c) r.k[c] = __builtin_amdgcn_raw_buffer_load_b64(rk, koff + 32 * c, 0, DK_ATTN_LOAD_AUX);
 #pragma unroll
-      for (int c = 0; c < CH; ++c) r.v[c] = bload8<ALIGN>(rv, voff + 64 * c);
+        for (int c = 0; c < CH; ++c) r.v[c] = __builtin_amdgcn_raw_buffer_load_b64(rv, voff + 32 * c, 0, DK_ATTN_LOAD_AUX);
+      } else {
+#pragma unroll
+        for (int c = 0; c < CH; ++c) r.k[c] = bload8<ALIGN>(rk, koff + 64 * c);
+#pragma unroll
+        for (int c = 0; c < CH; ++c) r.v[c] = bload8<ALIGN>(rv, voff + 64 * c);
+      }
     } else {
       const int t = t0 + row;
       const int lb = t / p.block_size;
       const int64_t phys = p.block_tables[u.seq * p.bt_stride + lb];
       const int64_t off = t - lb * p.block_size;
-      const uint16_t* kp = kbase + phys * p.k_sb + off * p.k_st + 8 * lg;
-      const uint16_t* vp = vbase + phys * p.v_sb + off * p.v_st + 8 * lg;
+      const KvT* kp = kbase + phys * p.k_sb + off * p.k_st + 8 * lg;
+      const KvT* vp = vbase + phys * p.v_sb + off * p.v_st + 8 * lg;
+      if constexpr (KV8) {
 #pragma unroll
-      for (int c = 0; c < CH; ++c) r.k[c] = load8<ALIGN>(kp + 32 * c);
+        for (int c = 0; c < CH; ++c) r.k[c] = *reinterpret_cast<const u32x2*>(kp + 32 * c);
 #pragma unroll
-      for (int c = 0; c < CH; ++c) r.v[c] = load8<ALIGN>(vp + 32 * c);
+        for (int c = 0; c < CH; ++c) r.v[c] = *reinterpret_cast<const u32x2*>(vp + 32 * c);
+      } else {
+#pragma unroll
+        for (int c = 0; c < CH; ++c) r.k[c] = load8<ALIGN>(kp + 32 * c);
+#pragma unroll
+        for (int c = 0; c < CH; ++c) r.v[c] = load8<ALIGN>(vp + 32 * c);
+      }
     }
   }
+
+  // A tile chunk as an MFMA operand in the model dtype.
+  __device__ __forceinline__ static u32x4 kv_operand(const u32x4& w) { return w; }
+  __device__ __forceinline__ static u32x4 kv_operand(const u32x2& w) { return fp8x8_to<E>(w); }
 
   // The first DEPTH tiles of this wave. The scheduling barriers keep the
   // tiles' load groups in program order, so the oldest outstanding loads are
@@ -313,7 +365,7 @@ struct UnitEngine {
     // Q·Kᵀ: S[token 4*lg + i][head l16].
     f32x4 s = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int c = 0; c < CH; ++c) s = E::mfma_16x16x32(r.k[c], qf[c], s);
+    for (int c = 0; c < CH; ++c) s = E::mfma_16x16x32(kv_operand(r.k[c]), qf[c], s);
 
     const int t0 = u.start + tile * kTile;
     float x[4];
@@ -353,8 +405,9 @@ struct UnitEngine {
 #pragma unroll
     for (int c = 0; c < CH; ++c) {
       const f32x4 z = {0.f, 0.f, 0.f, 0.f};
-      const f32x4 t_lo = E::mfma_16x16x32(r.v[c], eye0, z);  // columns 32c + l16
-      const f32x4 t_hi = E::mfma_16x16x32(r.v[c], eye1, z);  // columns 32c + 16 + l16
+      const u32x4 vc = kv_operand(r.v[c]);
+      const f32x4 t_lo = E::mfma_16x16x32(vc, eye0, z);  // columns 32c + l16
+      const f32x4 t_hi = E::mfma_16x16x32(vc, eye1, z);  // columns 32c + 16 + l16
       const u32x2 v_lo = {pack2<E>(t_lo[0], t_lo[1]), pack2<E>(t_lo[2], t_lo[3])};
       const u32x2 v_hi = {pack2<E>(t_hi[0], t_hi[1]), pack2<E>(t_hi[2], t_hi[3])};
       acc[2 * c] = E::mfma_16x16x16(p_hi, v_lo, acc[2 * c]);
@@ -417,7 +470,7 @@ struct UnitEngine {
         L += f * sm.l[w][h];
         O += f * sm.o[w][h][d];
       }
-      const float res = O / L;
+      const float res = O / L * p.v_scale;
       const int q_head = u.kv_head * group + h;
       if constexpr (SPLIT) {
         const int64_t row = (static_cast<int64_t>(u.seq) * p.num_q_heads + q_head) * p.max_partitions + u.slot;
@@ -450,8 +503,9 @@ struct UnitEngine {
 // i mod 8, and without the rotation every unit of a (sequence, KV head) would
 // land on one XCD, where a few long sequences would keep it busy long after
 // the others are idle.
-template <typename E, int D, bool SPLIT, bool BS16, int ALIGN, int NW>
-__global__ __launch_bounds__(NW * kWave) __attribute__((amdgpu_waves_per_eu(attn_occupancy<D>(), attn_occupancy<D>())))
+template <typename E, int D, bool SPLIT, bool BS16, int ALIGN, int NW, bool KV8>
+__global__ __launch_bounds__(NW * kWave) __attribute__((amdgpu_waves_per_eu(attn_occupancy<D, KV8>(),
+                                                                            attn_occupancy<D, KV8>())))
 void paged_attention_kernel(const KParams p) {
   __shared__ UnitSmem<D, NW> sm;
   const int per_plane = p.num_seqs * p.num_kv_heads;
@@ -483,7 +537,7 @@ void paged_attention_kernel(const KParams p) {
     }
     return;
   }
-  UnitEngine<E, D, SPLIT, BS16, ALIGN, NW> eng(p, sm);
+  UnitEngine<E, D, SPLIT, BS16, ALIGN, NW, KV8> eng(p, sm);
   const Unit u = make_unit(kv_head, seq, start, unit_tokens, seq_len, start / kPart);
   const int bt = eng.load_bt(u);
   eng.load_q(u);
@@ -521,8 +575,9 @@ constexpr int kMinShareTiles = 64;
 #endif
 constexpr int kStreamCost = DK_ATTN_STREAM_COST;
 
-template <typename E, int D, bool BS16, int ALIGN, int NW>
-__global__ __launch_bounds__(NW * kWave) __attribute__((amdgpu_waves_per_eu(attn_occupancy<D>(), attn_occupancy<D>())))
+template <typename E, int D, bool BS16, int ALIGN, int NW, bool KV8>
+__global__ __launch_bounds__(NW * kWave) __attribute__((amdgpu_waves_per_eu(attn_occupancy<D, KV8>(),
+                                                                            attn_occupancy<D, KV8>())))
 void paged_attention_balanced_kernel(const KParams p) {
   constexpr int NT = NW * kWave;
   __shared__ UnitSmem<D, NW> sm;
@@ -632,7 +687,7 @@ void paged_attention_balanced_kernel(const KParams p) {
   };
 
   if (!enter_stream()) return;
-  UnitEngine<E, D, true, BS16, ALIGN, NW> eng(p, sm);
+  UnitEngine<E, D, true, BS16, ALIGN, NW, KV8> eng(p, sm);
   Sub cur = make_sub();
   int cur_bt = eng.load_bt(cur.unit);
   eng.load_q(cur.unit);
@@ -799,11 +854,11 @@ constexpr int waves_per_group() {
 // the balanced kernel for KV pointers aligned to ALIGN bytes. With
 // `resident`, only reports how many balanced-kernel workgroups fit on the
 // current device at once (0 if unknown), cached per device.
-template <typename E, int D, int ALIGN, bool SPLIT, bool BS16, bool BALANCED>
+template <typename E, int D, int ALIGN, bool SPLIT, bool BS16, bool BALANCED, bool KV8>
 hipError_t launch_kernel(const KParams& kp, unsigned grid, hipStream_t stream, int* resident = nullptr) {
   constexpr int NW = waves_per_group<D>();
   if constexpr (BALANCED) {
-    const auto kernel = paged_attention_balanced_kernel<E, D, BS16, ALIGN, NW>;
+    const auto kernel = paged_attention_balanced_kernel<E, D, BS16, ALIGN, NW, KV8>;
     if (resident != nullptr) {
       static std::atomic<int> cache[kMaxDevices];
       *resident = 0;
@@ -825,25 +880,30 @@ hipError_t launch_kernel(const KParams& kp, unsigned grid, hipStream_t stream, i
     }
     hipLaunchKernelGGL(kernel, dim3(grid), dim3(NW * kWave), 0, stream, kp);
   } else {
-    hipLaunchKernelGGL((paged_attention_kernel<E, D, SPLIT, BS16, ALIGN, NW>), dim3(grid), dim3(NW * kWave), 0, stream,
+    hipLaunchKernelGGL((paged_attention_kernel<E, D, SPLIT, BS16, ALIGN, NW, KV8>), dim3(grid), dim3(NW * kWave), 0, stream,
                        kp);
   }
   return hipGetLastError();
 }
 
-template <typename E, int D, bool SPLIT, bool BS16, bool BALANCED>
+template <typename E, int D, bool SPLIT, bool BS16, bool BALANCED, bool KV8>
 hipError_t launch_aligned(const KParams& kp, unsigned grid, int align, hipStream_t stream, int* resident = nullptr) {
-  switch (align) {
-    case 16:
-      return launch_kernel<E, D, 16, SPLIT, BS16, BALANCED>(kp, grid, stream, resident);
-    case 8:
-      if constexpr (D <= 128) return launch_kernel<E, D, 8, SPLIT, BS16, BALANCED>(kp, grid, stream, resident);
-      return hipErrorInvalidValue;
-    case 4:
-      if constexpr (D == 64) return launch_kernel<E, D, 4, SPLIT, BS16, BALANCED>(kp, grid, stream, resident);
-      return hipErrorInvalidValue;
-    default:
-      return hipErrorInvalidValue;
+  if constexpr (KV8) {
+    // fp8 rows: 8-byte loads (checked by the host).
+    return launch_kernel<E, D, 8, SPLIT, BS16, BALANCED, true>(kp, grid, stream, resident);
+  } else {
+    switch (align) {
+      case 16:
+        return launch_kernel<E, D, 16, SPLIT, BS16, BALANCED, false>(kp, grid, stream, resident);
+      case 8:
+        if constexpr (D <= 128) return launch_kernel<E, D, 8, SPLIT, BS16, BALANCED, false>(kp, grid, stream, resident);
+        return hipErrorInvalidValue;
+      case 4:
+        if constexpr (D == 64) return launch_kernel<E, D, 4, SPLIT, BS16, BALANCED, false>(kp, grid, stream, resident);
+        return hipErrorInvalidValue;
+      default:
+        return hipErrorInvalidValue;
+    }
   }
 }
 
@@ -875,7 +935,7 @@ void launch_reduce_sized(const KParams& kp, int num_seqs, hipStream_t stream) {
   else launch_reduce<D, 16, PIECES, E>(kp, num_seqs, stream);
 }
 
-template <typename E, int D, bool BS16>
+template <typename E, int D, bool BS16, bool KV8>
 hipError_t launch_split(KParams kp, int num_kv_heads, int num_seqs, int align, hipStream_t stream) {
   const int64_t per_plane = static_cast<int64_t>(num_kv_heads) * num_seqs;
   const int64_t grid_units = per_plane * (kp.num_units + 1);  // 1024-token planes + two 512-token planes
@@ -886,15 +946,15 @@ hipError_t launch_split(KParams kp, int num_kv_heads, int num_seqs, int align, h
   const int64_t tile_bound = per_plane * kp.max_partitions * (kPart / kTile);
   int resident = 0;
   if (num_seqs <= kMaxBalancedSeqs && tile_bound < (int64_t{1} << 30) && forced != Schedule::kGrid) {
-    const hipError_t e = launch_aligned<E, D, true, BS16, true>(kp, 0, align, stream, &resident);
+    const hipError_t e = launch_aligned<E, D, true, BS16, true, KV8>(kp, 0, align, stream, &resident);
     if (e != hipSuccess) return e;
   }
   hipError_t e;
   const bool balanced = resident > 0 && (forced == Schedule::kBalanced || grid_units > resident);
   if (balanced) {
-    e = launch_aligned<E, D, true, BS16, true>(kp, static_cast<unsigned>(resident), align, stream);
+    e = launch_aligned<E, D, true, BS16, true, KV8>(kp, static_cast<unsigned>(resident), align, stream);
   } else {
-    e = launch_aligned<E, D, true, BS16, false>(kp, static_cast<unsigned>(grid_units), align, stream);
+    e = launch_aligned<E, D, true, BS16, false, KV8>(kp, static_cast<unsigned>(grid_units), align, stream);
   }
   if (e != hipSuccess) return e;
   if (balanced) launch_reduce_sized<E, D, true>(kp, num_seqs, stream);
@@ -902,37 +962,42 @@ hipError_t launch_split(KParams kp, int num_kv_heads, int num_seqs, int align, h
   return hipGetLastError();
 }
 
-template <typename E, int D>
+template <typename E, int D, bool KV8>
 hipError_t launch(const KParams& kp, int num_kv_heads, int num_seqs, bool split, bool bs16, int align,
                   hipStream_t stream) {
   if (!split) {
     const unsigned grid = static_cast<unsigned>(num_kv_heads * num_seqs);
-    return bs16 ? launch_aligned<E, D, false, true, false>(kp, grid, align, stream)
-                : launch_aligned<E, D, false, false, false>(kp, grid, align, stream);
+    return bs16 ? launch_aligned<E, D, false, true, false, KV8>(kp, grid, align, stream)
+                : launch_aligned<E, D, false, false, false, KV8>(kp, grid, align, stream);
   }
-  return bs16 ? launch_split<E, D, true>(kp, num_kv_heads, num_seqs, align, stream)
-              : launch_split<E, D, false>(kp, num_kv_heads, num_seqs, align, stream);
+  return bs16 ? launch_split<E, D, true, KV8>(kp, num_kv_heads, num_seqs, align, stream)
+              : launch_split<E, D, false, KV8>(kp, num_kv_heads, num_seqs, align, stream);
+}
+
+template <typename E, int D>
+hipError_t launch_kv(const KParams& kp, int num_kv_heads, int num_seqs, bool split, bool bs16, int align, bool kv8,
+                     hipStream_t stream) {
+  return kv8 ? launch<E, D, true>(kp, num_kv_heads, num_seqs, split, bs16, align, stream)
+             : launch<E, D, false>(kp, num_kv_heads, num_seqs, split, bs16, align, stream);
 }
 
 // Largest of 16/8/4 bytes that every K/V row start is aligned to.
-int kv_alignment(const dk_paged_attn_params& a) {
+// Largest of 16/8/4 bytes that every K/V row start is aligned to, for
+// elements of `elt` bytes.
+int kv_alignment(const dk_paged_attn_params& a, int elt) {
   const int64_t strides[6] = {a.k_stride_block, a.k_stride_token, a.k_stride_head,
                               a.v_stride_block, a.v_stride_token, a.v_stride_head};
   for (int align : {16, 8, 4}) {
     bool ok = aligned_to(a.k_cache, align) && aligned_to(a.v_cache, align);
-    for (int64_t s : strides) ok = ok && ((s * 2) % align == 0);
+    for (int64_t s : strides) ok = ok && ((s * elt) % align == 0);
     if (ok) return align;
   }
-  return 2;
+  return 1;
 }
 
-}  // namespace attn
-}  // namespace dk
-
-extern "C" int dk_paged_attention_decode(const dk_paged_attn_params* a, int dtype, int head_dim, int max_seq_len,
-                                         void* stream) {
-  using namespace dk;
-  using namespace dk::attn;
+// Both entry points: 16-bit caches (kv8 = false, scales 1) or e4m3fn caches.
+int paged_attention_entry(const dk_paged_attn_params* a, int dtype, int head_dim, int max_seq_len, bool kv8,
+                          float k_scale, float v_scale, void* stream) {
   clear_error();
   if (a == nullptr) return fail("paged_attention_decode: params must not be NULL");
   if (dtype != DK_FLOAT16 && dtype != DK_BFLOAT16)
@@ -950,9 +1015,14 @@ extern "C" int dk_paged_attention_decode(const dk_paged_attn_params* a, int dtyp
   if (a->q == nullptr || a->out == nullptr || a->k_cache == nullptr || a->v_cache == nullptr ||
       a->block_tables == nullptr || a->seq_lens == nullptr)
     return fail("paged_attention_decode: tensor pointers must not be NULL");
-  const int align = kv_alignment(*a);
-  if (align < 4 || (head_dim == 128 && align < 8) || (head_dim == 256 && align < 16))
+  const int align = kv_alignment(*a, kv8 ? 1 : 2);
+  if (kv8) {
+    if (align < 8) return fail("fp8 KV-cache pointers and strides must be multiples of 8 bytes");
+    if (!(k_scale == k_scale && v_scale == v_scale) || __builtin_isinf(k_scale) || __builtin_isinf(v_scale))
+      return fail("paged_attention_decode_fp8: k_scale and v_scale must be finite");
+  } else if (align < 4 || (head_dim == 128 && align < 8) || (head_dim == 256 && align < 16)) {
     return fail("KV-cache pointers must be aligned to head_dim / 16 bytes");
+  }
   if (a->num_seqs > 65535 || a->num_kv_heads > 65535 || a->num_q_heads > 65535)
     return fail("paged_attention_decode: num_seqs and head counts must be at most 65535");
 
@@ -996,7 +1066,8 @@ extern "C" int dk_paged_attention_decode(const dk_paged_attn_params* a, int dtyp
   // max_partitions x 512 tokens are read, so a too-small max_seq_len still
   // bounds every access.
   kp.num_units = split ? static_cast<int>(ceil_div64(a->max_partitions, 2)) : 1;
-  kp.scale_log2 = a->scale * kLog2e;
+  kp.scale_log2 = a->scale * k_scale * kLog2e;
+  kp.v_scale = v_scale;
   if (static_cast<int64_t>(a->num_seqs) * a->num_kv_heads * (kp.num_units + 1) >= (int64_t{1} << 31))
     return fail("paged_attention_decode: num_seqs x num_kv_heads x partitions is too large");
   kp.num_seqs = a->num_seqs;
@@ -1007,16 +1078,29 @@ extern "C" int dk_paged_attention_decode(const dk_paged_attn_params* a, int dtyp
   hipError_t e;
   if (dtype == DK_BFLOAT16) {
     switch (head_dim) {
-      case 64: e = launch<Bf16, 64>(kp, a->num_kv_heads, a->num_seqs, split, bs16, align, s); break;
-      case 128: e = launch<Bf16, 128>(kp, a->num_kv_heads, a->num_seqs, split, bs16, align, s); break;
-      default: e = launch<Bf16, 256>(kp, a->num_kv_heads, a->num_seqs, split, bs16, align, s); break;
+      case 64: e = launch_kv<Bf16, 64>(kp, a->num_kv_heads, a->num_seqs, split, bs16, align, kv8, s); break;
+      case 128: e = launch_kv<Bf16, 128>(kp, a->num_kv_heads, a->num_seqs, split, bs16, align, kv8, s); break;
+      default: e = launch_kv<Bf16, 256>(kp, a->num_kv_heads, a->num_seqs, split, bs16, align, kv8, s); break;
     }
   } else {
     switch (head_dim) {
-      case 64: e = launch<F16, 64>(kp, a->num_kv_heads, a->num_seqs, split, bs16, align, s); break;
-      case 128: e = launch<F16, 128>(kp, a->num_kv_heads, a->num_seqs, split, bs16, align, s); break;
-      default: e = launch<F16, 256>(kp, a->num_kv_heads, a->num_seqs, split, bs16, align, s); break;
+      case 64: e = launch_kv<F16, 64>(kp, a->num_kv_heads, a->num_seqs, split, bs16, align, kv8, s); break;
+      case 128: e = launch_kv<F16, 128>(kp, a->num_kv_heads, a->num_seqs, split, bs16, align, kv8, s); break;
+      default: e = launch_kv<F16, 256>(kp, a->num_kv_heads, a->num_seqs, split, bs16, align, kv8, s); break;
     }
   }
   return static_cast<int>(e);
+}
+
+}  // namespace attn
+}  // namespace dk
+
+extern "C" int dk_paged_attention_decode(const dk_paged_attn_params* a, int dtype, int head_dim, int max_seq_len,
+                                         void* stream) {
+  return dk::attn::paged_attention_entry(a, dtype, head_dim, max_seq_len, false, 1.0f, 1.0f, stream);
+}
+
+extern "C" int dk_paged_attention_decode_fp8(const dk_paged_attn_params* a, int dtype, int head_dim, int max_seq_len,
+                                             float k_scale, float v_scale, void* stream) {
+  return dk::attn::paged_attention_entry(a, dtype, head_dim, max_seq_len, true, k_scale, v_scale, stream);
 }

@@ -73,17 +73,28 @@ int64_t row_stride(const at::Tensor& t, const char* name) {
 // ---------------------------------------------------------------------------
 // paged_attention_decode (csrc/ops.cu:44-144)
 // ---------------------------------------------------------------------------
-void paged_attention_decode(at::Tensor& out, const at::Tensor& q, const at::Tensor& k_cache,
-                            const at::Tensor& v_cache, const at::Tensor& block_tables, const at::Tensor& seq_lens,
-                            double scale, int64_t max_seq_len, at::Tensor& tmp_out, at::Tensor& max_logits,
-                            at::Tensor& exp_sums) {
+namespace {
+
+// Shared by the 16-bit-cache op (the reference's) and the fp8-cache op.
+void attention_impl(at::Tensor& out, const at::Tensor& q, const at::Tensor& k_cache, const at::Tensor& v_cache,
+                    const at::Tensor& block_tables, const at::Tensor& seq_lens, double scale, int64_t max_seq_len,
+                    at::Tensor& tmp_out, at::Tensor& max_logits, at::Tensor& exp_sums, bool fp8, double k_scale,
+                    double v_scale) {
   TORCH_CHECK(q.is_cuda(), "paged_attention_decode: q must be a CUDA tensor");
   TORCH_CHECK(q.dim() == 3 && out.dim() == 3, "q and out must be [num_seqs, num_q_heads, head_dim]");
   TORCH_CHECK(k_cache.dim() == 4 && v_cache.dim() == 4,
               "k_cache and v_cache must be [num_blocks, block_size, num_kv_heads, head_dim]");
   check_same(q, out, "q/out");
-  check_same(q, k_cache, "q/k_cache");
-  check_same(q, v_cache, "q/v_cache");
+  if (fp8) {
+    TORCH_CHECK(k_cache.scalar_type() == at::ScalarType::Float8_e4m3fn &&
+                    v_cache.scalar_type() == at::ScalarType::Float8_e4m3fn,
+                "paged_attention_decode_fp8: k_cache and v_cache must be float8_e4m3fn");
+    TORCH_CHECK(k_cache.device() == q.device() && v_cache.device() == q.device(),
+                "paged_attention_decode_fp8: tensors must be on the same device");
+  } else {
+    check_same(q, k_cache, "q/k_cache");
+    check_same(q, v_cache, "q/v_cache");
+  }
   TORCH_CHECK(out.sizes() == q.sizes(), "out must have the same shape as q");
   TORCH_CHECK(k_cache.sizes() == v_cache.sizes(), "k_cache and v_cache shapes differ");
 
@@ -99,13 +110,22 @@ void paged_attention_decode(at::Tensor& out, const at::Tensor& q, const at::Tens
               " is not supported");
   TORCH_CHECK(q.stride(2) == 1 && out.stride(2) == 1 && k_cache.stride(3) == 1 && v_cache.stride(3) == 1,
               "head_dim must be the contiguous (innermost) dimension");
-  const int64_t vec = head_dim / 32;
-  for (int d = 0; d < 3; ++d) {
-    TORCH_CHECK(k_cache.stride(d) % vec == 0 && v_cache.stride(d) % vec == 0,
-                "KV-cache strides must be multiples of head_dim / 32 for vectorised loads");
+  if (fp8) {
+    for (int d = 0; d < 3; ++d) {
+      TORCH_CHECK(k_cache.stride(d) % 8 == 0 && v_cache.stride(d) % 8 == 0,
+                  "fp8 KV-cache pointers and strides must be multiples of 8 bytes");
+    }
+    TORCH_CHECK(aligned(k_cache.data_ptr(), 8) && aligned(v_cache.data_ptr(), 8),
+                "fp8 KV-cache pointers and strides must be multiples of 8 bytes");
+  } else {
+    const int64_t vec = head_dim / 32;
+    for (int d = 0; d < 3; ++d) {
+      TORCH_CHECK(k_cache.stride(d) % vec == 0 && v_cache.stride(d) % vec == 0,
+                  "KV-cache strides must be multiples of head_dim / 32 for vectorised loads");
+    }
+    TORCH_CHECK(aligned(k_cache.data_ptr(), vec * 2) && aligned(v_cache.data_ptr(), vec * 2),
+                "KV-cache pointers must be aligned to head_dim / 16 bytes");
   }
-  TORCH_CHECK(aligned(k_cache.data_ptr(), vec * 2) && aligned(v_cache.data_ptr(), vec * 2),
-              "KV-cache pointers must be aligned to head_dim / 16 bytes");
   TORCH_CHECK(block_tables.scalar_type() == at::kInt && block_tables.dim() == 2 && block_tables.stride(1) == 1,
               "block_tables must be a 2-D int32 tensor with a contiguous last dimension");
   TORCH_CHECK(seq_lens.scalar_type() == at::kInt && seq_lens.dim() == 1 && seq_lens.is_contiguous(),
@@ -163,9 +183,35 @@ void paged_attention_decode(at::Tensor& out, const at::Tensor& q, const at::Tens
 
   const int dt = dtype_code(q.scalar_type(), "paged_attention_decode");
   const DeviceGuard guard(q.device());
-  check_status(dk_paged_attention_decode(&p, dt, static_cast<int>(head_dim), static_cast<int>(max_seq_len),
-                                         stream_of(q)),
-               "paged_attention_decode");
+  if (fp8) {
+    check_status(dk_paged_attention_decode_fp8(&p, dt, static_cast<int>(head_dim), static_cast<int>(max_seq_len),
+                                               static_cast<float>(k_scale), static_cast<float>(v_scale), stream_of(q)),
+                 "paged_attention_decode_fp8");
+  } else {
+    check_status(dk_paged_attention_decode(&p, dt, static_cast<int>(head_dim), static_cast<int>(max_seq_len),
+                                           stream_of(q)),
+                 "paged_attention_decode");
+  }
+}
+
+}  // namespace
+
+void paged_attention_decode(at::Tensor& out, const at::Tensor& q, const at::Tensor& k_cache,
+                            const at::Tensor& v_cache, const at::Tensor& block_tables, const at::Tensor& seq_lens,
+                            double scale, int64_t max_seq_len, at::Tensor& tmp_out, at::Tensor& max_logits,
+                            at::Tensor& exp_sums) {
+  attention_impl(out, q, k_cache, v_cache, block_tables, seq_lens, scale, max_seq_len, tmp_out, max_logits, exp_sums,
+                 false, 1.0, 1.0);
+}
+
+// The same op over an fp8 (e4m3fn) KV cache with per-tensor scales; no
+// counterpart in the reference (README.md:185 lists FP8 KV as unsupported).
+void paged_attention_decode_fp8(at::Tensor& out, const at::Tensor& q, const at::Tensor& k_cache,
+                                const at::Tensor& v_cache, const at::Tensor& block_tables, const at::Tensor& seq_lens,
+                                double scale, int64_t max_seq_len, at::Tensor& tmp_out, at::Tensor& max_logits,
+                                at::Tensor& exp_sums, double k_scale, double v_scale) {
+  attention_impl(out, q, k_cache, v_cache, block_tables, seq_lens, scale, max_seq_len, tmp_out, max_logits, exp_sums,
+                 true, k_scale, v_scale);
 }
 
 // ---------------------------------------------------------------------------
@@ -370,6 +416,10 @@ TORCH_LIBRARY(decode_kernels, m) {
   m.def(
       "paged_attention_decode(Tensor! out, Tensor q, Tensor k_cache, Tensor v_cache, Tensor block_tables, "
       "Tensor seq_lens, float scale, int max_seq_len, Tensor! tmp_out, Tensor! max_logits, Tensor! exp_sums) -> ()");
+  m.def(
+      "paged_attention_decode_fp8(Tensor! out, Tensor q, Tensor k_cache, Tensor v_cache, Tensor block_tables, "
+      "Tensor seq_lens, float scale, int max_seq_len, Tensor! tmp_out, Tensor! max_logits, Tensor! exp_sums, "
+      "float k_scale, float v_scale) -> ()");
   m.def("gemm_tn(Tensor! c, Tensor a, Tensor b, Tensor? bias) -> ()");
   m.def("rms_norm(Tensor! out, Tensor input, Tensor weight, float eps) -> ()");
   m.def("fused_add_rms_norm(Tensor! input, Tensor! residual, Tensor weight, float eps) -> ()");
@@ -382,6 +432,7 @@ TORCH_LIBRARY(decode_kernels, m) {
 
 TORCH_LIBRARY_IMPL(decode_kernels, CUDA, m) {
   m.impl("paged_attention_decode", &paged_attention_decode);
+  m.impl("paged_attention_decode_fp8", &paged_attention_decode_fp8);
   m.impl("gemm_tn", &gemm_tn);
   m.impl("rms_norm", &rms_norm);
   m.impl("fused_add_rms_norm", &fused_add_rms_norm);

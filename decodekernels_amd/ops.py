@@ -41,12 +41,28 @@ def _require() -> None:
         )
 
 
+def _has_op(name: str) -> bool:
+    """False for an op a stale build of _C does not define (rebuilding fixes it)."""
+    try:
+        getattr(torch.ops.decode_kernels, name)
+        return True
+    except (AttributeError, RuntimeError):
+        return False
+
+
 if _AVAILABLE:
     # Meta implementations so torch.compile can trace through the mutating ops
     # (reference: decode_kernels/ops.py:41-61).
     @torch.library.register_fake("decode_kernels::paged_attention_decode")
     def _(out, q, k_cache, v_cache, block_tables, seq_lens, scale, max_seq_len, tmp_out, max_logits, exp_sums):
         return None
+
+    if _has_op("paged_attention_decode_fp8"):
+
+        @torch.library.register_fake("decode_kernels::paged_attention_decode_fp8")
+        def _(out, q, k_cache, v_cache, block_tables, seq_lens, scale, max_seq_len, tmp_out, max_logits, exp_sums,
+              k_scale, v_scale):
+            return None
 
     @torch.library.register_fake("decode_kernels::gemm_tn")
     def _(c, a, b, bias):
@@ -64,13 +80,17 @@ if _AVAILABLE:
     def _(out, input):
         return None
 
-    @torch.library.register_fake("decode_kernels::rotary_embedding")
-    def _(positions, query, key, head_size, cos_sin_cache, is_neox):
-        return None
+    if _has_op("rotary_embedding"):
 
-    @torch.library.register_fake("decode_kernels::reshape_and_cache")
-    def _(key, value, key_cache, value_cache, slot_mapping):
-        return None
+        @torch.library.register_fake("decode_kernels::rotary_embedding")
+        def _(positions, query, key, head_size, cos_sin_cache, is_neox):
+            return None
+
+    if _has_op("reshape_and_cache"):
+
+        @torch.library.register_fake("decode_kernels::reshape_and_cache")
+        def _(key, value, key_cache, value_cache, slot_mapping):
+            return None
 
 
 # ---------------------------------------------------------------------------
@@ -104,6 +124,8 @@ def paged_attention_decode(
     max_seq_len: int | None = None,
     out: torch.Tensor | None = None,
     workspace: tuple | None = None,
+    k_scale: float = 1.0,
+    v_scale: float = 1.0,
 ) -> torch.Tensor:
     """Single-token decode attention over a paged KV cache.
 
@@ -113,6 +135,10 @@ def paged_attention_decode(
     place); block_tables: [num_seqs, max_blocks] int32; seq_lens: [num_seqs]
     int32. ``max_seq_len`` must bound every entry of seq_lens; passing it
     avoids a device-to-host sync (reference: decode_kernels/ops.py:83-116).
+
+    An fp8 cache (``torch.float8_e4m3fn``, vLLM's fp8 KV cache) is read as
+    K = k_scale * k_cache and V = v_scale * v_cache with q / out in fp16 or
+    bf16 (``paged_attention_decode_fp8``; the reference has no fp8 path).
     """
     _require()
     num_seqs, num_q_heads, head_dim = q.shape
@@ -125,6 +151,14 @@ def paged_attention_decode(
     if workspace is None:
         workspace = alloc_workspace(num_seqs, num_q_heads, head_dim, max_seq_len, q.device)
     tmp_out, max_logits, exp_sums = workspace
+    if k_cache.dtype == torch.float8_e4m3fn:
+        torch.ops.decode_kernels.paged_attention_decode_fp8(
+            out, q, k_cache, v_cache, block_tables, seq_lens, float(scale), int(max_seq_len), tmp_out, max_logits,
+            exp_sums, float(k_scale), float(v_scale)
+        )
+        return out
+    if k_scale != 1.0 or v_scale != 1.0:
+        raise ValueError("k_scale / v_scale apply to an fp8 (float8_e4m3fn) KV cache only")
     torch.ops.decode_kernels.paged_attention_decode(
         out, q, k_cache, v_cache, block_tables, seq_lens, float(scale), int(max_seq_len), tmp_out, max_logits, exp_sums
     )

@@ -28,6 +28,8 @@ class PagedKV:
 
 
 def _cache(shape, gen, dtype, device):
+    if dtype.is_floating_point and dtype.itemsize == 1:  # fp8: N(0, 1) values rounded to the format
+        return torch.randn(*shape, generator=gen, dtype=torch.float32).to(dtype).to(device)
     return torch.randn(*shape, generator=gen, dtype=dtype).to(device)
 
 

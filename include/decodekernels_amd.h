@@ -81,6 +81,19 @@ typedef struct dk_paged_attn_params {
 int dk_paged_attention_decode(const dk_paged_attn_params* p, int dtype, int head_dim, int max_seq_len, void* stream);
 
 /*
+ * The same op over an fp8 KV cache: k_cache / v_cache hold OCP e4m3fn bytes
+ * (torch.float8_e4m3fn) with per-tensor dequantisation scales, K = k_scale * k8
+ * and V = v_scale * v8; q and out stay in `dtype` (fp16 / bf16). Strides are
+ * in elements (bytes); pointers and strides must be multiples of 8 bytes.
+ * Same workspace contract as dk_paged_attention_decode.
+ * No counterpart in DecodeKernels, whose README lists FP8 KV as unsupported
+ * (README.md:185); the signature follows vLLM's fp8 KV cache (e4m3 values,
+ * per-tensor k_scale / v_scale).
+ */
+int dk_paged_attention_decode_fp8(const dk_paged_attn_params* p, int dtype, int head_dim, int max_seq_len,
+                                  float k_scale, float v_scale, void* stream);
+
+/*
  * C[M,N] = A[M,K] * B[N,K]^T (+ bias[N]), fp32 accumulation, one rounding.
  * Replaces dk::launch_gemm_tn<T> (csrc/gemm_wmma.cuh:209-219).
  * K, lda and ldb must be multiples of 8; A and B 16-byte aligned; bias may be NULL.

@@ -1,0 +1,142 @@
+"""GPU parity tests of paged attention over an fp8 (e4m3fn) KV cache.
+
+The reference has no fp8 path (README.md:185); the oracle is the fp32
+reference attention on the dequantised cache (K = k_scale * k8, V = v_scale *
+v8) at the 16-bit bar (2e-2 bf16 / 5e-3 fp16 plus the final rounding). A
+structural check pins the conversion: with unit scales, an fp8 cache gives
+bit-for-bit the output of the 16-bit path on the same cache converted to the
+model dtype (e4m3fn values are exact in bf16 and fp16).
+"""
+
+import ctypes
+
+import pytest
+import torch
+
+import decodekernels_amd as dk
+from decodekernels_amd import capi
+from decodekernels_amd.testing import make_paged_kv
+from parity import assert_max_abs, attention_f32
+
+pytestmark = pytest.mark.gpu
+
+FP8 = torch.float8_e4m3fn
+DTYPES = [torch.float16, torch.bfloat16]
+
+
+def _q(n, hq, d, dtype, seed=1):
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    return torch.randn(n, hq, d, generator=g, device="cuda", dtype=dtype)
+
+
+def _check(q, kv, k_scale, v_scale, dtype, **kw):
+    out = dk.paged_attention_decode(q, kv.k_cache, kv.v_cache, kv.block_tables, kv.seq_lens, k_scale=k_scale,
+                                    v_scale=v_scale, **kw)
+    ref = attention_f32(q, kv.k_cache.float() * k_scale, kv.v_cache.float() * v_scale, kv.block_tables, kv.seq_lens)
+    assert_max_abs(out, ref, dtype, "fp8 paged_attention_decode")
+    return out
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("head_dim", [64, 128, 256])
+@pytest.mark.parametrize("group", [1, 4, 8])
+@pytest.mark.parametrize("layout", ["nhd", "hnd", "vllm"])
+def test_fp8_single_pass_and_split(dtype, head_dim, group, layout):
+    lens = [1, 17, 300, 512, 513, 1500, 0, 2100]
+    kv = make_paged_kv(lens, 2, head_dim, 16, FP8, "cuda", layout=layout, seed=head_dim + group)
+    q = _q(len(lens), 2 * group, head_dim, dtype)
+    out = _check(q, kv, 0.05, 0.7, dtype)
+    assert (out[6] == 0).all(), "an empty sequence gives zeros"
+    short = [1, 17, 300, 512]
+    kv_s = make_paged_kv(short, 2, head_dim, 32, FP8, "cuda", layout=layout, seed=head_dim + group + 1)
+    _check(_q(len(short), 2 * group, head_dim, dtype, seed=2), kv_s, 0.05, 0.7, dtype)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("schedule", ["grid", "balanced"])
+def test_fp8_long_contexts_both_schedules(dtype, schedule, monkeypatch):
+    monkeypatch.setenv("DK_ATTN_SCHEDULE", schedule)
+    lens = [16384, 3000, 7777, 1, 600, 9000, 12000, 5]
+    kv = make_paged_kv(lens, 8, 128, 16, FP8, "cuda", layout="vllm", seed=7)
+    _check(_q(len(lens), 32, 128, dtype, seed=3), kv, 0.031, 0.25, dtype)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("split", [False, True])
+def test_fp8_equals_16bit_path_on_the_converted_cache(dtype, split):
+    lens = [700, 33, 2000, 512] if split else [100, 33, 512, 7]
+    kv = make_paged_kv(lens, 4, 128, 16, FP8, "cuda", layout="nhd", seed=11)
+    q = _q(len(lens), 16, 128, dtype, seed=4)
+    got = dk.paged_attention_decode(q, kv.k_cache, kv.v_cache, kv.block_tables, kv.seq_lens)
+    want = dk.paged_attention_decode(q, kv.k_cache.to(dtype), kv.v_cache.to(dtype), kv.block_tables, kv.seq_lens)
+    torch.cuda.synchronize()
+    assert torch.equal(got, want)
+
+
+def test_fp8_block_sizes_that_split_tiles():
+    lens = [5, 40, 700, 1300]
+    for bs in (8, 24):
+        kv = make_paged_kv(lens, 2, 64, bs, FP8, "cuda", layout="nhd", seed=bs)
+        _check(_q(len(lens), 8, 64, torch.bfloat16, seed=bs), kv, 0.1, 0.1, torch.bfloat16)
+
+
+def test_fp8_graph_replay_follows_new_lengths():
+    dtype = torch.bfloat16
+    kv = make_paged_kv([2048] * 3, 2, 128, 16, FP8, "cuda", seed=13)
+    kv.seq_lens.copy_(torch.tensor([300, 1500, 40], dtype=torch.int32))
+    q = _q(3, 8, 128, dtype, seed=5)
+    out = torch.empty_like(q)
+    ws = dk.alloc_workspace(3, 8, 128, 2048, "cuda")
+
+    def step():
+        dk.paged_attention_decode(q, kv.k_cache, kv.v_cache, kv.block_tables, kv.seq_lens, max_seq_len=2048,
+                                  out=out, workspace=ws, k_scale=0.2, v_scale=0.3)
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        step()
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step()
+    for lens in ([300, 1500, 40], [2048, 1, 777], [0, 513, 2047]):
+        kv.seq_lens.copy_(torch.tensor(lens, dtype=torch.int32))
+        graph.replay()
+        torch.cuda.synchronize()
+        ref = attention_f32(q, kv.k_cache.float() * 0.2, kv.v_cache.float() * 0.3, kv.block_tables, kv.seq_lens)
+        assert_max_abs(out, ref, dtype, f"replay {lens}")
+
+
+def test_fp8_capi_matches_torch_op():
+    dtype = torch.float16
+    lens = [3, 200, 512, 1900]
+    kv = make_paged_kv(lens, 4, 128, 16, FP8, "cuda", layout="vllm", seed=21)
+    q = _q(len(lens), 16, 128, dtype, seed=6)
+    ws = dk.alloc_workspace(len(lens), 16, 128, max(lens), "cuda")
+    out = torch.empty_like(q)
+    p = capi.attn_params(out, q, kv.k_cache, kv.v_cache, kv.block_tables, kv.seq_lens, 128**-0.5, ws)
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    rc = capi.lib().dk_paged_attention_decode_fp8(ctypes.byref(p), capi.dtype_code(dtype), 128, max(lens), 0.5, 2.0,
+                                                  stream)
+    assert rc == 0, capi.last_error()
+    via_torch = dk.paged_attention_decode(q, kv.k_cache, kv.v_cache, kv.block_tables, kv.seq_lens,
+                                          max_seq_len=max(lens), k_scale=0.5, v_scale=2.0)
+    torch.cuda.synchronize()
+    assert torch.equal(out, via_torch)
+
+
+def test_fp8_rejects_bad_arguments():
+    kv = make_paged_kv([10, 20], 2, 128, 16, FP8, "cuda", seed=1)
+    q = _q(2, 8, 128, torch.bfloat16)
+    with pytest.raises(RuntimeError, match="finite"):
+        dk.paged_attention_decode(q, kv.k_cache, kv.v_cache, kv.block_tables, kv.seq_lens, k_scale=float("inf"))
+    with pytest.raises(RuntimeError, match="multiples of 8 bytes"):
+        flat = torch.zeros(kv.k_cache.numel() + 4, dtype=FP8, device="cuda")
+        k_off = flat[4:].view(kv.k_cache.shape)
+        dk.paged_attention_decode(q, k_off, kv.v_cache, kv.block_tables, kv.seq_lens)
+    with pytest.raises(RuntimeError, match="float16 or bfloat16"):
+        dk.paged_attention_decode(q.float(), kv.k_cache, kv.v_cache, kv.block_tables, kv.seq_lens)
+    with pytest.raises(ValueError, match="fp8"):
+        kv16 = make_paged_kv([10], 2, 128, 16, torch.bfloat16, "cuda")
+        dk.paged_attention_decode(q[:1], kv16.k_cache, kv16.v_cache, kv16.block_tables, kv16.seq_lens, k_scale=0.5)

@@ -17,6 +17,7 @@ def test_library_exports_every_declared_symbol():
     declared = capi.declared_functions()
     assert set(declared) >= {
         "dk_paged_attention_decode",
+        "dk_paged_attention_decode_fp8",
         "dk_gemm_tn",
         "dk_rms_norm",
         "dk_fused_add_rms_norm",
@@ -90,6 +91,21 @@ def test_capi_attention_workspace_too_small_and_misaligned():
     p.k_stride_token = 130  # 260 bytes: not 8-byte aligned rows at head_dim 128
     rc = capi.lib().dk_paged_attention_decode(ctypes.byref(p), capi.DK_FLOAT16, 128, 10, None)
     assert rc == capi.HIP_ERROR_INVALID_VALUE and "aligned" in capi.last_error()
+
+
+def test_capi_attention_fp8_validation():
+    L = capi.lib()
+    p = _attn_params()
+    p.k_stride_token = 132  # bytes: not a multiple of 8
+    rc = L.dk_paged_attention_decode_fp8(ctypes.byref(p), capi.DK_BFLOAT16, 128, 10, 1.0, 1.0, None)
+    assert rc == capi.HIP_ERROR_INVALID_VALUE and "multiples of 8 bytes" in capi.last_error()
+    p = _attn_params()
+    rc = L.dk_paged_attention_decode_fp8(ctypes.byref(p), capi.DK_BFLOAT16, 128, 10, float("nan"), 1.0, None)
+    assert rc == capi.HIP_ERROR_INVALID_VALUE and "finite" in capi.last_error()
+    rc = L.dk_paged_attention_decode_fp8(ctypes.byref(p), 5, 128, 10, 1.0, 1.0, None)
+    assert rc == capi.HIP_ERROR_INVALID_VALUE and "float16 or bfloat16" in capi.last_error()
+    p.num_seqs = 0
+    assert L.dk_paged_attention_decode_fp8(ctypes.byref(p), capi.DK_FLOAT16, 128, 10, 1.0, 1.0, None) == 0
 
 
 def test_capi_attention_zero_seqs_is_a_no_op():
@@ -232,6 +248,9 @@ def test_ops_are_registered_with_reference_schemas():
         "rms_norm": "rms_norm(Tensor(a0!) out, Tensor input, Tensor weight, float eps) -> ()",
         "fused_add_rms_norm": "fused_add_rms_norm(Tensor(a0!) input, Tensor(a1!) residual, Tensor weight, float eps) -> ()",
         "silu_and_mul": "silu_and_mul(Tensor(a0!) out, Tensor input) -> ()",
+        "paged_attention_decode_fp8": "paged_attention_decode_fp8(Tensor(a0!) out, Tensor q, Tensor k_cache, "
+        "Tensor v_cache, Tensor block_tables, Tensor seq_lens, float scale, int max_seq_len, Tensor(a1!) tmp_out, "
+        "Tensor(a2!) max_logits, Tensor(a3!) exp_sums, float k_scale, float v_scale) -> ()",
         "rotary_embedding": "rotary_embedding(Tensor positions, Tensor(a0!) query, Tensor(a1!)? key, int head_size, "
         "Tensor cos_sin_cache, bool is_neox) -> ()",
         "reshape_and_cache": "reshape_and_cache(Tensor key, Tensor value, Tensor(a0!) key_cache, "
