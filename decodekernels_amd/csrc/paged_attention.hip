@@ -61,6 +61,9 @@ constexpr int kUnit = 2 * kPart;          // split-K work unit: two slots (its b
 #ifndef DK_ATTN_DEPTH_FP8
 #define DK_ATTN_DEPTH_FP8 2  // tiles in flight per wave with an fp8 cache
 #endif
+#ifndef DK_ATTN_VTR
+#define DK_ATTN_VTR 1  // V into the P.V operand layout: 1 LDS transpose reads, 0 identity MFMAs
+#endif
 #ifndef DK_ATTN_OCC_FP8_D128
 #define DK_ATTN_OCC_FP8_D128 3  // waves per SIMD targeted at head_dim 128 with an fp8 cache
 #endif
@@ -123,6 +126,19 @@ __device__ __forceinline__ u32x4 bload8(__amdgpu_buffer_rsrc_t r, int off) {
   }
 }
 
+// Raw buffer load of 16 bytes at byte offset `off`, aligned to ALIGN (16 or 8).
+template <int ALIGN>
+__device__ __forceinline__ u32x4 bload16b(__amdgpu_buffer_rsrc_t r, int off) {
+  constexpr int A = DK_ATTN_LOAD_AUX;
+  if constexpr (ALIGN >= 16) {
+    return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, A);
+  } else {
+    const u32x2 a = __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, A);
+    const u32x2 b = __builtin_amdgcn_raw_buffer_load_b64(r, off + 8, 0, A);
+    return u32x4{a[0], a[1], b[0], b[1]};
+  }
+}
+
 template <int ALIGN>
 __device__ __forceinline__ u32x2 bload4(__amdgpu_buffer_rsrc_t r, int off) {
   constexpr int A = DK_ATTN_LOAD_AUX;
@@ -142,12 +158,23 @@ struct TileRegs {
   u32x4 v[CHUNKS];
 };
 
-// An fp8 (e4m3fn) cache tile: lane l holds the same 8 columns as raw bytes.
+// An fp8 (e4m3fn) cache tile: lane l holds 16 contiguous bytes of row l % 16
+// per 64 columns (columns 64 j + 16 (l / 16) ...), one 16-byte load each --
+// 64 bytes of every row per load, as the 16-bit tiles. The columns of MFMA
+// chunk c are then 64 (c / 2) + 16 (l / 16) + 8 (c % 2) ...; the query
+// fragments use the same columns, so Q.K^T is unchanged.
 template <int CHUNKS>
 struct TileRegs<CHUNKS, true> {
-  u32x2 k[CHUNKS];
-  u32x2 v[CHUNKS];
+  u32x4 k[CHUNKS / 2];
+  u32x4 v[CHUNKS / 2];
 };
+
+// 16 bytes at an 8-byte-aligned address (fp8 rows are 8-byte aligned).
+__device__ __forceinline__ u32x4 load16_8b(const uint8_t* p) {
+  const u32x2 a = reinterpret_cast<const u32x2*>(p)[0];
+  const u32x2 b = reinterpret_cast<const u32x2*>(p)[1];
+  return u32x4{a[0], a[1], b[0], b[1]};
+}
 
 // 8 e4m3fn bytes -> 8 elements of E, exactly (every e4m3fn value is a bf16
 // and an fp16 value); v_cvt_pk_f32_fp8 matches torch.float8_e4m3fn on all
@@ -176,12 +203,23 @@ constexpr int attn_occupancy() {
 }
 
 // LDS of one work unit: per-wave softmax state and partial outputs, merged at the end.
+// Row pitch (16-bit elements) of a wave's V tile in LDS: 32 bytes of padding
+// put the 16 rows' 8-byte transpose reads of one 16-lane group on distinct
+// banks (rows start 8 banks apart).
+template <int D>
+constexpr int vt_pitch() {
+  return D + 16;
+}
+
 template <int D, int NW>
 struct UnitSmem {
   float m[NW][16];              // reference max per head (log2 units)
   float t[NW][16];              // true max per head
   float l[NW][16];              // exp-sum against the reference max
   float o[NW][kMaxGroup][D];    // partial outputs
+#if DK_ATTN_VTR
+  uint16_t vt[NW][16 * vt_pitch<D>()];  // each wave's current V tile (model dtype)
+#endif
 };
 
 // A work unit: tokens [start, end) of sequence `seq` (end > start, at most
@@ -271,13 +309,18 @@ struct UnitEngine {
 
   // Query fragments (B operand of Q·Kᵀ): head l16, columns 8*lg + 32*c ... +7,
   // in the model dtype; heads past the group are zero.
+  // First column of this lane's 8 columns of MFMA chunk c.
+  __device__ __forceinline__ int chunk_col(int c) const {
+    return KV8 ? 64 * (c / 2) + 16 * lg + 8 * (c % 2) : 32 * c + 8 * lg;
+  }
+
   __device__ __forceinline__ void load_q(const Unit& u) {
     const uint16_t* qrow = p.q + u.seq * p.q_ss + (u.kv_head * p.group + l16) * p.q_sh;
 #pragma unroll
     for (int c = 0; c < CH; ++c) {
       u32x4 w = {0u, 0u, 0u, 0u};
       if (l16 < p.group) {
-        const uint16_t* src = qrow + 8 * lg + 32 * c;
+        const uint16_t* src = qrow + chunk_col(c);
 #pragma unroll
         for (int e = 0; e < 4; ++e) w[e] = static_cast<uint32_t>(src[2 * e]) | (static_cast<uint32_t>(src[2 * e + 1]) << 16);
       }
@@ -311,14 +354,16 @@ struct UnitEngine {
       const int nrec = live ? 0x7fffffff : 0;
       const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(const_cast<KvT*>(kt), 0, nrec, kRsrcWord3);
       const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(const_cast<KvT*>(vt), 0, nrec, kRsrcWord3);
-      const int koff = kElt * (row * static_cast<int>(p.k_st) + 8 * lg);
-      const int voff = kElt * (row * static_cast<int>(p.v_st) + 8 * lg);
       if constexpr (KV8) {
+        const int koff = row * static_cast<int>(p.k_st) + 16 * lg;
+        const int voff = row * static_cast<int>(p.v_st) + 16 * lg;
 #pragma unroll
-        for (int c = 0; c < CH; ++c) r.k[c] = __builtin_amdgcn_raw_buffer_load_b64(rk, koff + 32 * c, 0, DK_ATTN_LOAD_AUX);
+        for (int j = 0; j < CH / 2; ++j) r.k[j] = bload16b<ALIGN>(rk, koff + 64 * j);
 #pragma unroll
-        for (int c = 0; c < CH; ++c) r.v[c] = __builtin_amdgcn_raw_buffer_load_b64(rv, voff + 32 * c, 0, DK_ATTN_LOAD_AUX);
+        for (int j = 0; j < CH / 2; ++j) r.v[j] = bload16b<ALIGN>(rv, voff + 64 * j);
       } else {
+        const int koff = kElt * (row * static_cast<int>(p.k_st) + 8 * lg);
+        const int voff = kElt * (row * static_cast<int>(p.v_st) + 8 * lg);
 #pragma unroll
         for (int c = 0; c < CH; ++c) r.k[c] = bload8<ALIGN>(rk, koff + 64 * c);
 #pragma unroll
@@ -329,14 +374,16 @@ struct UnitEngine {
       const int lb = t / p.block_size;
       const int64_t phys = p.block_tables[u.seq * p.bt_stride + lb];
       const int64_t off = t - lb * p.block_size;
-      const KvT* kp = kbase + phys * p.k_sb + off * p.k_st + 8 * lg;
-      const KvT* vp = vbase + phys * p.v_sb + off * p.v_st + 8 * lg;
       if constexpr (KV8) {
+        const KvT* kp = kbase + phys * p.k_sb + off * p.k_st + 16 * lg;
+        const KvT* vp = vbase + phys * p.v_sb + off * p.v_st + 16 * lg;
 #pragma unroll
-        for (int c = 0; c < CH; ++c) r.k[c] = *reinterpret_cast<const u32x2*>(kp + 32 * c);
+        for (int j = 0; j < CH / 2; ++j) r.k[j] = load16_8b(kp + 64 * j);
 #pragma unroll
-        for (int c = 0; c < CH; ++c) r.v[c] = *reinterpret_cast<const u32x2*>(vp + 32 * c);
+        for (int j = 0; j < CH / 2; ++j) r.v[j] = load16_8b(vp + 64 * j);
       } else {
+        const KvT* kp = kbase + phys * p.k_sb + off * p.k_st + 8 * lg;
+        const KvT* vp = vbase + phys * p.v_sb + off * p.v_st + 8 * lg;
 #pragma unroll
         for (int c = 0; c < CH; ++c) r.k[c] = load8<ALIGN>(kp + 32 * c);
 #pragma unroll
@@ -345,9 +392,15 @@ struct UnitEngine {
     }
   }
 
-  // A tile chunk as an MFMA operand in the model dtype.
-  __device__ __forceinline__ static u32x4 kv_operand(const u32x4& w) { return w; }
-  __device__ __forceinline__ static u32x4 kv_operand(const u32x2& w) { return fp8x8_to<E>(w); }
+  // K chunk c of a tile as an MFMA operand in the model dtype.
+  __device__ __forceinline__ static u32x4 k_operand(const Tile& r, int c) {
+    if constexpr (KV8) {
+      const u32x4 w = r.k[c / 2];
+      return c % 2 == 0 ? fp8x8_to<E>(u32x2{w[0], w[1]}) : fp8x8_to<E>(u32x2{w[2], w[3]});
+    } else {
+      return r.k[c];
+    }
+  }
 
   // The first DEPTH tiles of this wave. The scheduling barriers keep the
   // tiles' load groups in program order, so the oldest outstanding loads are
@@ -365,7 +418,7 @@ struct UnitEngine {
     // Q·Kᵀ: S[token 4*lg + i][head l16].
     f32x4 s = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int c = 0; c < CH; ++c) s = E::mfma_16x16x32(kv_operand(r.k[c]), qf[c], s);
+    for (int c = 0; c < CH; ++c) s = E::mfma_16x16x32(k_operand(r, c), qf[c], s);
 
     const int t0 = u.start + tile * kTile;
     float x[4];
@@ -402,10 +455,44 @@ struct UnitEngine {
     const u32x2 p_hi = {pack2<E>(pr[0], pr[1]), pack2<E>(pr[2], pr[3])};
     const u32x2 p_lo = {pack2<E>(pr[0] - E::lo(p_hi[0]), pr[1] - E::hi(p_hi[0])),
                         pack2<E>(pr[2] - E::lo(p_hi[1]), pr[3] - E::hi(p_hi[1]))};
+#if DK_ATTN_VTR
+    // V through this wave's LDS tile: lane l writes its row (token l16,
+    // columns 8 lg + 32 c ...) and reads back, with ds_read_b64_tr_b16, the
+    // B operand of v_mfma_f32_16x16x16 for 16-column block nb -- V[token
+    // 4 lg + e][column 16 nb + l16], e = 0..3. The transpose read hands lane
+    // j of a 16-lane group element j % 4 of group lane 4 k + (j % 16) / 4 as
+    // its element k (measured on the device), so group lane s reads the four
+    // columns 16 nb + 4 (s % 4) ... of token 4 lg + (s % 16) / 4.
+    uint16_t* vt = sm.vt[wave];
+    if constexpr (KV8) {
+#pragma unroll
+      for (int j = 0; j < CH / 2; ++j) {
+        const u32x4 w = r.v[j];
+        uint16_t* dst = vt + l16 * vt_pitch<D>() + 64 * j + 16 * lg;
+        *reinterpret_cast<u32x4*>(dst) = fp8x8_to<E>(u32x2{w[0], w[1]});
+        *reinterpret_cast<u32x4*>(dst + 8) = fp8x8_to<E>(u32x2{w[2], w[3]});
+      }
+    } else {
+#pragma unroll
+      for (int c = 0; c < CH; ++c) *reinterpret_cast<u32x4*>(vt + l16 * vt_pitch<D>() + 8 * lg + 32 * c) = r.v[c];
+    }
+    const int tr_row = 4 * lg + l16 / 4;
+    const int tr_col = 4 * (l16 % 4);
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+      using lds_v4i16 = __attribute__((address_space(3))) s16x4;
+      // (a C-style cast is the generic -> LDS address-space conversion)
+      const auto src = (lds_v4i16*)(vt + tr_row * vt_pitch<D>() + 16 * nb + tr_col);
+      const u32x2 vb = __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16(src));
+      acc[nb] = E::mfma_16x16x16(p_hi, vb, acc[nb]);
+      acc[nb] = E::mfma_16x16x16(p_lo, vb, acc[nb]);
+    }
+#else
+    static_assert(!KV8, "the fp8 cache path reads V through the LDS transpose");
 #pragma unroll
     for (int c = 0; c < CH; ++c) {
       const f32x4 z = {0.f, 0.f, 0.f, 0.f};
-      const u32x4 vc = kv_operand(r.v[c]);
+      const u32x4 vc = r.v[c];
       const f32x4 t_lo = E::mfma_16x16x32(vc, eye0, z);  // columns 32c + l16
       const f32x4 t_hi = E::mfma_16x16x32(vc, eye1, z);  // columns 32c + 16 + l16
       const u32x2 v_lo = {pack2<E>(t_lo[0], t_lo[1]), pack2<E>(t_lo[2], t_lo[3])};
@@ -415,6 +502,7 @@ struct UnitEngine {
       acc[2 * c + 1] = E::mfma_16x16x16(p_hi, v_hi, acc[2 * c + 1]);
       acc[2 * c + 1] = E::mfma_16x16x16(p_lo, v_hi, acc[2 * c + 1]);
     }
+#endif
   }
 
   // Steady state: consume the oldest tile, refill its registers DEPTH tiles
@@ -889,7 +977,9 @@ hipError_t launch_kernel(const KParams& kp, unsigned grid, hipStream_t stream, i
 template <typename E, int D, bool SPLIT, bool BS16, bool BALANCED, bool KV8>
 hipError_t launch_aligned(const KParams& kp, unsigned grid, int align, hipStream_t stream, int* resident = nullptr) {
   if constexpr (KV8) {
-    // fp8 rows: 8-byte loads (checked by the host).
+    // fp8 rows: 16-byte loads when 16-byte aligned, else pairs of 8-byte loads
+    // (8-byte alignment is checked by the host).
+    if (align >= 16) return launch_kernel<E, D, 16, SPLIT, BS16, BALANCED, true>(kp, grid, stream, resident);
     return launch_kernel<E, D, 8, SPLIT, BS16, BALANCED, true>(kp, grid, stream, resident);
   } else {
     switch (align) {
