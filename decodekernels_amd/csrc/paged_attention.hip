@@ -81,7 +81,8 @@ constexpr int kUnit = 2 * kPart;          // split-K work unit: two slots (its b
 #endif
 constexpr int kWaves = DK_ATTN_WAVES;
 constexpr int kTile = 16;
-constexpr int kMaxGroup = DK_MAX_GQA_GROUP;
+constexpr int kMaxGroup = DK_MAX_GQA_GROUP;  // 16: the MFMA tile's padded head count
+constexpr int kMergeHeads = 8;               // heads per LDS merge pass (two passes above 8)
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
 
@@ -216,7 +217,7 @@ struct UnitSmem {
   float m[NW][16];              // reference max per head (log2 units)
   float t[NW][16];              // true max per head
   float l[NW][16];              // exp-sum against the reference max
-  float o[NW][kMaxGroup][D];    // partial outputs
+  float o[NW][kMergeHeads][D];  // partial outputs of one merge pass
 #if DK_ATTN_VTR
   uint16_t vt[NW][16 * vt_pitch<D>()];  // each wave's current V tile (model dtype)
 #endif
@@ -533,20 +534,32 @@ struct UnitEngine {
       sm.t[wave][lane] = m_true;
       sm.l[wave][lane] = l_tot;
     }
-    // acc[n] lane l: O[head 4*lg + i][column 16n + l16].
+    // Heads in passes of kMergeHeads (one pass up to 8, two up to 16).
+    for (int h0 = 0; h0 < group; h0 += kMergeHeads) {
+      const int hn = min(kMergeHeads, group - h0);
+      // acc[n] lane l: O[head 4*lg + i][column 16n + l16].
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int h = 4 * lg + i;
-      if (h < group) {
+      for (int i = 0; i < 4; ++i) {
+        const int h = 4 * lg + i - h0;
+        if (h >= 0 && h < hn) {
 #pragma unroll
-        for (int n = 0; n < NB; ++n) sm.o[wave][h][16 * n + l16] = acc[n][i];
+          for (int n = 0; n < NB; ++n) sm.o[wave][h][16 * n + l16] = acc[n][i];
+        }
       }
+      lds_barrier();
+      merge_pass(u, h0, hn);
+      lds_barrier();
     }
-    lds_barrier();
+  }
 
-    for (int idx = tid; idx < group * D; idx += NT) {
-      const int h = idx / D;
-      const int d = idx - h * D;
+  // Combines the waves' partial outputs of heads h0 .. h0 + hn - 1 (in LDS)
+  // and writes them.
+  __device__ __forceinline__ void merge_pass(const Unit& u, int h0, int hn) {
+    const int group = p.group;
+    for (int idx = tid; idx < hn * D; idx += NT) {
+      const int hh = idx / D;
+      const int d = idx - hh * D;
+      const int h = h0 + hh;
       float M = sm.m[0][h];
 #pragma unroll
       for (int w = 1; w < NW; ++w) M = fmaxf(M, sm.m[w][h]);
@@ -556,7 +569,7 @@ struct UnitEngine {
       for (int w = 0; w < NW; ++w) {
         const float f = __builtin_amdgcn_exp2f(sm.m[w][h] - M);
         L += f * sm.l[w][h];
-        O += f * sm.o[w][h][d];
+        O += f * sm.o[w][hh][d];
       }
       const float res = O / L * p.v_scale;
       const int q_head = u.kv_head * group + h;
@@ -579,7 +592,6 @@ struct UnitEngine {
         p.out[u.seq * p.o_ss + q_head * p.o_sh + d] = E::from_float(res);
       }
     }
-    lds_barrier();
   }
 };
 

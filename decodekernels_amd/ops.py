@@ -15,7 +15,7 @@ import math
 import torch
 
 PARTITION_SIZE = 512  # tokens per split-K workspace slot (DK_PARTITION_SIZE in the C ABI)
-MAX_GQA_GROUP = 8  # query heads per KV head (DK_MAX_GQA_GROUP)
+MAX_GQA_GROUP = 16  # query heads per KV head (DK_MAX_GQA_GROUP; the reference stops at 8)
 SUPPORTED_HEAD_DIMS = (64, 128, 256)
 
 try:

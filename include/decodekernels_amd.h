@@ -34,8 +34,9 @@ enum dk_dtype {
 /* Tokens per split-K partition of the workspace contract (reference:
  * csrc/paged_attention.cuh:34, decode_kernels/ops.py:14). */
 #define DK_PARTITION_SIZE 512
-/* Largest GQA group (query heads per KV head) (csrc/paged_attention.cuh:37). */
-#define DK_MAX_GQA_GROUP 8
+/* Largest GQA group (query heads per KV head); the reference's is 8
+ * (csrc/paged_attention.cuh:37), this library's 16. */
+#define DK_MAX_GQA_GROUP 16
 
 /*
  * Launch descriptor of paged decode attention. Same fields and meaning as

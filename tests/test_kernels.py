@@ -158,6 +158,32 @@ def test_paged_attention_long_context_outlier_rows():
     _check_attention(_q(1, 32, 128, torch.float16), kv, torch.float16)
 
 
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("head_dim", [64, 128, 256])
+@pytest.mark.parametrize("group", [9, 12, 16])
+def test_paged_attention_groups_above_8(dtype, head_dim, group):
+    """GQA groups of 9-16 query heads per KV head (Llama-3.1-405B: 16), which
+    the reference rejects; the heads' partial outputs merge in two passes."""
+    lens = [1, 300, 512, 513, 2100, 0, 777]
+    kv = make_paged_kv(lens, 2, head_dim, 16, dtype, "cuda", layout="vllm", seed=group + head_dim)
+    out = _check_attention(_q(len(lens), 2 * group, head_dim, dtype, seed=group), kv, dtype)
+    assert (out[5] == 0).all()
+    short = [7, 64, 512]
+    kv = make_paged_kv(short, 1, head_dim, 32, dtype, "cuda", seed=group)
+    _check_attention(_q(len(short), group, head_dim, dtype, seed=group + 1), kv, dtype)
+
+
+@pytest.mark.parametrize("schedule", ["grid", "balanced"])
+def test_paged_attention_group_16_fp8_cache(schedule, monkeypatch):
+    monkeypatch.setenv("DK_ATTN_SCHEDULE", schedule)
+    lens = [9000, 40, 3000, 1]
+    kv = make_paged_kv(lens, 8, 128, 16, torch.float8_e4m3fn, "cuda", layout="vllm", seed=3)
+    q = _q(len(lens), 128, 128, torch.bfloat16, seed=4)
+    out = dk.paged_attention_decode(q, kv.k_cache, kv.v_cache, kv.block_tables, kv.seq_lens, k_scale=0.1, v_scale=0.3)
+    ref = attention_f32(q, kv.k_cache.float() * 0.1, kv.v_cache.float() * 0.3, kv.block_tables, kv.seq_lens)
+    assert_max_abs(out, ref, torch.bfloat16, "group 16, fp8 cache")
+
+
 def _log_uniform_lens(n, max_len, seed, zeros=4):
     """Lengths log-uniform in [1, max_len], a few empty, the first at max_len."""
     g = torch.Generator().manual_seed(seed)
@@ -265,7 +291,7 @@ def test_paged_attention_graph_replay(schedule, monkeypatch):
 def test_paged_attention_rejects_bad_inputs():
     kv = make_paged_kv([10], 2, 128, 16, torch.float16, "cuda")
     with pytest.raises(RuntimeError, match="GQA group"):
-        dk.paged_attention_decode(_q(1, 32, 128, torch.float16), kv.k_cache, kv.v_cache, kv.block_tables, kv.seq_lens)
+        dk.paged_attention_decode(_q(1, 64, 128, torch.float16), kv.k_cache, kv.v_cache, kv.block_tables, kv.seq_lens)
     kv96 = make_paged_kv([10], 2, 96, 16, torch.float16, "cuda")
     with pytest.raises(RuntimeError, match="head_dim"):
         dk.paged_attention_decode(_q(1, 2, 96, torch.float16), kv96.k_cache, kv96.v_cache, kv96.block_tables, kv96.seq_lens)
