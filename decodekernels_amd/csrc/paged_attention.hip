@@ -199,8 +199,9 @@ constexpr float kLazyMax = 8.0f;
 // allocation (one wave, no spills).
 template <int D, bool KV8 = false>
 constexpr int attn_occupancy() {
-  if constexpr (KV8) return D >= 256 ? DK_ATTN_OCC_FP8_D256 : (D == 128 ? DK_ATTN_OCC_FP8_D128 : DK_ATTN_OCC_D64);
-  return D >= 256 ? 1 : (D == 128 ? DK_ATTN_OCC_D128 : DK_ATTN_OCC_D64);
+  // Classes: D <= 64, 64 < D <= 128 (96, 128), D > 128 (192, 256).
+  if constexpr (KV8) return D > 128 ? DK_ATTN_OCC_FP8_D256 : (D > 64 ? DK_ATTN_OCC_FP8_D128 : DK_ATTN_OCC_D64);
+  return D > 128 ? 1 : (D > 64 ? DK_ATTN_OCC_D128 : DK_ATTN_OCC_D64);
 }
 
 // LDS of one work unit: per-wave softmax state and partial outputs, merged at the end.
@@ -253,7 +254,7 @@ template <typename E, int D, bool SPLIT, bool BS16, int ALIGN, int NW, bool KV8>
 struct UnitEngine {
   static constexpr int CH = D / 32;  // 32-column chunks per row
   static constexpr int NB = D / 16;  // 16-column output blocks
-  static constexpr int DEPTH = KV8 ? DK_ATTN_DEPTH_FP8 : (D >= 256 ? DK_ATTN_DEPTH_D256 : DK_ATTN_DEPTH);
+  static constexpr int DEPTH = KV8 ? DK_ATTN_DEPTH_FP8 : (D > 128 ? DK_ATTN_DEPTH_D256 : DK_ATTN_DEPTH);
   static constexpr int NT = NW * kWave;
   using Tile = TileRegs<CH, KV8>;
 
@@ -850,7 +851,7 @@ constexpr int reduce_waves() {
 template <typename E, int D, int WPH, bool PIECES>
 __global__ __launch_bounds__(reduce_waves<WPH>() * kWave) void paged_attention_reduce_kernel(const KParams p) {
   constexpr int kReduceWaves = reduce_waves<WPH>();
-  constexpr int C = D / kWave;  // columns per lane (1, 2 or 4)
+  constexpr int C = (D + kWave - 1) / kWave;  // columns per lane (1-4); lanes past D / C idle
   constexpr int HPW = kReduceWaves / WPH;  // heads per workgroup
   const int wave = static_cast<int>(threadIdx.x) / kWave;
   const int q_head = blockIdx.x * HPW + wave / WPH;
@@ -859,10 +860,11 @@ __global__ __launch_bounds__(reduce_waves<WPH>() * kWave) void paged_attention_r
   const int lane = threadIdx.x % kWave;
   __shared__ float red[WPH > 1 ? kReduceWaves : 1][D + 1];
   const bool active = q_head < p.num_q_heads;
-  uint16_t* out = p.out + seq * p.o_ss + (active ? q_head : 0) * p.o_sh + C * lane;
+  const bool cols = C * lane < D;  // this lane owns output columns
+  uint16_t* out = p.out + seq * p.o_ss + (active ? q_head : 0) * p.o_sh + (cols ? C * lane : 0);
   const int seq_len = p.seq_lens[seq];
   if (seq_len <= 0) {
-    if (active && sub == 0) {
+    if (active && sub == 0 && cols) {
 #pragma unroll
       for (int c = 0; c < C; ++c) out[c] = 0;
     }
@@ -871,7 +873,7 @@ __global__ __launch_bounds__(reduce_waves<WPH>() * kWave) void paged_attention_r
   const int64_t row0 = (static_cast<int64_t>(seq) * p.num_q_heads + (active ? q_head : 0)) * p.max_partitions;
   const float* ml = p.max_logits + row0;
   const float* es = p.exp_sums + row0;
-  const float* tmp = p.tmp_out + row0 * D + C * lane;
+  const float* tmp = p.tmp_out + row0 * D + (cols ? C * lane : 0);
 
   int entries;  // entries j map to rows row_of(j)
   bool slot1 = true;
@@ -916,14 +918,16 @@ __global__ __launch_bounds__(reduce_waves<WPH>() * kWave) void paged_attention_r
       const f32x4 v = *reinterpret_cast<const f32x4*>(t);
 #pragma unroll
       for (int c = 0; c < 4; ++c) acc[c] = fmaf(w, v[c], acc[c]);
-    } else {
+    } else if (cols) {
 #pragma unroll
       for (int c = 0; c < C; ++c) acc[c] = fmaf(w, t[c], acc[c]);
     }
   }
   if constexpr (WPH > 1) {
+    if (cols) {
 #pragma unroll
-    for (int c = 0; c < C; ++c) red[wave][C * lane + c] = acc[c];
+      for (int c = 0; c < C; ++c) red[wave][C * lane + c] = acc[c];
+    }
     if (lane == 0) red[wave][D] = W;
     __syncthreads();
     if (sub != 0 || !active) return;
@@ -933,11 +937,13 @@ __global__ __launch_bounds__(reduce_waves<WPH>() * kWave) void paged_attention_r
 #pragma unroll
     for (int w = 0; w < WPH; ++w) {
       W += red[wave + w][D];
+      if (cols) {
 #pragma unroll
-      for (int c = 0; c < C; ++c) acc[c] += red[wave + w][C * lane + c];
+        for (int c = 0; c < C; ++c) acc[c] += red[wave + w][C * lane + c];
+      }
     }
   }
-  if (!active) return;
+  if (!active || !cols) return;
   const float inv = 1.0f / W;
 #pragma unroll
   for (int c = 0; c < C; ++c) out[c] = E::from_float(acc[c] * inv);
@@ -947,7 +953,7 @@ constexpr int kMaxDevices = 64;
 
 template <int D>
 constexpr int waves_per_group() {
-  return D >= 256 ? DK_ATTN_WAVES_D256 : kWaves;
+  return D > 128 ? DK_ATTN_WAVES_D256 : kWaves;
 }
 
 // Launches the grid kernel (BALANCED = false, one workgroup per unit slot) or
@@ -1110,8 +1116,9 @@ int paged_attention_entry(const dk_paged_attn_params* a, int dtype, int head_dim
     return fail("num_q_heads must be a multiple of num_kv_heads");
   const int group = a->num_q_heads / a->num_kv_heads;
   if (group > kMaxGroup) return fail("GQA group size above %d is not supported", kMaxGroup);
-  if (head_dim != 64 && head_dim != 128 && head_dim != 256)
-    return fail("head_dim must be 64, 128 or 256, got %d", head_dim);
+  if (head_dim != 64 && head_dim != 96 && head_dim != 128 && head_dim != 192 && head_dim != 256)
+    return fail("head_dim must be 64, 96, 128, 192 or 256, got %d", head_dim);
+  if (kv8 && head_dim % 64 != 0) return fail("paged_attention_decode_fp8: head_dim must be 64, 128, 192 or 256");
   if (a->block_size <= 0) return fail("paged_attention_decode: block_size must be positive");
   if (max_seq_len < 0) return fail("max_seq_len must be non-negative");
   if (a->q == nullptr || a->out == nullptr || a->k_cache == nullptr || a->v_cache == nullptr ||
@@ -1122,7 +1129,7 @@ int paged_attention_entry(const dk_paged_attn_params* a, int dtype, int head_dim
     if (align < 8) return fail("fp8 KV-cache pointers and strides must be multiples of 8 bytes");
     if (!(k_scale == k_scale && v_scale == v_scale) || __builtin_isinf(k_scale) || __builtin_isinf(v_scale))
       return fail("paged_attention_decode_fp8: k_scale and v_scale must be finite");
-  } else if (align < 4 || (head_dim == 128 && align < 8) || (head_dim == 256 && align < 16)) {
+  } else if (align < 4 || (head_dim > 64 && head_dim <= 128 && align < 8) || (head_dim > 128 && align < 16)) {
     return fail("KV-cache pointers must be aligned to head_dim / 16 bytes");
   }
   if (a->num_seqs > 65535 || a->num_kv_heads > 65535 || a->num_q_heads > 65535)
@@ -1181,13 +1188,17 @@ int paged_attention_entry(const dk_paged_attn_params* a, int dtype, int head_dim
   if (dtype == DK_BFLOAT16) {
     switch (head_dim) {
       case 64: e = launch_kv<Bf16, 64>(kp, a->num_kv_heads, a->num_seqs, split, bs16, align, kv8, s); break;
+      case 96: e = launch<Bf16, 96, false>(kp, a->num_kv_heads, a->num_seqs, split, bs16, align, s); break;
       case 128: e = launch_kv<Bf16, 128>(kp, a->num_kv_heads, a->num_seqs, split, bs16, align, kv8, s); break;
+      case 192: e = launch_kv<Bf16, 192>(kp, a->num_kv_heads, a->num_seqs, split, bs16, align, kv8, s); break;
       default: e = launch_kv<Bf16, 256>(kp, a->num_kv_heads, a->num_seqs, split, bs16, align, kv8, s); break;
     }
   } else {
     switch (head_dim) {
       case 64: e = launch_kv<F16, 64>(kp, a->num_kv_heads, a->num_seqs, split, bs16, align, kv8, s); break;
+      case 96: e = launch<F16, 96, false>(kp, a->num_kv_heads, a->num_seqs, split, bs16, align, s); break;
       case 128: e = launch_kv<F16, 128>(kp, a->num_kv_heads, a->num_seqs, split, bs16, align, kv8, s); break;
+      case 192: e = launch_kv<F16, 192>(kp, a->num_kv_heads, a->num_seqs, split, bs16, align, kv8, s); break;
       default: e = launch_kv<F16, 256>(kp, a->num_kv_heads, a->num_seqs, split, bs16, align, kv8, s); break;
     }
   }

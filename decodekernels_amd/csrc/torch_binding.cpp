@@ -103,8 +103,8 @@ void attention_impl(at::Tensor& out, const at::Tensor& q, const at::Tensor& k_ca
   const int64_t head_dim = q.size(2);
   const int64_t num_kv_heads = k_cache.size(2);
   TORCH_CHECK(k_cache.size(3) == head_dim, "cache head_dim does not match q");
-  TORCH_CHECK(head_dim == 64 || head_dim == 128 || head_dim == 256, "head_dim must be 64, 128 or 256, got ",
-              head_dim);
+  TORCH_CHECK(head_dim == 64 || head_dim == 96 || head_dim == 128 || head_dim == 192 || head_dim == 256,
+              "head_dim must be 64, 96, 128, 192 or 256, got ", head_dim);
   TORCH_CHECK(num_kv_heads > 0 && num_q_heads % num_kv_heads == 0, "num_q_heads must be a multiple of num_kv_heads");
   TORCH_CHECK(num_q_heads / num_kv_heads <= DK_MAX_GQA_GROUP, "GQA group size above ", DK_MAX_GQA_GROUP,
               " is not supported");
@@ -118,12 +118,13 @@ void attention_impl(at::Tensor& out, const at::Tensor& q, const at::Tensor& k_ca
     TORCH_CHECK(aligned(k_cache.data_ptr(), 8) && aligned(v_cache.data_ptr(), 8),
                 "fp8 KV-cache pointers and strides must be multiples of 8 bytes");
   } else {
-    const int64_t vec = head_dim / 32;
+    // Row starts aligned to 4 / 8 / 16 bytes for head_dim <= 64 / <= 128 / above.
+    const int64_t align = head_dim <= 64 ? 4 : (head_dim <= 128 ? 8 : 16);
     for (int d = 0; d < 3; ++d) {
-      TORCH_CHECK(k_cache.stride(d) % vec == 0 && v_cache.stride(d) % vec == 0,
+      TORCH_CHECK((k_cache.stride(d) * 2) % align == 0 && (v_cache.stride(d) * 2) % align == 0,
                   "KV-cache strides must be multiples of head_dim / 32 for vectorised loads");
     }
-    TORCH_CHECK(aligned(k_cache.data_ptr(), vec * 2) && aligned(v_cache.data_ptr(), vec * 2),
+    TORCH_CHECK(aligned(k_cache.data_ptr(), align) && aligned(v_cache.data_ptr(), align),
                 "KV-cache pointers must be aligned to head_dim / 16 bytes");
   }
   TORCH_CHECK(block_tables.scalar_type() == at::kInt && block_tables.dim() == 2 && block_tables.stride(1) == 1,

@@ -75,7 +75,8 @@ typedef struct dk_paged_attn_params {
  * Single-token decode attention over a paged KV cache, with flash-decoding
  * split-K when max_seq_len > DK_PARTITION_SIZE.
  * Replaces dk::launch_paged_attention_decode<T> (csrc/paged_attention.cuh:312-333).
- * head_dim in {64, 128, 256}; num_q_heads / num_kv_heads <= DK_MAX_GQA_GROUP.
+ * head_dim in {64, 96, 128, 192, 256} (the reference: 64, 128, 256);
+ * num_q_heads / num_kv_heads <= DK_MAX_GQA_GROUP.
  * max_seq_len is an upper bound on seq_lens that selects the single-pass or
  * split-K path; with split-K, p->max_partitions must be >= ceil(max_seq_len / 512).
  */

@@ -68,7 +68,7 @@ def _attn_params(num_q_heads=8, num_kv_heads=2, block_size=16, max_partitions=1)
     [
         (dict(num_q_heads=64, num_kv_heads=2), 128, 10, capi.DK_BFLOAT16, "GQA group"),
         (dict(num_q_heads=6, num_kv_heads=4), 128, 10, capi.DK_BFLOAT16, "multiple of num_kv_heads"),
-        (dict(), 96, 10, capi.DK_FLOAT16, "head_dim"),
+        (dict(), 80, 10, capi.DK_FLOAT16, "head_dim"),
         (dict(), 128, 10, 7, "float16 or bfloat16"),
         (dict(block_size=0), 128, 10, capi.DK_FLOAT16, "block_size"),
         (dict(), 128, -1, capi.DK_FLOAT16, "non-negative"),
@@ -226,7 +226,7 @@ def test_capi_fill_helpers_read_tensor_layouts():
 # Python wrappers (host logic only)
 # ---------------------------------------------------------------------------
 def test_constants_and_partitions():
-    assert dk.PARTITION_SIZE == 512 and dk.MAX_GQA_GROUP == 16 and dk.SUPPORTED_HEAD_DIMS == (64, 128, 256)
+    assert dk.PARTITION_SIZE == 512 and dk.MAX_GQA_GROUP == 16 and dk.SUPPORTED_HEAD_DIMS == (64, 96, 128, 192, 256)
     assert [dk.num_partitions(n) for n in (0, 1, 512, 513, 131072)] == [1, 1, 1, 2, 256]
 
 

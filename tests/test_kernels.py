@@ -173,6 +173,40 @@ def test_paged_attention_groups_above_8(dtype, head_dim, group):
     _check_attention(_q(len(short), group, head_dim, dtype, seed=group + 1), kv, dtype)
 
 
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("head_dim", [96, 192])
+@pytest.mark.parametrize("group", [1, 4, 8, 16])
+@pytest.mark.parametrize("layout", ["nhd", "vllm"])
+def test_paged_attention_head_dims_96_192(dtype, head_dim, group, layout):
+    """Head dims the reference rejects (Phi-3: 96; 192), single pass and split-K."""
+    lens = [1, 17, 300, 512, 513, 1500, 0, 2100]
+    kv = make_paged_kv(lens, 2, head_dim, 16, dtype, "cuda", layout=layout, seed=head_dim + group)
+    out = _check_attention(_q(len(lens), 2 * group, head_dim, dtype, seed=group), kv, dtype)
+    assert (out[6] == 0).all()
+
+
+@pytest.mark.parametrize("head_dim", [96, 192])
+@pytest.mark.parametrize("schedule", ["grid", "balanced"])
+def test_paged_attention_head_dims_96_192_long(head_dim, schedule, monkeypatch):
+    monkeypatch.setenv("DK_ATTN_SCHEDULE", schedule)
+    lens = _log_uniform_lens(24, 12000, seed=head_dim)
+    kv = make_paged_kv(lens, 4, head_dim, 32, torch.bfloat16, "cuda", layout="hnd", seed=head_dim)
+    _check_attention(_q(len(lens), 16, head_dim, torch.bfloat16, seed=5), kv, torch.bfloat16, max_seq_len=12000)
+
+
+def test_paged_attention_head_dim_192_fp8_cache():
+    lens = [5, 700, 3000, 1]
+    kv = make_paged_kv(lens, 2, 192, 16, torch.float8_e4m3fn, "cuda", layout="vllm", seed=8)
+    q = _q(len(lens), 16, 192, torch.float16, seed=6)
+    out = dk.paged_attention_decode(q, kv.k_cache, kv.v_cache, kv.block_tables, kv.seq_lens, k_scale=0.2, v_scale=0.9)
+    ref = attention_f32(q, kv.k_cache.float() * 0.2, kv.v_cache.float() * 0.9, kv.block_tables, kv.seq_lens)
+    assert_max_abs(out, ref, torch.float16, "head_dim 192, fp8 cache")
+    kv96 = make_paged_kv(lens, 2, 96, 16, torch.float8_e4m3fn, "cuda", seed=9)
+    with pytest.raises(RuntimeError, match="head_dim"):
+        dk.paged_attention_decode(_q(len(lens), 4, 96, torch.float16), kv96.k_cache, kv96.v_cache, kv96.block_tables,
+                                  kv96.seq_lens)
+
+
 @pytest.mark.parametrize("schedule", ["grid", "balanced"])
 def test_paged_attention_group_16_fp8_cache(schedule, monkeypatch):
     monkeypatch.setenv("DK_ATTN_SCHEDULE", schedule)
@@ -292,9 +326,9 @@ def test_paged_attention_rejects_bad_inputs():
     kv = make_paged_kv([10], 2, 128, 16, torch.float16, "cuda")
     with pytest.raises(RuntimeError, match="GQA group"):
         dk.paged_attention_decode(_q(1, 64, 128, torch.float16), kv.k_cache, kv.v_cache, kv.block_tables, kv.seq_lens)
-    kv96 = make_paged_kv([10], 2, 96, 16, torch.float16, "cuda")
+    kv80 = make_paged_kv([10], 2, 80, 16, torch.float16, "cuda")
     with pytest.raises(RuntimeError, match="head_dim"):
-        dk.paged_attention_decode(_q(1, 2, 96, torch.float16), kv96.k_cache, kv96.v_cache, kv96.block_tables, kv96.seq_lens)
+        dk.paged_attention_decode(_q(1, 2, 80, torch.float16), kv80.k_cache, kv80.v_cache, kv80.block_tables, kv80.seq_lens)
     with pytest.raises(RuntimeError, match="tmp_out must be"):
         ws = dk.alloc_workspace(1, 4, 128, 600, "cuda")
         dk.paged_attention_decode(_q(1, 4, 128, torch.float16), kv.k_cache, kv.v_cache, kv.block_tables, kv.seq_lens,

@@ -71,7 +71,7 @@ def test_attention_eligible_base_case():
         (dict(logits_soft_cap=30.0), {}, None),
         (dict(sliding_window=(128, 0)), {}, None),
         (dict(sinks=torch.zeros(HQ)), {}, None),
-        (dict(head_size=96), {}, None),
+        (dict(head_size=80), {}, None),
         (dict(num_heads=HKV * 32), {}, None),
         (dict(num_heads=7), {}, None),
         ({}, dict(max_query_len=4), None),
