@@ -102,6 +102,7 @@ struct KParams {
   int num_q_heads, group, block_size, max_partitions;
   int num_seqs, num_kv_heads;
   int num_units;  // split-K grid: unit positions per sequence, ceil(max_partitions / 2)
+  int pair_ratio;  // balanced kernel: share of workgroups [0, grid/2) over the others', x100
   float scale_log2;  // softmax scale x log2(e) (x k_scale for an fp8 cache)
   float v_scale;     // multiplies the output (fp8 cache's v_scale; 1 otherwise)
 };
@@ -675,6 +676,9 @@ constexpr int kMinShareTiles = 64;
 #define DK_ATTN_STREAM_COST 8  // per-stream overhead, in tiles, of the share balance
 #endif
 constexpr int kStreamCost = DK_ATTN_STREAM_COST;
+#ifndef DK_ATTN_PAIR_RATIO
+#define DK_ATTN_PAIR_RATIO 180  // with two workgroups per CU: first-half share / second-half share, x100
+#endif
 
 template <typename E, int D, bool BS16, int ALIGN, int NW, bool KV8>
 __global__ __launch_bounds__(NW * kWave) __attribute__((amdgpu_waves_per_eu(attn_occupancy<D, KV8>(),
@@ -721,11 +725,26 @@ void paged_attention_balanced_kernel(const KParams p) {
   const int hkv = p.num_kv_heads;
   const int total = pre[S] * hkv;  // < 2^31 (checked by the host)
   const int G = gridDim.x;
-  const int share = max(kMinShareTiles, (total + G - 1) / G);
+  // Shares: workgroups [0, H) take share_a each, [H, G) share_b.
+  const int H = G / 2;
+  int share_a, share_b;
+  {
+    const int64_t r = p.pair_ratio;
+    const int64_t denom = static_cast<int64_t>(H) * r + static_cast<int64_t>(G - H) * 100;
+    share_b = max(kMinShareTiles, static_cast<int>((static_cast<int64_t>(total) * 100 + denom - 1) / denom));
+    share_a = max(kMinShareTiles, static_cast<int>((static_cast<int64_t>(share_b) * r + 99) / 100));
+  }
+  const int64_t split_at = static_cast<int64_t>(H) * share_a;
+  auto first_pos = [&](int wg) -> int64_t {
+    return wg < H ? static_cast<int64_t>(wg) * share_a : split_at + static_cast<int64_t>(wg - H) * share_b;
+  };
+  auto owner = [&](int x) -> int {  // workgroup whose share holds cost position x
+    return x < split_at ? static_cast<int>(x / share_a) : H + static_cast<int>((x - split_at) / share_b);
+  };
   const int w = blockIdx.x;
-  const int a = w * share;
-  if (a >= total) return;
-  const int b = min(a + share, total);
+  if (first_pos(w) >= total) return;
+  const int a = static_cast<int>(first_pos(w));
+  const int b = static_cast<int>(min(first_pos(w + 1), static_cast<int64_t>(total)));
   auto cost_of = [&](int s) { return pre[s + 1] - pre[s]; };
 
   // Stream holding cost position a: the last sequence whose first position
@@ -763,7 +782,7 @@ void paged_attention_balanced_kernel(const KParams p) {
       hi = min(b, first + n) - first;
       if (lo < hi) {
         u = lo;
-        row = w - first / share;
+        row = w - owner(first);
         last_tile_here = hi == n;
         return true;
       }
@@ -961,7 +980,8 @@ constexpr int waves_per_group() {
 // `resident`, only reports how many balanced-kernel workgroups fit on the
 // current device at once (0 if unknown), cached per device.
 template <typename E, int D, int ALIGN, bool SPLIT, bool BS16, bool BALANCED, bool KV8>
-hipError_t launch_kernel(const KParams& kp, unsigned grid, hipStream_t stream, int* resident = nullptr) {
+hipError_t launch_kernel(const KParams& kp, unsigned grid, hipStream_t stream, int* resident = nullptr,
+                         int* per_cu_out = nullptr) {
   constexpr int NW = waves_per_group<D>();
   if constexpr (BALANCED) {
     const auto kernel = paged_attention_balanced_kernel<E, D, BS16, ALIGN, NW, KV8>;
@@ -970,18 +990,21 @@ hipError_t launch_kernel(const KParams& kp, unsigned grid, hipStream_t stream, i
       *resident = 0;
       int dev = 0;
       if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return hipSuccess;
+      // Packed (workgroups per CU) << 20 | CUs.
       int v = cache[dev].load(std::memory_order_relaxed);
       if (v <= 0) {
         int per_cu = 0;
         int cus = 0;
         if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void*>(kernel), NW * kWave, 0) !=
                 hipSuccess ||
-            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+            per_cu <= 0 || per_cu > 1023 || cus <= 0 || cus >= (1 << 20))
           return hipSuccess;
-        v = per_cu * cus;
+        v = (per_cu << 20) | cus;
         cache[dev].store(v, std::memory_order_relaxed);
       }
-      *resident = v;
+      *resident = (v >> 20) * (v & 0xfffff);
+      if (per_cu_out != nullptr) *per_cu_out = v >> 20;
       return hipSuccess;
     }
     hipLaunchKernelGGL(kernel, dim3(grid), dim3(NW * kWave), 0, stream, kp);
@@ -993,21 +1016,23 @@ hipError_t launch_kernel(const KParams& kp, unsigned grid, hipStream_t stream, i
 }
 
 template <typename E, int D, bool SPLIT, bool BS16, bool BALANCED, bool KV8>
-hipError_t launch_aligned(const KParams& kp, unsigned grid, int align, hipStream_t stream, int* resident = nullptr) {
+hipError_t launch_aligned(const KParams& kp, unsigned grid, int align, hipStream_t stream, int* resident = nullptr,
+                          int* per_cu = nullptr) {
   if constexpr (KV8) {
     // fp8 rows: 16-byte loads when 16-byte aligned, else pairs of 8-byte loads
     // (8-byte alignment is checked by the host).
-    if (align >= 16) return launch_kernel<E, D, 16, SPLIT, BS16, BALANCED, true>(kp, grid, stream, resident);
-    return launch_kernel<E, D, 8, SPLIT, BS16, BALANCED, true>(kp, grid, stream, resident);
+    if (align >= 16) return launch_kernel<E, D, 16, SPLIT, BS16, BALANCED, true>(kp, grid, stream, resident, per_cu);
+    return launch_kernel<E, D, 8, SPLIT, BS16, BALANCED, true>(kp, grid, stream, resident, per_cu);
   } else {
     switch (align) {
       case 16:
-        return launch_kernel<E, D, 16, SPLIT, BS16, BALANCED, false>(kp, grid, stream, resident);
+        return launch_kernel<E, D, 16, SPLIT, BS16, BALANCED, false>(kp, grid, stream, resident, per_cu);
       case 8:
-        if constexpr (D <= 128) return launch_kernel<E, D, 8, SPLIT, BS16, BALANCED, false>(kp, grid, stream, resident);
+        if constexpr (D <= 128)
+          return launch_kernel<E, D, 8, SPLIT, BS16, BALANCED, false>(kp, grid, stream, resident, per_cu);
         return hipErrorInvalidValue;
       case 4:
-        if constexpr (D == 64) return launch_kernel<E, D, 4, SPLIT, BS16, BALANCED, false>(kp, grid, stream, resident);
+        if constexpr (D == 64) return launch_kernel<E, D, 4, SPLIT, BS16, BALANCED, false>(kp, grid, stream, resident, per_cu);
         return hipErrorInvalidValue;
       default:
         return hipErrorInvalidValue;
@@ -1053,10 +1078,16 @@ hipError_t launch_split(KParams kp, int num_kv_heads, int num_seqs, int align, h
   const Schedule forced = forced_schedule();
   const int64_t tile_bound = per_plane * kp.max_partitions * (kPart / kTile);
   int resident = 0;
+  int per_cu = 0;
   if (num_seqs <= kMaxBalancedSeqs && tile_bound < (int64_t{1} << 30) && forced != Schedule::kGrid) {
-    const hipError_t e = launch_aligned<E, D, true, BS16, true, KV8>(kp, 0, align, stream, &resident);
+    const hipError_t e = launch_aligned<E, D, true, BS16, true, KV8>(kp, 0, align, stream, &resident, &per_cu);
     if (e != hipSuccess) return e;
   }
+  // Two workgroups per CU sharing its SIMDs (4 waves each): the one
+  // dispatched first (blockIdx < grid / 2; the second round of dispatch fills
+  // each CU's second slot) streams faster, so the first half of the grid
+  // takes the larger shares. (2-wave workgroups at 1 wave/SIMD do not share.)
+  kp.pair_ratio = per_cu == 2 && waves_per_group<D>() == 4 ? DK_ATTN_PAIR_RATIO : 100;
   hipError_t e;
   const bool balanced = resident > 0 && (forced == Schedule::kBalanced || grid_units > resident);
   if (balanced) {
