@@ -13,9 +13,10 @@
 //   activation tiles are loaded once per workgroup with contiguous 16-byte
 //   loads into LDS and shared by the waves that own different output columns.
 //   8 waves per workgroup, split between N (16 columns each) and K so that a
-//   launch keeps >= 192 workgroups; buffer loads with descriptor bounds make
-//   rows past M/N and columns past K read as zero, and a DEPTH-deep register
-//   ring keeps weight loads in flight across the per-step barrier.
+//   launch keeps >= 384 (M <= 16) or >= 192 workgroups; buffer loads with
+//   descriptor bounds make rows past M/N and columns past K read as zero, and
+//   DEPTH-deep register rings of weights and activations keep loads in flight
+//   across the per-step barrier.
 // * LDS-DMA (M > 64, batched decode and prefill): A and B tiles go from HBM
 //   straight into LDS (buffer_load ... lds), bank-conflict-free XOR-swizzled,
 //   through a multi-stage ring; five tile shapes from 256x256 down to 64x64,
@@ -51,9 +52,9 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base, int64_t
 // 16-byte loads (8 lanes cover a 128-byte row segment), written to LDS and
 // read by the WN waves of that group, so each activation byte crosses the
 // L1 once per workgroup instead of once per wave. Weight fragments go
-// straight from HBM to registers through a DEPTH-deep ring. All waves step
-// through the chunks together (one barrier per step); the WK partial tiles
-// are summed through LDS at the end.
+// straight from HBM to registers; weights and activations both run through
+// DEPTH-deep register rings. All waves step through the chunks together (one
+// barrier per step); the WK partial tiles are summed through LDS at the end.
 constexpr int kLdsBK = 64;
 constexpr int kLdsARow = kLdsBK + 8;  // padded LDS row (elements)
 
@@ -139,19 +140,27 @@ __global__ __launch_bounds__(WN * WK * kWave) void gemm_skinny_lds_kernel(const 
 #pragma unroll
   for (int i = 0; i < MT; ++i) acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
 
+  // Step j's weight fragments and activation vectors live in ring slot
+  // j % DEPTH; both are issued DEPTH steps ahead. Loads complete in issue
+  // order, so the wait for step j + 1's activations (stored to LDS during
+  // step j) covers only loads issued up to step j + 1 - DEPTH: DEPTH - 1
+  // steps of both operands stay in flight across each barrier.
   u32x4 bring[DEPTH][KS];
-  AR areg;
-  load_a(0, areg);
+  AR aring[DEPTH];
 #pragma unroll
-  for (int d = 0; d < DEPTH; ++d) load_b(d, bring[d]);
-  store_a(0, areg);
-  load_a(1, areg);
+  for (int d = 0; d < DEPTH; ++d) {
+    load_a(d, aring[d]);
+    load_b(d, bring[d]);
+  }
+  store_a(0, aring[0]);
+  load_a(DEPTH, aring[0]);
   __syncthreads();
 
   for (int base = 0; base < steps; base += DEPTH) {
 #pragma unroll
     for (int d = 0; d < DEPTH; ++d) {
       const int step = base + d;
+      const int d1 = (d + 1) % DEPTH;
       if (step < steps) {
         const uint16_t* at = lds_a[wk][step & 1];
 #pragma unroll
@@ -164,8 +173,8 @@ __global__ __launch_bounds__(WN * WK * kWave) void gemm_skinny_lds_kernel(const 
         }
       }
       load_b(step + DEPTH, bring[d]);
-      if (step + 1 < steps) store_a((step + 1) & 1, areg);
-      load_a(step + 2, areg);
+      if (step + 1 < steps) store_a((step + 1) & 1, aring[d1]);
+      load_a(step + 1 + DEPTH, aring[d1]);
       __syncthreads();
     }
   }
@@ -397,20 +406,38 @@ hipError_t launch_dma(const uint16_t* A, const uint16_t* B, const uint16_t* bias
   return hipGetLastError();
 }
 
+#ifndef DK_SKINNY_WAVES
+#define DK_SKINNY_WAVES 8  // waves per skinny workgroup
+#endif
+#ifndef DK_SKINNY_DEPTH
+#define DK_SKINNY_DEPTH 2  // k-steps of weights and activations in flight per wave
+#endif
+#ifndef DK_SKINNY_MIN_WGS
+#define DK_SKINNY_MIN_WGS 192  // fewest workgroups the N split may leave, M > 16
+#endif
+#ifndef DK_SKINNY_MIN_WGS_M16
+#define DK_SKINNY_MIN_WGS_M16 384  // the same for M <= 16
+#endif
+
 template <typename E>
 hipError_t launch(const uint16_t* A, const uint16_t* B, const uint16_t* bias, uint16_t* C, int M, int N, int K,
                   int lda, int ldb, int ldc, hipStream_t s) {
   if (M <= 64) {
     {
-      // 8 waves; as many along N as keep >= 192 workgroups (more columns per
-      // workgroup share each activation tile), the rest split K.
-      const int wn = (M > 32 && N >= 24576) ? 8 : (N >= 64 * 192 ? 4 : (N >= 32 * 192 ? 2 : 1));
+      // DK_SKINNY_WAVES waves; as many along N as keep enough workgroups
+      // (more columns per workgroup share each activation tile), the rest
+      // split K. Measured: with one 16-row activation tile (M <= 16) the
+      // activation traffic is small and 384 workgroups beat 192 (qkv, N =
+      // 6144); with 32 or 64 rows the activation tile reloads cost more.
+      constexpr int kW = DK_SKINNY_WAVES;
       const int mt = M <= 16 ? 1 : (M <= 32 ? 2 : 4);
+      const int min_wgs = mt == 1 ? DK_SKINNY_MIN_WGS_M16 : DK_SKINNY_MIN_WGS;
+      int wn = (M > 32 && N >= 24576) ? 8 : (N >= 64 * min_wgs ? 4 : (N >= 32 * min_wgs ? 2 : 1));
+      wn = wn > kW ? kW : wn;
       const dim3 g2(static_cast<unsigned>(ceil_div64(N, 16 * wn)));
-      const dim3 b2(8 * kWave);
-#define DK_SKINNY_LDS(MT_, WN_)                                                                               \
-  hipLaunchKernelGGL((gemm_skinny_lds_kernel<E, MT_, WN_, 8 / WN_, 3>), g2, b2, 0, s, A, B, bias, C, M, N, K, lda, \
-                     ldb, ldc)
+#define DK_SKINNY_LDS(MT_, WN_)                                                                          \
+  hipLaunchKernelGGL((gemm_skinny_lds_kernel<E, MT_, WN_, (kW / WN_ > 0 ? kW / WN_ : 1), DK_SKINNY_DEPTH>), g2, \
+                     dim3(WN_ * (kW / WN_ > 0 ? kW / WN_ : 1) * kWave), 0, s, A, B, bias, C, M, N, K, lda, ldb, ldc)
       switch (mt * 10 + wn) {
         case 11: DK_SKINNY_LDS(1, 1); break;
         case 12: DK_SKINNY_LDS(1, 2); break;
