@@ -872,7 +872,7 @@ __global__ __launch_bounds__(reduce_waves<WPH>() * kWave) void paged_attention_r
   constexpr int kReduceWaves = reduce_waves<WPH>();
   constexpr int C = (D + kWave - 1) / kWave;  // columns per lane (1-4); lanes past D / C idle
   constexpr int HPW = kReduceWaves / WPH;  // heads per workgroup
-  const int wave = static_cast<int>(threadIdx.x) / kWave;
+  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) / kWave);
   const int q_head = blockIdx.x * HPW + wave / WPH;
   const int sub = wave % WPH;
   const int seq = blockIdx.y;
@@ -881,26 +881,64 @@ __global__ __launch_bounds__(reduce_waves<WPH>() * kWave) void paged_attention_r
   const bool active = q_head < p.num_q_heads;
   const bool cols = C * lane < D;  // this lane owns output columns
   uint16_t* out = p.out + seq * p.o_ss + (active ? q_head : 0) * p.o_sh + (cols ? C * lane : 0);
-  const int seq_len = p.seq_lens[seq];
-  if (seq_len <= 0) {
-    if (active && sub == 0 && cols) {
-#pragma unroll
-      for (int c = 0; c < C; ++c) out[c] = 0;
-    }
-    return;
-  }
   const int64_t row0 = (static_cast<int64_t>(seq) * p.num_q_heads + (active ? q_head : 0)) * p.max_partitions;
   const float* ml = p.max_logits + row0;
   const float* es = p.exp_sums + row0;
   const float* tmp = p.tmp_out + row0 * D + (cols ? C * lane : 0);
+  const int P = p.max_partitions;
 
-  int entries;  // entries j map to rows row_of(j)
-  bool slot1 = true;
-  float M = -__builtin_huge_valf();
+  float acc[C];
+#pragma unroll
+  for (int c = 0; c < C; ++c) acc[c] = 0.0f;
+  auto load_row = [&](int i, float (&v)[C]) {
+    const float* t = tmp + static_cast<int64_t>(i) * D;
+    if constexpr (C == 4) {
+      const f32x4 x = *reinterpret_cast<const f32x4*>(t);
+#pragma unroll
+      for (int c = 0; c < 4; ++c) v[c] = x[c];
+    } else {
+#pragma unroll
+      for (int c = 0; c < C; ++c) v[c] = cols ? t[c] : 0.0f;
+    }
+  };
+  auto add_row = [&](float w, const float (&v)[C]) {
+#pragma unroll
+    for (int c = 0; c < C; ++c) acc[c] = fmaf(w, v[c], acc[c]);
+  };
+
+  float W = 0.0f;
   if constexpr (PIECES) {
-    const int P = p.max_partitions;
-    entries = P;
-    for (int base = 0; base < P; base += kWave) {
+    // Rows 0 .. n-1 hold the stream's pieces, row n (if < P) is marked
+    // empty. Everything that does not depend on n loads at once: the length,
+    // the first 64 (exp-sum, max-logit) pairs (lane j holds row j's) and the
+    // first kPre rows this wave merges (rows are in the workspace whatever n
+    // is; values past n are never used).
+    constexpr int kPre = 2;
+    const int seq_len = p.seq_lens[seq];
+    const bool in0 = lane < P;
+    const float e_l = in0 ? es[lane] : 0.0f;
+    const float m_l = in0 ? ml[lane] : -__builtin_huge_valf();
+    float pre[kPre][C];
+#pragma unroll
+    for (int r = 0; r < kPre; ++r) {
+      if (sub + r * WPH < P) load_row(sub + r * WPH, pre[r]);
+    }
+    if (seq_len <= 0) {
+      if (active && sub == 0 && cols) {
+#pragma unroll
+        for (int c = 0; c < C; ++c) out[c] = 0;
+      }
+      return;
+    }
+    int entries = P;
+    float M = -__builtin_huge_valf();
+    {
+      const unsigned long long z = __ballot(e_l == 0.0f);  // lanes past P count as empty
+      const int t = z != 0 ? __ffsll(static_cast<long long>(z)) - 1 : kWave;
+      if (lane < t) M = m_l;
+      if (z != 0) entries = t;
+    }
+    for (int base = kWave; entries == P && base < P; base += kWave) {  // more than 64 rows
       const int j = base + lane;
       const bool in = j < P;
       const float e = in ? es[j] : 0.0f;
@@ -908,38 +946,64 @@ __global__ __launch_bounds__(reduce_waves<WPH>() * kWave) void paged_attention_r
       const unsigned long long z = __ballot(e == 0.0f);
       const int t = z != 0 ? __ffsll(static_cast<long long>(z)) - 1 : kWave;
       if (lane < t) M = fmaxf(M, m);
-      if (z != 0) {
-        entries = base + t;
-        break;
+      if (z != 0) entries = base + t;
+    }
+    M = wave_max(M);
+#pragma unroll
+    for (int r = 0; r < kPre; ++r) {
+      const int j = sub + r * WPH;  // wave-uniform; rows < 64 come from the lanes that loaded them
+      if (j < entries) {
+        float e, m;
+        if (j < kWave) {
+          e = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, e_l), j));
+          m = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, m_l), j));
+        } else {
+          e = es[j];
+          m = ml[j];
+        }
+        const float w = e * __builtin_amdgcn_exp2f((m - M) * kLog2e);
+        W += w;
+        add_row(w, pre[r]);
       }
     }
+    // The rest: plain loads (a cross-lane read in this runtime-count loop
+    // would keep it from unrolling, and the unrolled loads overlap).
+#pragma unroll 4
+    for (int j = sub + kPre * WPH; j < entries; j += WPH) {
+      const float w = es[j] * __builtin_amdgcn_exp2f((ml[j] - M) * kLog2e);
+      W += w;
+      float v[C];
+      load_row(j, v);
+      add_row(w, v);
+    }
   } else {
-    const int n = min((seq_len + kPart - 1) / kPart, p.max_partitions);
-    entries = 2 + (n - 1) / 2;  // slot 0, slot 1, then slot 2 (j - 1)
-    slot1 = n > 1 && es[1] != 0.0f;
+    // Rows p = tokens [512 p, 512 p + 512): results in rows 0, 1 and the
+    // even rows >= 2, walked by index.
+    const int seq_len = p.seq_lens[seq];
+    if (seq_len <= 0) {
+      if (active && sub == 0 && cols) {
+#pragma unroll
+        for (int c = 0; c < C; ++c) out[c] = 0;
+      }
+      return;
+    }
+    const int n = min((seq_len + kPart - 1) / kPart, P);
+    const int entries = 2 + (n - 1) / 2;  // slot 0, slot 1, then slot 2 (j - 1)
+    const bool slot1 = n > 1 && es[1] != 0.0f;
+    float M = -__builtin_huge_valf();
     for (int j = lane; j < entries; j += kWave) {
       if (j != 1 || slot1) M = fmaxf(M, ml[j < 2 ? j : 2 * (j - 1)]);
     }
-  }
-  M = wave_max(M);
-  float W = 0.0f;
-  float acc[C];
-#pragma unroll
-  for (int c = 0; c < C; ++c) acc[c] = 0.0f;
+    M = wave_max(M);
 #pragma unroll 4
-  for (int j = sub; j < entries; j += WPH) {
-    if (!PIECES && j == 1 && !slot1) continue;
-    const int i = PIECES ? j : (j < 2 ? j : 2 * (j - 1));
-    const float w = es[i] * __builtin_amdgcn_exp2f((ml[i] - M) * kLog2e);
-    W += w;
-    const float* t = tmp + static_cast<int64_t>(i) * D;
-    if constexpr (C == 4) {
-      const f32x4 v = *reinterpret_cast<const f32x4*>(t);
-#pragma unroll
-      for (int c = 0; c < 4; ++c) acc[c] = fmaf(w, v[c], acc[c]);
-    } else if (cols) {
-#pragma unroll
-      for (int c = 0; c < C; ++c) acc[c] = fmaf(w, t[c], acc[c]);
+    for (int j = sub; j < entries; j += WPH) {
+      if (j == 1 && !slot1) continue;
+      const int i = j < 2 ? j : 2 * (j - 1);
+      const float w = es[i] * __builtin_amdgcn_exp2f((ml[i] - M) * kLog2e);
+      W += w;
+      float v[C];
+      load_row(i, v);
+      add_row(w, v);
     }
   }
   if constexpr (WPH > 1) {
