@@ -380,6 +380,31 @@ def test_gemm_decode_layer_shapes(M, N):
     assert_max_abs(dk.gemm(a, b), gemm_f32(a, b), torch.bfloat16, f"gemm {M}x{N}")
 
 
+# Every (row tiles, waves along N) pair the skinny launch policy picks, with
+# ragged N and K: M <= 16 splits N into >= 384 workgroups (1/2/4 waves along
+# N at N < 12288 / < 24576 / above), 16 < M <= 64 into >= 192 (1/2/4 waves,
+# and 8 for M > 32 with N >= 24576).
+SKINNY_POLICY_SHAPES = [
+    (1, 12328, 520),  # 1 row tile, 2 waves along N
+    (16, 24600, 136),  # 1 row tile, 4 waves along N
+    (17, 6152, 1032),  # 2 row tiles, 2 waves along N
+    (32, 12296, 136),  # 2 row tiles, 4 waves along N
+    (33, 1000, 4104),  # 4 row tiles, 1 wave along N
+    (40, 6168, 520),  # 4 row tiles, 2 waves along N
+    (63, 12304, 136),  # 4 row tiles, 4 waves along N
+    (64, 24584, 136),  # 4 row tiles, 8 waves along N
+]
+
+
+@pytest.mark.parametrize("M,N,K", SKINNY_POLICY_SHAPES)
+def test_gemm_skinny_policy_boundaries(M, N, K):
+    g = torch.Generator(device="cuda").manual_seed(M * 7 + K)
+    a = torch.randn(M, K, generator=g, device="cuda", dtype=torch.bfloat16)
+    b = torch.randn(N, K, generator=g, device="cuda", dtype=torch.bfloat16) / K**0.5
+    bias = torch.randn(N, generator=g, device="cuda", dtype=torch.bfloat16)
+    assert_max_abs(dk.gemm(a, b, bias), gemm_f32(a, b, bias), torch.bfloat16, f"gemm {M}x{N}x{K}")
+
+
 def test_gemm_batched_input_and_strided_rows():
     a = torch.randn(2, 3, 256, device="cuda", dtype=torch.float16)
     b = torch.randn(80, 256, device="cuda", dtype=torch.float16) / 16
