@@ -503,6 +503,7 @@ def main() -> int:
         "roofline": {
             "bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
+            "kernel": "one paged_attention_decode call: paged_attention_balanced_kernel + paged_attention_reduce_kernel",
         },
     }
     if not args.no_cpu:
