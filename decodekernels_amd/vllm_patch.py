@@ -16,10 +16,13 @@ handle, with counters so a silent fallback cannot pass for a result.
 * ``RMSNorm.forward_cuda`` -- rms_norm / fused_add_rms_norm.
 * ``SiluAndMul.forward_cuda`` -- silu_and_mul.
 
-Prefill and mixed batches, quantized KV caches, sliding windows, ALiBi,
-soft-capping, attention sinks, context parallelism, cross/encoder attention and
-graph capture all go to vLLM's implementation
-(reference: decode_kernels/vllm_patch.py:60-99).
+Prefill and mixed batches, sliding windows, ALiBi, soft-capping, attention
+sinks, context parallelism, cross/encoder attention and graph capture all go to
+vLLM's implementation (reference: decode_kernels/vllm_patch.py:60-99). Unlike
+the reference, an fp8 KV cache (``kv_cache_dtype`` "fp8" / "fp8_e4m3", OCP
+e4m3fn -- vLLM's fp8 on gfx950) with float scales on the layer runs
+``paged_attention_decode_fp8``; other quantized caches (e4m3fnuz, e5m2, ...)
+fall back.
 """
 
 from __future__ import annotations
@@ -87,8 +90,36 @@ def split_kv_cache(kv_cache: torch.Tensor, head_size: int):
     return None
 
 
-def _attention_eligible(impl, query, kv_cache, attn_metadata, output, output_scale, output_block_scale) -> bool:
-    """The reference's eligibility rules (decode_kernels/vllm_patch.py:60-99), plus a cache-layout check."""
+def _platform_fp8_is_e4m3fn() -> bool:
+    """True when vLLM's fp8 storage format on this platform is OCP e4m3fn (gfx950; gfx942 uses e4m3fnuz)."""
+    try:
+        from vllm.platforms import current_platform
+
+        return current_platform.fp8_dtype() == torch.float8_e4m3fn
+    except Exception:  # noqa: BLE001  (vLLM absent or no such query: not known to be e4m3fn)
+        return False
+
+
+def fp8_kv_scales(impl, kv_cache: torch.Tensor, layer) -> tuple[float, float] | None:
+    """(k_scale, v_scale) when vLLM's KV cache is fp8 e4m3fn -- stored as
+    float8_e4m3fn, or as uint8 on a platform whose fp8 is e4m3fn -- and the
+    layer carries its scales as floats (``_k_scale_float`` / ``_v_scale_float``,
+    read without a device sync); None otherwise."""
+    if str(getattr(impl, "kv_cache_dtype", "auto")) not in ("fp8", "fp8_e4m3"):
+        return None
+    if kv_cache.dtype != torch.float8_e4m3fn and not (kv_cache.dtype == torch.uint8 and _platform_fp8_is_e4m3fn()):
+        return None
+    k_scale = getattr(layer, "_k_scale_float", None)
+    v_scale = getattr(layer, "_v_scale_float", None)
+    if not all(isinstance(x, float) and 0.0 < x < float("inf") for x in (k_scale, v_scale)):
+        return None
+    return k_scale, v_scale
+
+
+def _attention_eligible(impl, query, kv_cache, attn_metadata, output, output_scale, output_block_scale,
+                        layer=None) -> bool:
+    """The reference's eligibility rules (decode_kernels/vllm_patch.py:60-99), plus a cache-layout check
+    and fp8 (e4m3fn) caches with float scales on ``layer``."""
     if attn_metadata is None or output_scale is not None or output_block_scale is not None:
         return False
     if query.is_cuda and torch.cuda.is_current_stream_capturing():
@@ -101,7 +132,10 @@ def _attention_eligible(impl, query, kv_cache, attn_metadata, output, output_sca
         return False
     if getattr(impl, "dcp_world_size", 1) > 1:
         return False
-    if str(getattr(impl, "kv_cache_dtype", "auto")) not in ("auto", "float16", "bfloat16") or kv_cache.dtype != query.dtype:
+    if str(getattr(impl, "kv_cache_dtype", "auto")) in ("auto", "float16", "bfloat16"):
+        if kv_cache.dtype != query.dtype:
+            return False
+    elif fp8_kv_scales(impl, kv_cache, layer) is None:
         return False
     if query.dtype not in _HALF_TYPES:
         return False
@@ -135,10 +169,16 @@ def _make_attention_forward(original):
     def forward(self, layer, query, key, value, kv_cache, attn_metadata, output=None, output_scale=None,
                 output_block_scale=None, *args, **kwargs):
         if output is not None and not args and not kwargs and _attention_eligible(
-            self, query, kv_cache, attn_metadata, output, output_scale, output_block_scale
+            self, query, kv_cache, attn_metadata, output, output_scale, output_block_scale, layer
         ):
             n = attn_metadata.num_actual_tokens
             key_cache, value_cache = split_kv_cache(kv_cache, self.head_size)
+            scales = {}
+            fp8 = fp8_kv_scales(self, kv_cache, layer)
+            if fp8 is not None:  # uint8 storage read as e4m3fn, in place
+                key_cache = key_cache.view(torch.float8_e4m3fn)
+                value_cache = value_cache.view(torch.float8_e4m3fn)
+                scales = {"k_scale": fp8[0], "v_scale": fp8[1]}
             q = query[:n].reshape(n, self.num_heads, self.head_size)
             out = output[:n].view(n, self.num_heads, self.head_size)
             dk_ops.paged_attention_decode(
@@ -150,6 +190,7 @@ def _make_attention_forward(original):
                 scale=self.scale,
                 max_seq_len=attn_metadata.max_seq_len,
                 out=out,
+                **scales,
             )
             _STATS["attention_kernel_calls"] += 1
             return output

@@ -108,6 +108,63 @@ def test_attention_fallback_branches(impl_over, meta_over, other):
 
 
 # ---------------------------------------------------------------------------
+# fp8 (e4m3fn) KV caches
+# ---------------------------------------------------------------------------
+def _platform(monkeypatch, fp8_dtype):
+    """A fake ``vllm.platforms`` whose current_platform stores fp8 as ``fp8_dtype``."""
+    for name in ("vllm",):
+        monkeypatch.setitem(sys.modules, name, types.ModuleType(name))
+    mod = types.ModuleType("vllm.platforms")
+    mod.current_platform = SimpleNamespace(fp8_dtype=lambda: fp8_dtype)
+    monkeypatch.setitem(sys.modules, "vllm.platforms", mod)
+
+
+def _fp8_inputs(storage=torch.uint8):
+    q, kv, meta, out = _inputs()
+    kv8 = kv.to(torch.float8_e4m3fn)
+    return q, (kv8.view(torch.uint8) if storage == torch.uint8 else kv8), meta, out
+
+
+def test_fp8_cache_eligible_on_e4m3fn_platform(monkeypatch):
+    _platform(monkeypatch, torch.float8_e4m3fn)
+    q, kv, meta, out = _fp8_inputs()
+    layer = SimpleNamespace(_k_scale_float=0.5, _v_scale_float=2.0)
+    impl = _impl(kv_cache_dtype="fp8")
+    assert vllm_patch.fp8_kv_scales(impl, kv, layer) == (0.5, 2.0)
+    assert vllm_patch._attention_eligible(impl, q, kv, meta, out, None, None, layer)
+    # an e4m3fn tensor needs no platform query
+    _, kv8, _, _ = _fp8_inputs(torch.float8_e4m3fn)
+    assert vllm_patch._attention_eligible(_impl(kv_cache_dtype="fp8_e4m3"), q, kv8, meta, out, None, None, layer)
+
+
+@pytest.mark.parametrize("case", ["fnuz_platform", "no_platform", "no_scales", "tensor_scales", "zero_scale", "e5m2",
+                                  "fnuz_tensor", "auto_with_uint8"])
+def test_fp8_cache_fallbacks(monkeypatch, case):
+    _platform(monkeypatch, torch.float8_e4m3fn)
+    q, kv, meta, out = _fp8_inputs()
+    layer = SimpleNamespace(_k_scale_float=0.5, _v_scale_float=2.0)
+    impl = _impl(kv_cache_dtype="fp8")
+    if case == "fnuz_platform":
+        _platform(monkeypatch, torch.float8_e4m3fnuz)
+    elif case == "no_platform":
+        monkeypatch.delitem(sys.modules, "vllm.platforms")
+        monkeypatch.setitem(sys.modules, "vllm.platforms", None)  # import fails
+    elif case == "no_scales":
+        layer = SimpleNamespace()
+    elif case == "tensor_scales":
+        layer = SimpleNamespace(_k_scale_float=torch.tensor(0.5), _v_scale_float=torch.tensor(2.0))
+    elif case == "zero_scale":
+        layer = SimpleNamespace(_k_scale_float=0.0, _v_scale_float=2.0)
+    elif case == "e5m2":
+        impl = _impl(kv_cache_dtype="fp8_e5m2")
+    elif case == "fnuz_tensor":
+        kv = kv.view(torch.float8_e4m3fnuz)
+    elif case == "auto_with_uint8":
+        impl = _impl(kv_cache_dtype="auto")
+    assert not vllm_patch._attention_eligible(impl, q, kv, meta, out, None, None, layer)
+
+
+# ---------------------------------------------------------------------------
 # Patch mechanics against fake vLLM modules
 # ---------------------------------------------------------------------------
 @pytest.fixture
@@ -171,6 +228,27 @@ def test_attention_patch_routes_decode_batches(fake_vllm):
     assert kwargs["max_seq_len"] == 5 and kwargs["out"].data_ptr() == out.data_ptr()
     meta.max_query_len = 2  # prefill / mixed batch
     impl.forward(None, q, None, None, kv, meta, out)
+    assert fake_vllm.calls[-1] == "vllm_attention"
+    assert vllm_patch.stats()["attention_kernel_calls"] == 1
+    assert vllm_patch.stats()["attention_fallback_calls"] == 1
+
+
+def test_attention_patch_routes_fp8_caches_with_scales(fake_vllm, monkeypatch):
+    _platform(monkeypatch, torch.float8_e4m3fn)
+    vllm_patch.apply(["attention"])
+    impl = fake_vllm.FlashAttentionImpl()
+    for k, v in vars(_impl(kv_cache_dtype="fp8")).items():
+        setattr(impl, k, v)
+    q, kv, meta, out = _fp8_inputs()
+    layer = SimpleNamespace(_k_scale_float=0.25, _v_scale_float=4.0)
+    assert impl.forward(layer, q, None, None, kv, meta, out) is out
+    kind, args, kwargs = fake_vllm.calls[-1]
+    assert kind == "dk_attention"
+    assert args[1].dtype == torch.float8_e4m3fn and args[2].dtype == torch.float8_e4m3fn
+    assert args[1].data_ptr() == kv.data_ptr() and args[1].shape == (10, BS, HKV, D)
+    assert torch.equal(args[2][:, :, 0, :].view(torch.uint8), kv.transpose(1, 2)[:, :, 0, D:])
+    assert kwargs["k_scale"] == 0.25 and kwargs["v_scale"] == 4.0
+    impl.forward(SimpleNamespace(), q, None, None, kv, meta, out)  # no scales on the layer -> vLLM
     assert fake_vllm.calls[-1] == "vllm_attention"
     assert vllm_patch.stats()["attention_kernel_calls"] == 1
     assert vllm_patch.stats()["attention_fallback_calls"] == 1
