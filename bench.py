@@ -265,12 +265,14 @@ def c5_seq_lens(num_seqs: int = 256, seed: int = 5) -> list:
 
 def layer_step(num_seqs, hq, hkv, d, bs, seq_lens, dtype, layout, seed, hidden=4096, inter=14336):
     """One random-init decoder layer's decode step on this path: fused_add_rms_norm
-    -> qkv gemm -> rotary embedding of the q and k columns -> the new token's k
-    and v columns written to its cache slot -> paged attention (q read in place
-    from the qkv output) -> o gemm -> fused_add_rms_norm -> gate_up gemm ->
-    silu_and_mul -> down gemm. The new token is the last of each sequence
-    (position len - 1). Returns the per-op callables and the bytes the step
-    must move."""
+    -> qkv gemm -> rotary embedding of the q and k columns and the new token's
+    k and v columns written to its cache slot (one launch,
+    rotary_embedding_and_cache) -> paged attention (q read in place from the
+    qkv output) -> o gemm -> fused_add_rms_norm -> gate_up gemm -> silu_and_mul
+    -> down gemm. The new token is the last of each sequence (position
+    len - 1). Returns the step's per-op callables, the two unfused ops the
+    fused one replaces (timed for comparison only) and the bytes the step must
+    move."""
     g = torch.Generator(device="cuda").manual_seed(seed)
     kw = dict(device="cuda", dtype=dtype)
     nqkv = 6144  # Llama-3-8B's fused q|k|v projection; q is its first hq * d columns
@@ -302,8 +304,8 @@ def layer_step(num_seqs, hq, hkv, d, bs, seq_lens, dtype, layout, seed, hidden=4
     ops = {
         "fused_add_rms_norm": lambda: dko.fused_add_rms_norm(x, resid, ln1, 1e-5),
         "qkv_gemm": lambda: dko.gemm_tn(qkv, x, w_qkv, None),
-        "rotary_embedding": lambda: dko.rotary_embedding(positions, qkv[:, : hq * d], k_new, d, rope, True),
-        "cache_write": lambda: dko.reshape_and_cache(k_new, v_new, case["k"], case["v"], slots),
+        "rotary_embedding_and_cache": lambda: dko.rotary_embedding_and_cache(
+            positions, qkv[:, : hq * d], k_new, v_new, d, rope, True, case["k"], case["v"], slots),
         "attention": lambda: dk.paged_attention_decode(q, case["k"], case["v"], case["bt"], case["lens"],
                                                        max_seq_len=max_len, out=attn, workspace=ws),
         "o_gemm": lambda: dko.gemm_tn(o, attn.view(num_seqs, hq * d), w_o, None),
@@ -315,7 +317,11 @@ def layer_step(num_seqs, hq, hkv, d, bs, seq_lens, dtype, layout, seed, hidden=4
     elt = torch.finfo(dtype).bits // 8
     nbytes = case["bytes"] + elt * (w_qkv.numel() + w_o.numel() + w_gu.numel() + w_down.numel())
     nbytes += num_seqs * (2 * (hq + hkv) * d * elt + d * 4 + 4 * hkv * d * elt)  # rope rows + table row, k/v copy
-    return ops, nbytes
+    unfused = {
+        "rotary_embedding": lambda: dko.rotary_embedding(positions, qkv[:, : hq * d], k_new, d, rope, True),
+        "cache_write": lambda: dko.reshape_and_cache(k_new, v_new, case["k"], case["v"], slots),
+    }
+    return ops, unfused, nbytes
 
 
 def extras_layer_step() -> dict:
@@ -333,7 +339,7 @@ def extras_layer_step() -> dict:
                                 torch.bfloat16, "vllm")),
     )
     for name, args in cases:
-        ops, nbytes = layer_step(*args, seed=50)
+        ops, unfused, nbytes = layer_step(*args, seed=50)
 
         def step():
             for fn in ops.values():
@@ -342,6 +348,7 @@ def extras_layer_step() -> dict:
         step()
         torch.cuda.synchronize()
         per_op = {k: time_cold(fn, iters=20)["median_us"] for k, fn in ops.items()}
+        unfused_us = {k: time_cold(fn, iters=20)["median_us"] for k, fn in unfused.items()}
         eager_us = time_back_to_back(step, 20, 3) * 1e3
         side = torch.cuda.Stream()
         side.wait_stream(torch.cuda.current_stream())
@@ -355,6 +362,7 @@ def extras_layer_step() -> dict:
         res[name] = {
             "eager_us": round(eager_us, 1), "graph_us": round(graph_us, 1),
             "sum_of_cold_ops_us": round(sum(per_op.values()), 1), "ops_cold_us": per_op,
+            "unfused_rope_and_cache_cold_us": unfused_us,
             "weights_plus_kv_MB": round(nbytes / 1e6, 1),
             "graph_GB/s": round(nbytes / (graph_us * 1e-6) / 1e9, 1),
         }

@@ -7,7 +7,8 @@ Same public API as DecodeKernels' ``decode_kernels`` package
 (``decode_kernels/__init__.py:7-27``); the ops are registered under the same
 ``torch.ops.decode_kernels.*`` names. ``rotary_embedding`` and
 ``reshape_and_cache`` add the two steps around attention that the reference
-leaves to vLLM (vLLM's signatures).
+leaves to vLLM (vLLM's signatures); ``rotary_embedding_and_cache`` runs both
+in one launch.
 """
 
 from .ops import (
@@ -23,6 +24,7 @@ from .ops import (
     reshape_and_cache,
     rms_norm,
     rotary_embedding,
+    rotary_embedding_and_cache,
     silu_and_mul,
 )
 
@@ -39,6 +41,7 @@ __all__ = [
     "reshape_and_cache",
     "rms_norm",
     "rotary_embedding",
+    "rotary_embedding_and_cache",
     "silu_and_mul",
 ]
 __version__ = "0.1.0"

@@ -150,6 +150,10 @@ _SIGNATURES = {
         ctypes.c_int,
         [ctypes.POINTER(CacheWriteParams), ctypes.c_int, ctypes.c_void_p],
     ),
+    "dk_rotary_embedding_and_cache": (
+        ctypes.c_int,
+        [ctypes.POINTER(RotaryParams), ctypes.POINTER(CacheWriteParams), ctypes.c_int, ctypes.c_void_p],
+    ),
     "dk_last_error": (ctypes.c_char_p, []),
     "dk_error_string": (ctypes.c_char_p, [ctypes.c_int]),
     "dk_version": (ctypes.c_char_p, []),

@@ -179,25 +179,172 @@ __global__ __launch_bounds__(kThreads) void reshape_and_cache_kernel(const KPara
 }
 
 }  // namespace cache
+
+namespace rope_cache {
+
+constexpr int kThreads = 256;
+
+struct KParams {
+  rope::KParams r;   // positions, q, k (rotated in place), cos | sin table
+  cache::KParams c;  // key (== r.k), value, caches, slots
+};
+
+// rotary_embedding followed by reshape_and_cache in one launch, one
+// workgroup per token. The thread that rotates a pair of k also writes it to
+// the cache slot (nothing is read back after it is written), the k columns
+// past rot_dim and the v row are copied. Identical results to the two ops in
+// sequence: same per-pair arithmetic, and a skipped position (outside the
+// table) caches the unrotated k, a skipped slot rotates without caching.
+// VEC: 4 pairs per rotation step and 16-byte copies; else one element.
+template <typename E, typename CT, bool NEOX, bool VEC>
+__global__ __launch_bounds__(kThreads) void rotary_and_cache_kernel(const KParams p) {
+  constexpr int VW = VEC ? 4 : 1;
+  constexpr int VC = VEC ? 8 : 1;
+  const int t = blockIdx.x;
+  const rope::KParams& r = p.r;
+  const cache::KParams& c = p.c;
+  const int64_t pos = r.positions[t];
+  const bool rot = pos >= 0 && pos < r.max_position;
+  const int64_t slot = c.slots[t];
+  const int64_t blk = slot >= 0 ? slot / c.block_size : 0;
+  const int64_t off = slot - blk * c.block_size;
+  const bool put = slot >= 0 && blk < c.num_blocks;
+  if (!rot && !put) return;
+  const int half = r.rot_dim / 2;
+  const int64_t crow = pos * r.cache_stride;
+  const int steps = half / VW;         // rotation steps per head
+  const int rot_items = (r.hq + r.hkv) * steps;
+  const int tail = (c.d - r.rot_dim) / VC;  // k copy chunks past rot_dim, per head
+  const int vrow = c.d / VC;               // v copy chunks per head
+  const int copy_items = put ? c.hkv * (tail + vrow) : 0;
+  for (int it = threadIdx.x; it < rot_items + copy_items; it += kThreads) {
+    if (it < rot_items) {
+      const int h = it / steps;
+      const int i0 = (it - h * steps) * VW;
+      const bool is_k = h >= r.hq;
+      if (!is_k && !rot) continue;
+      if (is_k && !rot && !put) continue;
+      const int hk = h - r.hq;
+      uint16_t* v = is_k ? r.k + t * r.k_st + hk * r.k_sh : r.q + t * r.q_st + h * r.q_sh;
+      uint16_t* kc = is_k ? c.kc + blk * c.kc_sb + off * c.kc_st + hk * c.kc_sh : nullptr;
+      // Element offsets of the VW x / y values: NeoX x at i0.., y at half + i0..; GPT-J interleaved at 2 i0.
+      float x[VW], y[VW], ox[VW], oy[VW];
+      if constexpr (NEOX) {
+        if constexpr (VEC) {
+          const u32x2 a = *reinterpret_cast<const u32x2*>(v + i0);
+          const u32x2 b = *reinterpret_cast<const u32x2*>(v + half + i0);
+          x[0] = E::lo(a[0]), x[1] = E::hi(a[0]), x[2] = E::lo(a[1]), x[3] = E::hi(a[1]);
+          y[0] = E::lo(b[0]), y[1] = E::hi(b[0]), y[2] = E::lo(b[1]), y[3] = E::hi(b[1]);
+        } else {
+          x[0] = E::to_float(v[i0]);
+          y[0] = E::to_float(v[half + i0]);
+        }
+      } else {
+        if constexpr (VEC) {
+          const u32x4 a = *reinterpret_cast<const u32x4*>(v + 2 * i0);
+#pragma unroll
+          for (int j = 0; j < 4; ++j) x[j] = E::lo(a[j]), y[j] = E::hi(a[j]);
+        } else {
+          x[0] = E::to_float(v[2 * i0]);
+          y[0] = E::to_float(v[2 * i0 + 1]);
+        }
+      }
+      if (rot) {
+#pragma unroll
+        for (int j = 0; j < VW; ++j) {
+          const float cs = rope::table<E, CT>(r.cache, crow + i0 + j);
+          const float sn = rope::table<E, CT>(r.cache, crow + half + i0 + j);
+          rope::rotate(x[j], y[j], cs, sn, ox[j], oy[j]);
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < VW; ++j) ox[j] = x[j], oy[j] = y[j];
+      }
+      // Destinations: the row itself (rotated only) and, for k, the cache slot.
+      uint16_t* dst[2] = {rot ? v : nullptr, is_k && put ? kc : nullptr};
+#pragma unroll
+      for (int d = 0; d < 2; ++d) {
+        uint16_t* o = dst[d];
+        if (o == nullptr) continue;
+        if constexpr (NEOX) {
+          if constexpr (VEC) {
+            *reinterpret_cast<u32x2*>(o + i0) = u32x2{pack2<E>(ox[0], ox[1]), pack2<E>(ox[2], ox[3])};
+            *reinterpret_cast<u32x2*>(o + half + i0) = u32x2{pack2<E>(oy[0], oy[1]), pack2<E>(oy[2], oy[3])};
+          } else {
+            o[i0] = E::from_float(ox[0]);
+            o[half + i0] = E::from_float(oy[0]);
+          }
+        } else {
+          if constexpr (VEC) {
+            u32x4 w;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) w[j] = pack2<E>(ox[j], oy[j]);
+            *reinterpret_cast<u32x4*>(o + 2 * i0) = w;
+          } else {
+            o[2 * i0] = E::from_float(ox[0]);
+            o[2 * i0 + 1] = E::from_float(oy[0]);
+          }
+        }
+      }
+    } else {
+      // Copies: k columns past rot_dim, then the v row.
+      const int cc = it - rot_items;
+      const bool is_v = cc >= c.hkv * tail;
+      const int ci = is_v ? cc - c.hkv * tail : cc;
+      const int per = is_v ? vrow : tail;
+      const int h = ci / per;
+      const int d0 = (is_v ? 0 : r.rot_dim) + (ci - h * per) * VC;
+      const uint16_t* src = is_v ? c.value + t * c.v_st + h * c.v_sh + d0 : c.key + t * c.k_st + h * c.k_sh + d0;
+      uint16_t* dst = is_v ? c.vc + blk * c.vc_sb + off * c.vc_st + h * c.vc_sh + d0
+                           : c.kc + blk * c.kc_sb + off * c.kc_st + h * c.kc_sh + d0;
+      if constexpr (VEC) {
+        *reinterpret_cast<u32x4*>(dst) = *reinterpret_cast<const u32x4*>(src);
+      } else {
+        *dst = *src;
+      }
+    }
+  }
+}
+
+template <typename E, typename CT>
+hipError_t launch(const KParams& kp, bool neox, bool vec, hipStream_t s) {
+  const dim3 grid(kp.r.num_tokens), block(kThreads);
+  if (neox) {
+    if (vec) hipLaunchKernelGGL((rotary_and_cache_kernel<E, CT, true, true>), grid, block, 0, s, kp);
+    else hipLaunchKernelGGL((rotary_and_cache_kernel<E, CT, true, false>), grid, block, 0, s, kp);
+  } else {
+    if (vec) hipLaunchKernelGGL((rotary_and_cache_kernel<E, CT, false, true>), grid, block, 0, s, kp);
+    else hipLaunchKernelGGL((rotary_and_cache_kernel<E, CT, false, false>), grid, block, 0, s, kp);
+  }
+  return hipGetLastError();
+}
+
+}  // namespace rope_cache
 }  // namespace dk
 
-extern "C" int dk_rotary_embedding(const dk_rotary_params* a, int dtype, void* stream) {
-  using namespace dk;
-  clear_error();
-  if (a == nullptr) return fail("rotary_embedding: params must not be NULL");
-  if (dtype != DK_FLOAT16 && dtype != DK_BFLOAT16)
-    return fail("rotary_embedding: expected float16 or bfloat16, got dtype code %d", dtype);
+namespace dk {
+namespace {
+
+// Argument checks and kernel parameters of rotary_embedding; returns a
+// dk error code (0: launchable, with *empty set when there is nothing to do).
+int rotary_params(const char* op, const dk_rotary_params* a, int dtype, rope::KParams& kp, bool& neox, bool& vec,
+                  bool& empty) {
+  empty = false;
+  if (a == nullptr) return fail("%s: params must not be NULL", op);
+  if (dtype != DK_FLOAT16 && dtype != DK_BFLOAT16) return fail("%s: expected float16 or bfloat16, got dtype code %d", op, dtype);
   if (a->cache_dtype != dtype && a->cache_dtype != DK_FLOAT32)
-    return fail("rotary_embedding: cos_sin_cache must be float32 or the query dtype");
-  if (a->num_tokens < 0 || a->num_q_heads < 0 || a->num_kv_heads < 0)
-    return fail("rotary_embedding: sizes must be non-negative");
-  if (a->num_tokens == 0) return hipSuccess;
+    return fail("%s: cos_sin_cache must be float32 or the query dtype", op);
+  if (a->num_tokens < 0 || a->num_q_heads < 0 || a->num_kv_heads < 0) return fail("%s: sizes must be non-negative", op);
+  if (a->num_tokens == 0) {
+    empty = true;
+    return 0;
+  }
   if (a->rot_dim <= 0 || a->rot_dim % 2 != 0 || a->rot_dim > a->head_size)
-    return fail("rotary_embedding: rot_dim must be even and at most head_size");
+    return fail("%s: rot_dim must be even and at most head_size", op);
   if (a->positions == nullptr || a->query == nullptr || a->cos_sin_cache == nullptr)
-    return fail("rotary_embedding: positions, query and cos_sin_cache must not be NULL");
-  if (a->num_tokens > 0x7fffffff / 2) return fail("rotary_embedding: too many tokens");
-  rope::KParams kp{};
+    return fail("%s: positions, query and cos_sin_cache must not be NULL", op);
+  if (a->num_tokens > 0x7fffffff / 2) return fail("%s: too many tokens", op);
+  kp = rope::KParams{};
   kp.positions = a->positions;
   kp.q = static_cast<uint16_t*>(a->query);
   kp.k = static_cast<uint16_t*>(a->key);
@@ -212,40 +359,33 @@ extern "C" int dk_rotary_embedding(const dk_rotary_params* a, int dtype, void* s
   kp.hkv = a->key != nullptr ? a->num_kv_heads : 0;
   kp.rot_dim = a->rot_dim;
   kp.max_position = a->max_position;
-  const bool neox = a->is_neox != 0;
+  neox = a->is_neox != 0;
   // Vector path: 4 pairs per step, every row start aligned to the vector.
   const int half = a->rot_dim / 2;
   const int vbytes = neox ? 8 : 16;
   const int velems = vbytes / 2;
-  bool vec = half % 4 == 0 && aligned_to(a->query, vbytes) && a->q_stride_token % velems == 0 &&
-             a->q_stride_head % velems == 0 && (!neox || half % velems == 0);
+  vec = half % 4 == 0 && aligned_to(a->query, vbytes) && a->q_stride_token % velems == 0 &&
+        a->q_stride_head % velems == 0 && (!neox || half % velems == 0);
   if (kp.hkv > 0)
     vec = vec && aligned_to(a->key, vbytes) && a->k_stride_token % velems == 0 && a->k_stride_head % velems == 0;
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  hipError_t e;
-  if (a->cache_dtype == DK_FLOAT32) {
-    e = dtype == DK_BFLOAT16 ? rope::launch_rotary<Bf16, float>(kp, neox, vec, s)
-                             : rope::launch_rotary<F16, float>(kp, neox, vec, s);
-  } else {
-    e = dtype == DK_BFLOAT16 ? rope::launch_rotary<Bf16, uint16_t>(kp, neox, vec, s)
-                             : rope::launch_rotary<F16, uint16_t>(kp, neox, vec, s);
-  }
-  return static_cast<int>(e);
+  return 0;
 }
 
-extern "C" int dk_reshape_and_cache(const dk_cache_write_params* a, int dtype, void* stream) {
-  using namespace dk;
-  clear_error();
-  if (a == nullptr) return fail("reshape_and_cache: params must not be NULL");
-  if (dtype != DK_FLOAT16 && dtype != DK_BFLOAT16)
-    return fail("reshape_and_cache: expected float16 or bfloat16, got dtype code %d", dtype);
+// Argument checks and kernel parameters of reshape_and_cache (as above).
+int cache_params(const char* op, const dk_cache_write_params* a, int dtype, cache::KParams& kp, bool& vec, bool& empty) {
+  empty = false;
+  if (a == nullptr) return fail("%s: params must not be NULL", op);
+  if (dtype != DK_FLOAT16 && dtype != DK_BFLOAT16) return fail("%s: expected float16 or bfloat16, got dtype code %d", op, dtype);
   if (a->num_tokens < 0 || a->num_kv_heads <= 0 || a->head_size <= 0 || a->block_size <= 0 || a->num_blocks < 0)
-    return fail("reshape_and_cache: sizes must be positive");
-  if (a->num_tokens == 0) return hipSuccess;
+    return fail("%s: sizes must be positive", op);
+  if (a->num_tokens == 0) {
+    empty = true;
+    return 0;
+  }
   if (a->key == nullptr || a->value == nullptr || a->key_cache == nullptr || a->value_cache == nullptr ||
       a->slot_mapping == nullptr)
-    return fail("reshape_and_cache: pointers must not be NULL");
-  cache::KParams kp{};
+    return fail("%s: pointers must not be NULL", op);
+  kp = cache::KParams{};
   kp.key = static_cast<const uint16_t*>(a->key);
   kp.value = static_cast<const uint16_t*>(a->value);
   kp.kc = static_cast<uint16_t*>(a->key_cache);
@@ -266,15 +406,77 @@ extern "C" int dk_reshape_and_cache(const dk_cache_write_params* a, int dtype, v
   kp.d = a->head_size;
   kp.block_size = a->block_size;
   kp.num_blocks = a->num_blocks;
-  const bool vec = a->head_size % 8 == 0 && aligned_to(a->key, 16) && aligned_to(a->value, 16) &&
-                   aligned_to(a->key_cache, 16) && aligned_to(a->value_cache, 16) &&
-                   a->k_stride_token % 8 == 0 && a->k_stride_head % 8 == 0 && a->v_stride_token % 8 == 0 &&
-                   a->v_stride_head % 8 == 0 && a->kc_stride_block % 8 == 0 && a->kc_stride_token % 8 == 0 &&
-                   a->kc_stride_head % 8 == 0 && a->vc_stride_block % 8 == 0 && a->vc_stride_token % 8 == 0 &&
-                   a->vc_stride_head % 8 == 0;
+  vec = a->head_size % 8 == 0 && aligned_to(a->key, 16) && aligned_to(a->value, 16) && aligned_to(a->key_cache, 16) &&
+        aligned_to(a->value_cache, 16) && a->k_stride_token % 8 == 0 && a->k_stride_head % 8 == 0 &&
+        a->v_stride_token % 8 == 0 && a->v_stride_head % 8 == 0 && a->kc_stride_block % 8 == 0 &&
+        a->kc_stride_token % 8 == 0 && a->kc_stride_head % 8 == 0 && a->vc_stride_block % 8 == 0 &&
+        a->vc_stride_token % 8 == 0 && a->vc_stride_head % 8 == 0;
+  return 0;
+}
+
+}  // namespace
+}  // namespace dk
+
+extern "C" int dk_rotary_embedding(const dk_rotary_params* a, int dtype, void* stream) {
+  using namespace dk;
+  clear_error();
+  rope::KParams kp;
+  bool neox = false, vec = false, empty = false;
+  if (const int rc = rotary_params("rotary_embedding", a, dtype, kp, neox, vec, empty)) return rc;
+  if (empty) return hipSuccess;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  hipError_t e;
+  if (a->cache_dtype == DK_FLOAT32) {
+    e = dtype == DK_BFLOAT16 ? rope::launch_rotary<Bf16, float>(kp, neox, vec, s)
+                             : rope::launch_rotary<F16, float>(kp, neox, vec, s);
+  } else {
+    e = dtype == DK_BFLOAT16 ? rope::launch_rotary<Bf16, uint16_t>(kp, neox, vec, s)
+                             : rope::launch_rotary<F16, uint16_t>(kp, neox, vec, s);
+  }
+  return static_cast<int>(e);
+}
+
+extern "C" int dk_reshape_and_cache(const dk_cache_write_params* a, int dtype, void* stream) {
+  using namespace dk;
+  clear_error();
+  cache::KParams kp;
+  bool vec = false, empty = false;
+  if (const int rc = cache_params("reshape_and_cache", a, dtype, kp, vec, empty)) return rc;
+  if (empty) return hipSuccess;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const dim3 grid(a->num_tokens), block(cache::kThreads);
   if (vec) hipLaunchKernelGGL((cache::reshape_and_cache_kernel<8>), grid, block, 0, s, kp);
   else hipLaunchKernelGGL((cache::reshape_and_cache_kernel<1>), grid, block, 0, s, kp);
   return static_cast<int>(hipGetLastError());
+}
+
+extern "C" int dk_rotary_embedding_and_cache(const dk_rotary_params* r, const dk_cache_write_params* c, int dtype,
+                                             void* stream) {
+  using namespace dk;
+  clear_error();
+  const char* op = "rotary_embedding_and_cache";
+  rope_cache::KParams kp;
+  bool neox = false, rvec = false, cvec = false, rempty = false, cempty = false;
+  if (const int rc = rotary_params(op, r, dtype, kp.r, neox, rvec, rempty)) return rc;
+  if (const int rc = cache_params(op, c, dtype, kp.c, cvec, cempty)) return rc;
+  if (r->num_tokens != c->num_tokens) return fail("%s: the rotary and cache token counts differ", op);
+  if (rempty) return hipSuccess;
+  if (r->key == nullptr || r->key != c->key || r->k_stride_token != c->k_stride_token ||
+      r->k_stride_head != c->k_stride_head)
+    return fail("%s: the rotated key and the cached key must be the same tensor", op);
+  if (r->num_kv_heads != c->num_kv_heads || r->head_size != c->head_size)
+    return fail("%s: the rotary and cache head counts / sizes differ", op);
+  // The 16-byte copy path also needs rot_dim on a 16-byte boundary (the k
+  // columns past it are copied in 8-element chunks).
+  const bool vec = rvec && cvec && r->rot_dim % 8 == 0;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  hipError_t e;
+  if (r->cache_dtype == DK_FLOAT32) {
+    e = dtype == DK_BFLOAT16 ? rope_cache::launch<Bf16, float>(kp, neox, vec, s)
+                             : rope_cache::launch<F16, float>(kp, neox, vec, s);
+  } else {
+    e = dtype == DK_BFLOAT16 ? rope_cache::launch<Bf16, uint16_t>(kp, neox, vec, s)
+                             : rope_cache::launch<F16, uint16_t>(kp, neox, vec, s);
+  }
+  return static_cast<int>(e);
 }

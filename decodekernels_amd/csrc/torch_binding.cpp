@@ -323,8 +323,11 @@ int64_t heads_of(const at::Tensor& t, int64_t head_size) { return t.dim() == 2 ?
 
 }  // namespace
 
-void rotary_embedding(const at::Tensor& positions, at::Tensor& query, const std::optional<at::Tensor>& key,
-                      int64_t head_size, const at::Tensor& cos_sin_cache, bool is_neox) {
+namespace {
+
+// Checked dk_rotary_params of a rotary_embedding call (and its dtype code).
+dk_rotary_params rotary_params(const at::Tensor& positions, at::Tensor& query, const std::optional<at::Tensor>& key,
+                               int64_t head_size, const at::Tensor& cos_sin_cache, bool is_neox, int& dt) {
   TORCH_CHECK(query.is_cuda(), "rotary_embedding: query must be on CUDA");
   TORCH_CHECK(positions.scalar_type() == at::ScalarType::Long && positions.is_contiguous(),
               "rotary_embedding: positions must be contiguous int64");
@@ -335,7 +338,7 @@ void rotary_embedding(const at::Tensor& positions, at::Tensor& query, const std:
               "rotary_embedding: cos_sin_cache must be [max_position, rot_dim] with contiguous rows");
   TORCH_CHECK(cos_sin_cache.device() == query.device() && positions.device() == query.device(),
               "rotary_embedding: tensors must be on the same device");
-  const int dt = dtype_code(query.scalar_type(), "rotary_embedding");
+  dt = dtype_code(query.scalar_type(), "rotary_embedding");
   int cache_dt;
   if (cos_sin_cache.scalar_type() == at::ScalarType::Float) {
     cache_dt = DK_FLOAT32;
@@ -364,12 +367,12 @@ void rotary_embedding(const at::Tensor& positions, at::Tensor& query, const std:
   p.max_position = static_cast<int32_t>(cos_sin_cache.size(0));
   p.is_neox = is_neox ? 1 : 0;
   p.cache_dtype = cache_dt;
-  const DeviceGuard guard(query.device());
-  check_status(dk_rotary_embedding(&p, dt, stream_of(query)), "rotary_embedding");
+  return p;
 }
 
-void reshape_and_cache(const at::Tensor& key, const at::Tensor& value, at::Tensor& key_cache, at::Tensor& value_cache,
-                       const at::Tensor& slot_mapping) {
+// Checked dk_cache_write_params of a reshape_and_cache call (and its dtype code).
+dk_cache_write_params cache_params(const at::Tensor& key, const at::Tensor& value, at::Tensor& key_cache,
+                                   at::Tensor& value_cache, const at::Tensor& slot_mapping, int& dt) {
   TORCH_CHECK(key.is_cuda(), "reshape_and_cache: key must be on CUDA");
   check_same(key, value, "key/value");
   check_same(key, key_cache, "key/key_cache");
@@ -405,9 +408,39 @@ void reshape_and_cache(const at::Tensor& key, const at::Tensor& value, at::Tenso
   p.head_size = static_cast<int32_t>(D);
   p.block_size = static_cast<int32_t>(key_cache.size(1));
   p.num_blocks = static_cast<int32_t>(key_cache.size(0));
-  const int dt = dtype_code(key.scalar_type(), "reshape_and_cache");
+  dt = dtype_code(key.scalar_type(), "reshape_and_cache");
+  return p;
+}
+
+}  // namespace
+
+void rotary_embedding(const at::Tensor& positions, at::Tensor& query, const std::optional<at::Tensor>& key,
+                      int64_t head_size, const at::Tensor& cos_sin_cache, bool is_neox) {
+  int dt = 0;
+  const dk_rotary_params p = rotary_params(positions, query, key, head_size, cos_sin_cache, is_neox, dt);
+  const DeviceGuard guard(query.device());
+  check_status(dk_rotary_embedding(&p, dt, stream_of(query)), "rotary_embedding");
+}
+
+void reshape_and_cache(const at::Tensor& key, const at::Tensor& value, at::Tensor& key_cache, at::Tensor& value_cache,
+                       const at::Tensor& slot_mapping) {
+  int dt = 0;
+  const dk_cache_write_params p = cache_params(key, value, key_cache, value_cache, slot_mapping, dt);
   const DeviceGuard guard(key.device());
   check_status(dk_reshape_and_cache(&p, dt, stream_of(key)), "reshape_and_cache");
+}
+
+// rotary_embedding then reshape_and_cache of the rotated key, in one launch.
+void rotary_embedding_and_cache(const at::Tensor& positions, at::Tensor& query, at::Tensor& key,
+                                const at::Tensor& value, int64_t head_size, const at::Tensor& cos_sin_cache,
+                                bool is_neox, at::Tensor& key_cache, at::Tensor& value_cache,
+                                const at::Tensor& slot_mapping) {
+  int dt = 0, dt2 = 0;
+  const dk_rotary_params r = rotary_params(positions, query, key, head_size, cos_sin_cache, is_neox, dt);
+  const dk_cache_write_params c = cache_params(key, value, key_cache, value_cache, slot_mapping, dt2);
+  TORCH_CHECK(key_cache.size(3) == head_size, "rotary_embedding_and_cache: cache head_size must equal head_size");
+  const DeviceGuard guard(query.device());
+  check_status(dk_rotary_embedding_and_cache(&r, &c, dt, stream_of(query)), "rotary_embedding_and_cache");
 }
 
 // ---------------------------------------------------------------------------
@@ -429,6 +462,9 @@ TORCH_LIBRARY(decode_kernels, m) {
       "rotary_embedding(Tensor positions, Tensor! query, Tensor!? key, int head_size, Tensor cos_sin_cache, "
       "bool is_neox) -> ()");
   m.def("reshape_and_cache(Tensor key, Tensor value, Tensor! key_cache, Tensor! value_cache, Tensor slot_mapping) -> ()");
+  m.def(
+      "rotary_embedding_and_cache(Tensor positions, Tensor! query, Tensor! key, Tensor value, int head_size, "
+      "Tensor cos_sin_cache, bool is_neox, Tensor! key_cache, Tensor! value_cache, Tensor slot_mapping) -> ()");
 }
 
 TORCH_LIBRARY_IMPL(decode_kernels, CUDA, m) {
@@ -440,6 +476,7 @@ TORCH_LIBRARY_IMPL(decode_kernels, CUDA, m) {
   m.impl("silu_and_mul", &silu_and_mul);
   m.impl("rotary_embedding", &rotary_embedding);
   m.impl("reshape_and_cache", &reshape_and_cache);
+  m.impl("rotary_embedding_and_cache", &rotary_embedding_and_cache);
 }
 
 // Python module entry point: an empty module; importing it loads this

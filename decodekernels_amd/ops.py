@@ -92,6 +92,12 @@ if _AVAILABLE:
         def _(key, value, key_cache, value_cache, slot_mapping):
             return None
 
+    if _has_op("rotary_embedding_and_cache"):
+
+        @torch.library.register_fake("decode_kernels::rotary_embedding_and_cache")
+        def _(positions, query, key, value, head_size, cos_sin_cache, is_neox, key_cache, value_cache, slot_mapping):
+            return None
+
 
 # ---------------------------------------------------------------------------
 # Paged attention
@@ -246,3 +252,26 @@ def reshape_and_cache(
     paged_attention_decode reads (NHD, HND or vLLM's interleaved buffer)."""
     _require()
     torch.ops.decode_kernels.reshape_and_cache(key, value, key_cache, value_cache, slot_mapping)
+
+
+def rotary_embedding_and_cache(
+    positions: torch.Tensor,
+    query: torch.Tensor,
+    key: torch.Tensor,
+    value: torch.Tensor,
+    head_size: int,
+    cos_sin_cache: torch.Tensor,
+    is_neox: bool,
+    key_cache: torch.Tensor,
+    value_cache: torch.Tensor,
+    slot_mapping: torch.Tensor,
+):
+    """``rotary_embedding`` then ``reshape_and_cache`` of the rotated key, in one
+    launch: query and key rotated in place, the rotated key and ``value``
+    written to the cache slots. Same results as the two calls in sequence.
+    Returns (query, key)."""
+    _require()
+    torch.ops.decode_kernels.rotary_embedding_and_cache(
+        positions, query, key, value, int(head_size), cos_sin_cache, bool(is_neox), key_cache, value_cache, slot_mapping
+    )
+    return query, key

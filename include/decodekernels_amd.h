@@ -180,6 +180,19 @@ typedef struct dk_cache_write_params {
 
 int dk_reshape_and_cache(const dk_cache_write_params* p, int dtype, void* stream);
 
+/*
+ * dk_rotary_embedding followed by dk_reshape_and_cache in one launch: q and
+ * k rotated in place as by dk_rotary_embedding(r), then the rotated k and v
+ * written to the cache as by dk_reshape_and_cache(c). Results are identical
+ * to the two calls in sequence (a position outside the table caches the
+ * unrotated k; a skipped slot still rotates). r->key must be c->key with the
+ * same strides, and the token, KV-head and head-size counts must agree.
+ * No counterpart in DecodeKernels or as one op in vLLM: it saves a launch
+ * per decoder layer for engines that run both steps back to back.
+ */
+int dk_rotary_embedding_and_cache(const dk_rotary_params* r, const dk_cache_write_params* c, int dtype,
+                                  void* stream);
+
 /* Description of the last argument error raised on this thread ("" if none).
  * The reference reports these through TORCH_CHECK messages (csrc/ops.cu). */
 const char* dk_last_error(void);

@@ -24,6 +24,7 @@ def test_library_exports_every_declared_symbol():
         "dk_silu_and_mul",
         "dk_rotary_embedding",
         "dk_reshape_and_cache",
+        "dk_rotary_embedding_and_cache",
         "dk_last_error",
         "dk_error_string",
         "dk_version",
@@ -203,6 +204,35 @@ def test_capi_cache_write_validation(field, value, dtype, message):
     assert message in capi.last_error()
 
 
+def _fused_pair(num_tokens=2):
+    r = _rotary_params(num_tokens=num_tokens)
+    c = capi.CacheWriteParams()
+    c.key, c.value, c.key_cache, c.value_cache, c.slot_mapping = r.key, 0x20000, 0x30000, 0x40000, 0x50000
+    c.k_stride_token, c.k_stride_head = r.k_stride_token, r.k_stride_head
+    c.num_tokens, c.num_kv_heads, c.head_size, c.block_size, c.num_blocks = num_tokens, r.num_kv_heads, r.head_size, 16, 4
+    return r, c
+
+
+def test_capi_fused_rotary_and_cache_validation():
+    L = capi.lib()
+    r, c = _fused_pair(num_tokens=0)
+    assert L.dk_rotary_embedding_and_cache(ctypes.byref(r), ctypes.byref(c), capi.DK_BFLOAT16, None) == 0
+    for mutate, message in (
+        (lambda r, c: setattr(c, "num_tokens", 3), "token counts"),
+        (lambda r, c: setattr(c, "key", 0x60000), "same tensor"),
+        (lambda r, c: setattr(c, "k_stride_token", r.k_stride_token + 8), "same tensor"),
+        (lambda r, c: setattr(c, "num_kv_heads", r.num_kv_heads + 1), "head counts"),
+        (lambda r, c: setattr(r, "rot_dim", 3), "rot_dim"),
+        (lambda r, c: setattr(c, "block_size", 0), "positive"),
+    ):
+        r, c = _fused_pair()
+        mutate(r, c)
+        rc = L.dk_rotary_embedding_and_cache(ctypes.byref(r), ctypes.byref(c), capi.DK_BFLOAT16, None)
+        assert rc == capi.HIP_ERROR_INVALID_VALUE, message
+        assert message in capi.last_error()
+    assert L.dk_rotary_embedding_and_cache(None, None, capi.DK_FLOAT16, None) == capi.HIP_ERROR_INVALID_VALUE
+
+
 def test_capi_fill_helpers_read_tensor_layouts():
     pos = torch.arange(5)
     q = torch.zeros(5, 3 * 64, dtype=torch.bfloat16)
@@ -255,6 +285,9 @@ def test_ops_are_registered_with_reference_schemas():
         "Tensor cos_sin_cache, bool is_neox) -> ()",
         "reshape_and_cache": "reshape_and_cache(Tensor key, Tensor value, Tensor(a0!) key_cache, "
         "Tensor(a1!) value_cache, Tensor slot_mapping) -> ()",
+        "rotary_embedding_and_cache": "rotary_embedding_and_cache(Tensor positions, Tensor(a0!) query, "
+        "Tensor(a1!) key, Tensor value, int head_size, Tensor cos_sin_cache, bool is_neox, Tensor(a2!) key_cache, "
+        "Tensor(a3!) value_cache, Tensor slot_mapping) -> ()",
     }
     for name, schema in schemas.items():
         got = str(getattr(torch.ops.decode_kernels, name).default._schema).replace("decode_kernels::", "")
@@ -287,6 +320,9 @@ def test_wrappers_fail_loudly_without_extension(monkeypatch):
         lambda: ops.rotary_embedding(torch.zeros(2, dtype=torch.long), torch.zeros(2, 8), None, 8, torch.zeros(4, 8)),
         lambda: ops.reshape_and_cache(torch.zeros(2, 1, 8), torch.zeros(2, 1, 8), torch.zeros(1, 4, 1, 8),
                                       torch.zeros(1, 4, 1, 8), torch.zeros(2, dtype=torch.long)),
+        lambda: ops.rotary_embedding_and_cache(torch.zeros(2, dtype=torch.long), torch.zeros(2, 8), torch.zeros(2, 8),
+                                               torch.zeros(2, 8), 8, torch.zeros(4, 8), True, torch.zeros(1, 4, 1, 8),
+                                               torch.zeros(1, 4, 1, 8), torch.zeros(2, dtype=torch.long)),
     ):
         with pytest.raises(RuntimeError, match="not built"):
             call()

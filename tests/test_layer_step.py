@@ -11,7 +11,8 @@ Each stage is checked against the oracle applied to the previous stage's
 actual output (the bar of each op's own parity test), then the whole step is
 captured in a HIP graph and every replay -- with the sequence lengths,
 positions and slots rewritten on the device between replays -- must match an
-eager run bit for bit.
+eager run bit for bit. Each test also runs with rotary_embedding_and_cache in
+place of the two ops, which must give the same bits.
 """
 
 import pytest
@@ -37,7 +38,8 @@ EPS = 1e-5
 
 
 class Layer:
-    def __init__(self, seq_lens, dtype, seed=0):
+    def __init__(self, seq_lens, dtype, seed=0, fused_rope_cache=False):
+        self.fused_rope_cache = fused_rope_cache
         g = torch.Generator(device="cuda").manual_seed(seed)
         kw = dict(device="cuda", dtype=dtype)
         self.dtype = dtype
@@ -89,11 +91,18 @@ class Layer:
         ops.gemm_tn(self.qkv, self.x, self.w_qkv, None)
         if keep:
             self.saved["qkv"] = self.qkv.clone()
-        ops.rotary_embedding(self.positions, self.qkv[:, : HQ * D], self.k_new, D, self.rope, True)
-        if keep:
-            self.saved["k_cache"] = self.kv.k_cache.clone()
-            self.saved["v_cache"] = self.kv.v_cache.clone()
-        ops.reshape_and_cache(self.k_new, self.v_new, self.kv.k_cache, self.kv.v_cache, self.slots)
+        if self.fused_rope_cache:
+            if keep:
+                self.saved["k_cache"] = self.kv.k_cache.clone()
+                self.saved["v_cache"] = self.kv.v_cache.clone()
+            ops.rotary_embedding_and_cache(self.positions, self.qkv[:, : HQ * D], self.k_new, self.v_new, D,
+                                           self.rope, True, self.kv.k_cache, self.kv.v_cache, self.slots)
+        else:
+            ops.rotary_embedding(self.positions, self.qkv[:, : HQ * D], self.k_new, D, self.rope, True)
+            if keep:
+                self.saved["k_cache"] = self.kv.k_cache.clone()
+                self.saved["v_cache"] = self.kv.v_cache.clone()
+            ops.reshape_and_cache(self.k_new, self.v_new, self.kv.k_cache, self.kv.v_cache, self.slots)
         dk.paged_attention_decode(self.q, self.kv.k_cache, self.kv.v_cache, self.kv.block_tables, self.kv.seq_lens,
                                   max_seq_len=self.max_len, out=self.attn, workspace=self.ws)
         ops.gemm_tn(self.o, self.attn.view(self.n, HIDDEN), self.w_o, None)
@@ -114,8 +123,9 @@ SEQ_LENS = [0, 1, 600, 1500, 33, 2049, 512, 513]
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
-def test_layer_step_stages_match_oracle(dtype):
-    L = Layer(SEQ_LENS, dtype)
+@pytest.mark.parametrize("fused", [False, True])
+def test_layer_step_stages_match_oracle(dtype, fused):
+    L = Layer(SEQ_LENS, dtype, fused_rope_cache=fused)
     L.step(keep=True)
     torch.cuda.synchronize()
     x1, r1 = L.saved["norm1"]
@@ -145,9 +155,10 @@ def test_layer_step_stages_match_oracle(dtype):
     assert_max_abs(L.down, gemm_f32(L.act, L.w_down), dtype, "down gemm")
 
 
-def test_layer_step_graph_replays_match_eager():
+@pytest.mark.parametrize("fused", [False, True])
+def test_layer_step_graph_replays_match_eager(fused):
     dtype = torch.bfloat16
-    L = Layer(SEQ_LENS, dtype, seed=3)
+    L = Layer(SEQ_LENS, dtype, seed=3, fused_rope_cache=fused)
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(side):
@@ -168,3 +179,16 @@ def test_layer_step_graph_replays_match_eager():
         names = ("qkv", "k_cache", "v_cache", "attn", "o", "resid", "gate_up", "act", "down")
         for name, a, b in zip(names, got, want):
             assert torch.equal(a, b), f"replay {i}: {name} differs from the eager step"
+
+
+def test_layer_step_fused_rope_cache_equals_two_ops():
+    """The step with rotary_embedding_and_cache gives the same bits as with
+    rotary_embedding + reshape_and_cache."""
+    a = Layer(SEQ_LENS, torch.bfloat16, seed=5)
+    b = Layer(SEQ_LENS, torch.bfloat16, seed=5, fused_rope_cache=True)
+    a.step()
+    b.step()
+    torch.cuda.synchronize()
+    names = ("qkv", "k_cache", "v_cache", "attn", "o", "resid", "gate_up", "act", "down")
+    for name, x, y in zip(names, a.outputs(), b.outputs()):
+        assert torch.equal(x, y), f"{name} differs between the fused and the two-op step"

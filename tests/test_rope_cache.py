@@ -9,7 +9,8 @@ bit-exact. Cases: NeoX and GPT-J pairing, partial rot_dim, float32 and
 model-dtype tables, flat / 3-D / strided q and k (the vector and the scalar
 paths), key None, the three cache layouts paged attention reads, padding and
 out-of-range slots, and a decode step that appends a token through
-reshape_and_cache and attends over it.
+reshape_and_cache and attends over it. rotary_embedding_and_cache (both steps
+in one launch) must equal the two ops in sequence bit for bit, and the oracle.
 """
 
 import ctypes
@@ -253,3 +254,91 @@ def test_decode_step_appends_and_attends(dtype, layout):
     assert_ulp(k, want_k, 0, "rotary_embedding(key)")
     ref = attention_f32(q3, kv.k_cache, kv.v_cache, kv.block_tables, new_lens)
     assert_max_abs(out, ref, dtype, "paged_attention_decode after the cache write")
+
+
+# ---------------------------------------------------------------------------
+# rotary_embedding_and_cache: both steps in one launch, bit-identical to the
+# two ops in sequence and to the oracle
+# ---------------------------------------------------------------------------
+def _fused_inputs(dtype, is_neox, head_size, rot_dim, layout, seed, t=61, hq=8, hkv=2, bs=16, misalign=False):
+    kv = make_paged_kv([700, 300], hkv, head_size, bs, dtype, "cuda", layout=layout, seed=seed)
+    g = torch.Generator(device="cuda").manual_seed(seed + 1)
+    width = (hq + 2 * hkv) * head_size
+    buf = torch.randn(t, width + 1, generator=g, device="cuda", dtype=dtype)
+    qkv = buf[:, 1:] if misalign else buf[:, :width]  # misaligned rows take the scalar path
+    q, k = qkv[:, : hq * head_size], qkv[:, hq * head_size : (hq + hkv) * head_size]
+    v = qkv[:, (hq + hkv) * head_size :]
+    table_dtype = torch.float32 if is_neox else dtype
+    cache = rope_cos_sin_cache(4096, rot_dim).to(table_dtype).cuda()
+    pos = _positions(t, 4096, seed + 2)
+    slots = _slots(kv.k_cache.shape[0], bs, t, seed + 3)
+    return kv, buf, q, k, v, cache, pos, slots
+
+
+def _run_fused_and_pair(kv, buf, q, k, v, cache, pos, slots, head_size, is_neox):
+    """(fused results, two-op results): q, k, k_cache, v_cache of each."""
+    kc2, vc2 = kv.k_cache.clone(), kv.v_cache.clone()
+    buf2 = buf.clone()
+    off = q.data_ptr() - buf.data_ptr()
+    el = buf.element_size()
+    q2 = buf2.view(-1)[off // el :].as_strided(q.shape, q.stride())
+    k2 = buf2.view(-1)[(k.data_ptr() - buf.data_ptr()) // el :].as_strided(k.shape, k.stride())
+    v2 = buf2.view(-1)[(v.data_ptr() - buf.data_ptr()) // el :].as_strided(v.shape, v.stride())
+    dk.rotary_embedding(pos, q2, k2, head_size, cache, is_neox)
+    dk.reshape_and_cache(k2, v2, kc2, vc2, slots)
+    dk.rotary_embedding_and_cache(pos, q, k, v, head_size, cache, is_neox, kv.k_cache, kv.v_cache, slots)
+    torch.cuda.synchronize()
+    return (q, k, kv.k_cache, kv.v_cache), (q2, k2, kc2, vc2)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("is_neox", [True, False])
+@pytest.mark.parametrize("head_size,rot_dim", [(128, 128), (128, 64), (64, 64), (256, 256)])
+@pytest.mark.parametrize("layout", ["nhd", "hnd", "vllm"])
+def test_fused_rope_and_cache_equals_the_two_ops(dtype, is_neox, head_size, rot_dim, layout):
+    seed = head_size + rot_dim + 3 * is_neox
+    kv, buf, q, k, v, cache, pos, slots = _fused_inputs(dtype, is_neox, head_size, rot_dim, layout, seed)
+    kc0, vc0 = kv.k_cache.cpu(), kv.v_cache.cpu()
+    q0, k0, v0 = q.cpu(), k.cpu(), v.cpu()
+    fused, pair = _run_fused_and_pair(kv, buf, q, k, v, cache, pos, slots, head_size, is_neox)
+    for name, a, b in zip(("query", "key", "key_cache", "value_cache"), fused, pair):
+        assert torch.equal(a, b), f"fused {name} differs from rotary_embedding + reshape_and_cache"
+    want_q, want_k = rotary_embedding_reference(pos.cpu(), q0, k0, head_size, cache.cpu(), is_neox)
+    want_kc, want_vc = reshape_and_cache_reference(want_k.reshape(k0.shape[0], -1, head_size), v0, kc0, vc0,
+                                                   slots.cpu())
+    assert_ulp(q, want_q, 0, "fused rotary(query)")
+    assert_ulp(k, want_k, 0, "fused rotary(key)")
+    assert torch.equal(kv.k_cache.cpu(), want_kc) and torch.equal(kv.v_cache.cpu(), want_vc)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("is_neox", [True, False])
+@pytest.mark.parametrize("case", ["misaligned_rows", "rot_dim_36"])
+def test_fused_rope_and_cache_scalar_path(dtype, is_neox, case):
+    rot = 36 if case == "rot_dim_36" else 64  # rot_dim % 8 != 0 keeps the copies element-wise
+    kv, buf, q, k, v, cache, pos, slots = _fused_inputs(dtype, is_neox, 64, rot, "vllm", seed=40 + rot,
+                                                        misalign=case == "misaligned_rows")
+    fused, pair = _run_fused_and_pair(kv, buf, q, k, v, cache, pos, slots, 64, is_neox)
+    for name, a, b in zip(("query", "key", "key_cache", "value_cache"), fused, pair):
+        assert torch.equal(a, b), f"fused {name} differs ({case})"
+
+
+def test_fused_rope_and_cache_capi_and_errors():
+    dtype = torch.bfloat16
+    kv, buf, q, k, v, cache, pos, slots = _fused_inputs(dtype, True, 128, 128, "vllm", seed=50)
+    kv2 = make_paged_kv([700, 300], 2, 128, 16, dtype, "cuda", layout="vllm", seed=50)
+    buf2 = buf.clone()
+    q2, k2, v2 = buf2[:, : 8 * 128], buf2[:, 8 * 128 : 10 * 128], buf2[:, 10 * 128 : 12 * 128]
+    r = capi.rotary_params(pos, q2, k2, 128, cache, True)
+    c = capi.cache_write_params(k2, v2, kv2.k_cache, kv2.v_cache, slots)
+    rc = capi.lib().dk_rotary_embedding_and_cache(ctypes.byref(r), ctypes.byref(c), capi.dtype_code(dtype), _stream())
+    assert rc == 0, capi.last_error()
+    dk.rotary_embedding_and_cache(pos, q, k, v, 128, cache, True, kv.k_cache, kv.v_cache, slots)
+    torch.cuda.synchronize()
+    assert torch.equal(buf, buf2) and torch.equal(kv.k_cache, kv2.k_cache) and torch.equal(kv.v_cache, kv2.v_cache)
+    with pytest.raises(RuntimeError, match="one key / value row"):
+        dk.rotary_embedding_and_cache(pos, q, k, v, 128, cache, True, kv.k_cache, kv.v_cache, slots[:5])
+    with pytest.raises(RuntimeError, match="heads must match the cache"):
+        small = make_paged_kv([100], 2, 64, 16, dtype, "cuda", seed=51)
+        dk.rotary_embedding_and_cache(pos, q, k, v, 128, cache, True, small.k_cache, small.v_cache, slots)
+    dk.rotary_embedding_and_cache(pos[:0], q[:0], k[:0], v[:0], 128, cache, True, kv.k_cache, kv.v_cache, slots[:0])
