@@ -371,13 +371,29 @@ def test_gemm(dtype, M, N, K, with_bias):
 @pytest.mark.parametrize("M", [1, 8, 32, 64, 4096])
 @pytest.mark.parametrize("N", [6144, 4096, 28672])
 def test_gemm_decode_layer_shapes(M, N):
-    """The bf16 decode-layer projections (K=4096, A and B ~ N(0, 0.02))."""
-    if M == 4096 and N == 28672:
-        pytest.skip("covered by the benchmark; the CPU oracle takes too long here")
+    """The bf16 decode-layer projections (K=4096, A and B ~ N(0, 0.02)); the
+    largest against a GPU fp32 GEMM, the rest against the CPU oracle."""
     g = torch.Generator(device="cuda").manual_seed(M + N)
     a = torch.randn(M, 4096, generator=g, device="cuda", dtype=torch.bfloat16) * 0.02
     b = torch.randn(N, 4096, generator=g, device="cuda", dtype=torch.bfloat16) * 0.02
-    assert_max_abs(dk.gemm(a, b), gemm_f32(a, b), torch.bfloat16, f"gemm {M}x{N}")
+    ref = _gemm_f32_gpu(a, b) if M * N >= 4096 * 28672 else gemm_f32(a, b)
+    assert_max_abs(dk.gemm(a, b), ref, torch.bfloat16, f"gemm {M}x{N}")
+
+
+def _gemm_f32_gpu(a, b):
+    """Plain torch fp32 GEMM on the GPU (a 2-D mm of contiguous fp32 operands),
+    for shapes where the CPU oracle would take minutes."""
+    return torch.mm(a.float(), b.float().t().contiguous())
+
+
+@pytest.mark.parametrize("M", [1, 64, 4096])
+def test_gemm_down_projection_k14336(M):
+    """The decode layer's down projection (N = 4096, K = 14336), bf16."""
+    g = torch.Generator(device="cuda").manual_seed(M + 14336)
+    a = torch.randn(M, 14336, generator=g, device="cuda", dtype=torch.bfloat16) * 0.02
+    b = torch.randn(4096, 14336, generator=g, device="cuda", dtype=torch.bfloat16) * 0.02
+    ref = _gemm_f32_gpu(a, b) if M == 4096 else gemm_f32(a, b)
+    assert_max_abs(dk.gemm(a, b), ref, torch.bfloat16, f"gemm down {M}x4096x14336")
 
 
 # Every (row tiles, waves along N) pair the skinny launch policy picks, with
