@@ -150,6 +150,10 @@ _SIGNATURES = {
         ctypes.c_int,
         [ctypes.POINTER(CacheWriteParams), ctypes.c_int, ctypes.c_void_p],
     ),
+    "dk_reshape_and_cache_fp8": (
+        ctypes.c_int,
+        [ctypes.POINTER(CacheWriteParams), ctypes.c_int, ctypes.c_float, ctypes.c_float, ctypes.c_void_p],
+    ),
     "dk_rotary_embedding_and_cache": (
         ctypes.c_int,
         [ctypes.POINTER(RotaryParams), ctypes.POINTER(CacheWriteParams), ctypes.c_int, ctypes.c_void_p],

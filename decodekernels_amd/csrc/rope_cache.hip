@@ -18,6 +18,8 @@
 // token, 16-byte (or 8-byte) vectors where the layout allows, a scalar path
 // otherwise. Positions outside the table and slots outside the cache are
 // skipped rather than read or written out of bounds.
+#include <cmath>
+
 #include "../../include/decodekernels_amd.h"
 #include "dk_device.h"
 #include "dk_host.h"
@@ -174,6 +176,54 @@ __global__ __launch_bounds__(kThreads) void reshape_and_cache_kernel(const KPara
       *reinterpret_cast<u32x4*>(dst) = *reinterpret_cast<const u32x4*>(src);
     } else {
       *dst = *src;
+    }
+  }
+}
+
+// Into an fp8 (e4m3fn) cache, as vLLM's reshape_and_cache_flash does for an
+// "fp8" cache: x / scale in fp32, saturated to the largest finite value
+// (+-448; NaN stays NaN), rounded to nearest even by v_cvt_pk_fp8_f32, which
+// gives torch's float -> float8_e4m3fn cast on every input (checked on the
+// device over all values, midpoints and their neighbours). The caches hold
+// one byte per element; strides are in elements.
+__device__ __forceinline__ float sat_e4m3(float y) { return y != y ? y : fminf(fmaxf(y, -448.0f), 448.0f); }
+
+template <typename E, int VEC>
+__global__ __launch_bounds__(kThreads) void reshape_and_cache_fp8_kernel(const KParams p, float k_scale, float v_scale) {
+  const int t = blockIdx.x;
+  const int64_t slot = p.slots[t];
+  if (slot < 0) return;
+  const int64_t blk = slot / p.block_size;
+  const int64_t off = slot - blk * p.block_size;
+  if (blk >= p.num_blocks) return;
+  uint8_t* kc = reinterpret_cast<uint8_t*>(p.kc);
+  uint8_t* vc = reinterpret_cast<uint8_t*>(p.vc);
+  const int per_head = p.d / VEC;
+  const int n = p.hkv * per_head;
+  for (int c = threadIdx.x; c < 2 * n; c += kThreads) {
+    const bool is_v = c >= n;
+    const int cc = is_v ? c - n : c;
+    const int h = cc / per_head;
+    const int d0 = (cc - h * per_head) * VEC;
+    const uint16_t* src = is_v ? p.value + t * p.v_st + h * p.v_sh + d0 : p.key + t * p.k_st + h * p.k_sh + d0;
+    uint8_t* dst = is_v ? vc + blk * p.vc_sb + off * p.vc_st + h * p.vc_sh + d0
+                        : kc + blk * p.kc_sb + off * p.kc_st + h * p.kc_sh + d0;
+    const float scale = is_v ? v_scale : k_scale;
+    if constexpr (VEC == 8) {
+      const u32x4 x = *reinterpret_cast<const u32x4*>(src);
+      u32x2 o;
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        int w = __builtin_amdgcn_cvt_pk_fp8_f32(sat_e4m3(E::lo(x[2 * j]) / scale), sat_e4m3(E::hi(x[2 * j]) / scale), 0,
+                                                false);
+        w = __builtin_amdgcn_cvt_pk_fp8_f32(sat_e4m3(E::lo(x[2 * j + 1]) / scale),
+                                            sat_e4m3(E::hi(x[2 * j + 1]) / scale), w, true);
+        o[j] = static_cast<uint32_t>(w);
+      }
+      *reinterpret_cast<u32x2*>(dst) = o;
+    } else {
+      const int w = __builtin_amdgcn_cvt_pk_fp8_f32(sat_e4m3(E::to_float(*src) / scale), 0.0f, 0, false);
+      *dst = static_cast<uint8_t>(w & 0xff);
     }
   }
 }
@@ -447,6 +497,35 @@ extern "C" int dk_reshape_and_cache(const dk_cache_write_params* a, int dtype, v
   const dim3 grid(a->num_tokens), block(cache::kThreads);
   if (vec) hipLaunchKernelGGL((cache::reshape_and_cache_kernel<8>), grid, block, 0, s, kp);
   else hipLaunchKernelGGL((cache::reshape_and_cache_kernel<1>), grid, block, 0, s, kp);
+  return static_cast<int>(hipGetLastError());
+}
+
+extern "C" int dk_reshape_and_cache_fp8(const dk_cache_write_params* a, int dtype, float k_scale, float v_scale,
+                                        void* stream) {
+  using namespace dk;
+  clear_error();
+  const char* op = "reshape_and_cache_fp8";
+  cache::KParams kp;
+  bool vec16 = false, empty = false;
+  if (const int rc = cache_params(op, a, dtype, kp, vec16, empty)) return rc;
+  if (!(k_scale > 0.0f && v_scale > 0.0f && k_scale < INFINITY && v_scale < INFINITY))
+    return fail("%s: k_scale and v_scale must be positive and finite", op);
+  if (empty) return hipSuccess;
+  // 8 elements per step: 16-byte reads of key / value, 8-byte writes to the fp8 caches.
+  const bool vec = a->head_size % 8 == 0 && aligned_to(a->key, 16) && aligned_to(a->value, 16) &&
+                   aligned_to(a->key_cache, 8) && aligned_to(a->value_cache, 8) && a->k_stride_token % 8 == 0 &&
+                   a->k_stride_head % 8 == 0 && a->v_stride_token % 8 == 0 && a->v_stride_head % 8 == 0 &&
+                   a->kc_stride_block % 8 == 0 && a->kc_stride_token % 8 == 0 && a->kc_stride_head % 8 == 0 &&
+                   a->vc_stride_block % 8 == 0 && a->vc_stride_token % 8 == 0 && a->vc_stride_head % 8 == 0;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const dim3 grid(a->num_tokens), block(cache::kThreads);
+  if (dtype == DK_BFLOAT16) {
+    if (vec) hipLaunchKernelGGL((cache::reshape_and_cache_fp8_kernel<Bf16, 8>), grid, block, 0, s, kp, k_scale, v_scale);
+    else hipLaunchKernelGGL((cache::reshape_and_cache_fp8_kernel<Bf16, 1>), grid, block, 0, s, kp, k_scale, v_scale);
+  } else {
+    if (vec) hipLaunchKernelGGL((cache::reshape_and_cache_fp8_kernel<F16, 8>), grid, block, 0, s, kp, k_scale, v_scale);
+    else hipLaunchKernelGGL((cache::reshape_and_cache_fp8_kernel<F16, 1>), grid, block, 0, s, kp, k_scale, v_scale);
+  }
   return static_cast<int>(hipGetLastError());
 }
 

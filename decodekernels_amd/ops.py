@@ -92,6 +92,12 @@ if _AVAILABLE:
         def _(key, value, key_cache, value_cache, slot_mapping):
             return None
 
+    if _has_op("reshape_and_cache_fp8"):
+
+        @torch.library.register_fake("decode_kernels::reshape_and_cache_fp8")
+        def _(key, value, key_cache, value_cache, slot_mapping, k_scale, v_scale):
+            return None
+
     if _has_op("rotary_embedding_and_cache"):
 
         @torch.library.register_fake("decode_kernels::rotary_embedding_and_cache")
@@ -245,12 +251,26 @@ def reshape_and_cache(
     key_cache: torch.Tensor,
     value_cache: torch.Tensor,
     slot_mapping: torch.Tensor,
+    k_scale: float = 1.0,
+    v_scale: float = 1.0,
 ) -> None:
     """Writes key[t] / value[t] ([tokens, kv_heads, head_size]) into cache slot
     ``slot_mapping[t]`` (int64; negative = skip) of the
     [num_blocks, block_size, kv_heads, head_size] cache views -- the same views
-    paged_attention_decode reads (NHD, HND or vLLM's interleaved buffer)."""
+    paged_attention_decode reads (NHD, HND or vLLM's interleaved buffer).
+
+    Into ``torch.float8_e4m3fn`` caches the rows are quantized as vLLM's fp8
+    cache write does: x / scale in fp32, saturated to +-448, rounded to
+    nearest even (``reshape_and_cache_fp8``); paged_attention_decode then
+    reads the cache with the same k_scale / v_scale."""
     _require()
+    if key_cache.dtype == torch.float8_e4m3fn:
+        torch.ops.decode_kernels.reshape_and_cache_fp8(
+            key, value, key_cache, value_cache, slot_mapping, float(k_scale), float(v_scale)
+        )
+        return
+    if k_scale != 1.0 or v_scale != 1.0:
+        raise ValueError("k_scale / v_scale apply to an fp8 (float8_e4m3fn) KV cache only")
     torch.ops.decode_kernels.reshape_and_cache(key, value, key_cache, value_cache, slot_mapping)
 
 

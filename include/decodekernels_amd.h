@@ -181,6 +181,18 @@ typedef struct dk_cache_write_params {
 int dk_reshape_and_cache(const dk_cache_write_params* p, int dtype, void* stream);
 
 /*
+ * dk_reshape_and_cache into an fp8 (e4m3fn) cache: key / value (dtype
+ * DK_FLOAT16 or DK_BFLOAT16) are quantized as x / scale in fp32, saturated to
+ * +-448 (NaN stays NaN) and rounded to nearest even, then written to the
+ * one-byte-per-element caches (strides in elements, as for the 16-bit caches).
+ * k_scale / v_scale must be positive and finite: the per-tensor scales that
+ * dk_paged_attention_decode_fp8 then applies when it reads the cache.
+ * No counterpart in DecodeKernels: vLLM's reshape_and_cache_flash with
+ * kv_cache_dtype "fp8".
+ */
+int dk_reshape_and_cache_fp8(const dk_cache_write_params* p, int dtype, float k_scale, float v_scale, void* stream);
+
+/*
  * dk_rotary_embedding followed by dk_reshape_and_cache in one launch: q and
  * k rotated in place as by dk_rotary_embedding(r), then the rotated k and v
  * written to the cache as by dk_reshape_and_cache(c). Results are identical

@@ -14,7 +14,10 @@ decodekernels_amd kernels implement, as the expected results:
   table leave the token unchanged.
 * cache write: key_cache[slot // block_size, slot % block_size] = key[t]
   (same for value), slot = slot_mapping[t], negative or out-of-range slots
-  skipped.
+  skipped. Into an fp8 (e4m3fn) cache the rows are quantized as vLLM's
+  ``reshape_and_cache_flash`` does for ``kv_cache_dtype`` "fp8": x / scale in
+  fp32, saturated to the largest finite value (+-448, NaN stays NaN), rounded
+  to nearest even.
 
 Pinned in ``tests/test_oracle_rope_cache.py`` by an independent complex-number
 route, rotation invariants in float64 and an ``index_put_`` scatter.
@@ -60,8 +63,20 @@ def rotary_embedding_reference(positions, query, key, head_size, cos_sin_cache, 
     return apply(query), apply(key)
 
 
-def reshape_and_cache_reference(key, value, key_cache, value_cache, slot_mapping):
-    """Copies of the caches with each token's key / value row written to its slot."""
+E4M3_MAX = 448.0
+
+
+def quantize_e4m3(x: torch.Tensor, scale: float) -> torch.Tensor:
+    """x / scale in fp32, saturated to +-448 (NaN kept), rounded to nearest-even e4m3fn."""
+    y = x.float() / torch.tensor(scale, dtype=torch.float32)
+    return y.clamp(-E4M3_MAX, E4M3_MAX).to(torch.float8_e4m3fn)
+
+
+def reshape_and_cache_reference(key, value, key_cache, value_cache, slot_mapping, k_scale=1.0, v_scale=1.0):
+    """Copies of the caches with each token's key / value row written to its
+    slot (quantized with k_scale / v_scale when the caches are e4m3fn)."""
+    if key_cache.dtype == torch.float8_e4m3fn:
+        key, value = quantize_e4m3(key, k_scale), quantize_e4m3(value, v_scale)
     kc, vc = key_cache.clone(), value_cache.clone()
     num_blocks, block_size = kc.shape[0], kc.shape[1]
     nkv = kc.shape[2]

@@ -25,6 +25,7 @@ def test_library_exports_every_declared_symbol():
         "dk_rotary_embedding",
         "dk_reshape_and_cache",
         "dk_rotary_embedding_and_cache",
+        "dk_reshape_and_cache_fp8",
         "dk_last_error",
         "dk_error_string",
         "dk_version",
@@ -233,6 +234,25 @@ def test_capi_fused_rotary_and_cache_validation():
     assert L.dk_rotary_embedding_and_cache(None, None, capi.DK_FLOAT16, None) == capi.HIP_ERROR_INVALID_VALUE
 
 
+@pytest.mark.parametrize("ks,vs", [(0.0, 1.0), (1.0, -2.0), (float("inf"), 1.0), (1.0, float("nan"))])
+def test_capi_fp8_cache_write_rejects_bad_scales(ks, vs):
+    c = capi.CacheWriteParams()
+    c.key = c.value = c.key_cache = c.value_cache = c.slot_mapping = 0x10000
+    c.num_tokens, c.num_kv_heads, c.head_size, c.block_size, c.num_blocks = 2, 2, 128, 16, 4
+    rc = capi.lib().dk_reshape_and_cache_fp8(ctypes.byref(c), capi.DK_BFLOAT16, ks, vs, None)
+    assert rc == capi.HIP_ERROR_INVALID_VALUE
+    assert "positive and finite" in capi.last_error()
+    c.num_tokens = 0
+    assert capi.lib().dk_reshape_and_cache_fp8(ctypes.byref(c), capi.DK_BFLOAT16, 1.0, 1.0, None) == 0
+
+
+def test_cache_write_scales_need_an_fp8_cache():
+    kc = torch.zeros(1, 4, 1, 8, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="fp8"):
+        ops.reshape_and_cache(torch.zeros(2, 1, 8, dtype=torch.bfloat16), torch.zeros(2, 1, 8, dtype=torch.bfloat16), kc,
+                              kc.clone(), torch.zeros(2, dtype=torch.long), k_scale=0.5)
+
+
 def test_capi_fill_helpers_read_tensor_layouts():
     pos = torch.arange(5)
     q = torch.zeros(5, 3 * 64, dtype=torch.bfloat16)
@@ -285,6 +305,8 @@ def test_ops_are_registered_with_reference_schemas():
         "Tensor cos_sin_cache, bool is_neox) -> ()",
         "reshape_and_cache": "reshape_and_cache(Tensor key, Tensor value, Tensor(a0!) key_cache, "
         "Tensor(a1!) value_cache, Tensor slot_mapping) -> ()",
+        "reshape_and_cache_fp8": "reshape_and_cache_fp8(Tensor key, Tensor value, Tensor(a0!) key_cache, "
+        "Tensor(a1!) value_cache, Tensor slot_mapping, float k_scale, float v_scale) -> ()",
         "rotary_embedding_and_cache": "rotary_embedding_and_cache(Tensor positions, Tensor(a0!) query, "
         "Tensor(a1!) key, Tensor value, int head_size, Tensor cos_sin_cache, bool is_neox, Tensor(a2!) key_cache, "
         "Tensor(a3!) value_cache, Tensor slot_mapping) -> ()",

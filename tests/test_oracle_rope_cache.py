@@ -166,3 +166,103 @@ def test_cache_write_skips_slots_past_the_cache():
     key = torch.ones(2, 1, 8)
     nk, nv = reshape_and_cache_reference(key, key, kc, vc, torch.tensor([8, 3]))
     assert nk.sum() == 8 and nk[0, 3].sum() == 8 and nv[0, 3].sum() == 8
+
+
+# ---------------------------------------------------------------------------
+# fp8 (e4m3fn) cache write: quantize_e4m3 against a brute-force nearest search
+# ---------------------------------------------------------------------------
+def _e4m3_table():
+    """(values, codes) of every finite e4m3fn encoding, by decoding the 8 bits."""
+    codes = torch.arange(256, dtype=torch.int32)
+    vals = codes.to(torch.uint8).view(torch.float8_e4m3fn).float()
+    keep = torch.isfinite(vals)
+    return vals[keep].double(), codes[keep]
+
+
+def _brute_e4m3(x: torch.Tensor, scale: float, ties_even: bool = True) -> torch.Tensor:
+    """Nearest finite e4m3fn value to fp32(x / scale); ties go to the even
+    encoding (last mantissa bit 0) -- or away from zero with ties_even=False,
+    a planted mistake; beyond +-448 saturate; NaN stays NaN."""
+    vals, codes = _e4m3_table()
+    y = (x.float() / torch.tensor(scale, dtype=torch.float32)).double()
+    out = torch.empty_like(y)
+    for i, v in enumerate(y.tolist()):
+        if v != v:
+            out[i] = float("nan")
+            continue
+        v = max(min(v, 448.0), -448.0)
+        d = (vals - v).abs()
+        best = d.min()
+        ties = (d == best).nonzero().flatten()
+        if len(ties) == 1:
+            pick = ties[0]
+        elif ties_even:
+            pick = next(t for t in ties if int(codes[t]) % 2 == 0)
+        else:
+            pick = max(ties.tolist(), key=lambda t: abs(float(vals[t])))
+        out[i] = vals[pick]
+    return out
+
+
+def _fp8_probe_values():
+    vals, _ = _e4m3_table()
+    fin = vals.float().unique()
+    mids = (fin[1:] + fin[:-1]) / 2
+    extra = torch.tensor([449.0, 464.0, 500.0, 1e6, float("inf"), 1e-12, 2.0**-10, 3 * 2.0**-11, float("nan")])
+    up = torch.nextafter(mids, torch.full_like(mids, 1e9))
+    down = torch.nextafter(mids, torch.full_like(mids, -1e9))
+    g = torch.Generator().manual_seed(3)
+    rnd = torch.randn(400, generator=g) * 40
+    x = torch.cat([fin, mids, up, down, extra, rnd])
+    return torch.cat([x, -x])
+
+
+@pytest.mark.parametrize("scale", [1.0, 0.37, 2.5])
+def test_fp8_quantization_matches_brute_force(scale):
+    from oracle.rope_cache import quantize_e4m3
+
+    x = _fp8_probe_values() * scale  # the midpoints land back on midpoints after / scale (up to fp32 rounding)
+    got = quantize_e4m3(x, scale).double()
+    want = _brute_e4m3(x, scale)
+    same = (got == want) | (got.isnan() & want.isnan())
+    assert same.all(), [(float(x[i]), float(got[i]), float(want[i])) for i in (~same).nonzero().flatten()[:5]]
+
+
+@pytest.mark.parametrize("mistake", ["ties_away_from_zero", "multiply_by_scale", "no_saturation"])
+def test_fp8_quantization_pins_catch_planted_mistakes(mistake):
+    """Each wrong quantizer differs from the pinned oracle on the probe values."""
+    from oracle.rope_cache import quantize_e4m3
+
+    x = _fp8_probe_values()
+    if mistake == "ties_away_from_zero":
+        got = _brute_e4m3(x, 1.0, ties_even=False)
+        want = quantize_e4m3(x, 1.0).double()
+    elif mistake == "multiply_by_scale":
+        got = (x.float() * 2.5).clamp(-448, 448).to(torch.float8_e4m3fn).double()
+        want = _brute_e4m3(x, 2.5)
+    else:  # torch's cast alone turns values past the range into NaN
+        got = x.float().to(torch.float8_e4m3fn).double()
+        want = _brute_e4m3(x, 1.0)
+    same = (got == want) | (got.isnan() & want.isnan())
+    assert not same.all(), f"the brute-force pin does not catch {mistake}"
+
+
+def test_fp8_cache_write_reference_quantizes_rows():
+    from oracle.rope_cache import quantize_e4m3
+
+    nb, bs, h, d, t = 6, 16, 2, 64, 5
+    kc = torch.zeros(nb, bs, h, d, dtype=torch.float8_e4m3fn)
+    vc = torch.zeros_like(kc)
+    g = torch.Generator().manual_seed(4)
+    key = torch.randn(t, h, d, generator=g, dtype=torch.bfloat16) * 100
+    value = torch.randn(t, h * d, generator=g, dtype=torch.bfloat16)
+    slots = torch.tensor([3, -1, 40, 95, 96 * 2])
+    got_k, got_v = reshape_and_cache_reference(key, value, kc, vc, slots, k_scale=0.5, v_scale=0.01)
+    for i, s in enumerate(slots.tolist()):
+        if 0 <= s < nb * bs:
+            assert torch.equal(got_k[s // bs, s % bs].view(torch.uint8), quantize_e4m3(key[i], 0.5).view(torch.uint8))
+            assert torch.equal(got_v[s // bs, s % bs].view(torch.uint8),
+                               quantize_e4m3(value[i].view(h, d), 0.01).view(torch.uint8))
+    untouched = torch.ones(nb * bs, dtype=torch.bool)
+    untouched[[3, 40, 95]] = False
+    assert (got_k.view(nb * bs, h, d)[untouched].float() == 0).all()

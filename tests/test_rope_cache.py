@@ -342,3 +342,87 @@ def test_fused_rope_and_cache_capi_and_errors():
         small = make_paged_kv([100], 2, 64, 16, dtype, "cuda", seed=51)
         dk.rotary_embedding_and_cache(pos, q, k, v, 128, cache, True, small.k_cache, small.v_cache, slots)
     dk.rotary_embedding_and_cache(pos[:0], q[:0], k[:0], v[:0], 128, cache, True, kv.k_cache, kv.v_cache, slots[:0])
+
+
+# ---------------------------------------------------------------------------
+# Cache write into an fp8 (e4m3fn) cache: x / scale, saturated, nearest even
+# ---------------------------------------------------------------------------
+FP8 = torch.float8_e4m3fn
+
+
+def _fp8_rows(t, hkv, d, dtype, seed):
+    """Rows mixing ordinary values, exact e4m3 midpoints and values past +-448 (x scale later)."""
+    g = torch.Generator(device="cpu").manual_seed(seed)
+    x = torch.randn(t, hkv, d, generator=g) * 3
+    table = torch.arange(256, dtype=torch.int32).to(torch.uint8).view(FP8).float()
+    fin = table[torch.isfinite(table)].unique()
+    mids = (fin[1:] + fin[:-1]) / 2
+    pick = torch.randint(0, len(mids), (t, hkv, d // 4), generator=g)
+    x[..., : d // 4] = mids[pick]
+    x[:, 0, -2:] = torch.tensor([900.0, -2000.0])
+    return x.to(dtype).cuda()
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("layout", ["nhd", "hnd", "vllm"])
+@pytest.mark.parametrize("head_dim", [64, 128, 256])
+@pytest.mark.parametrize("k_scale,v_scale", [(1.0, 1.0), (0.37, 2.5)])
+def test_fp8_cache_write_matches_oracle(dtype, layout, head_dim, k_scale, v_scale):
+    hkv, t, bs = 2, 70, 16
+    kv = make_paged_kv([700, 300], hkv, head_dim, bs, FP8, "cuda", layout=layout, seed=head_dim)
+    key = _fp8_rows(t, hkv, head_dim, dtype, seed=1) * k_scale
+    value = _fp8_rows(t, hkv, head_dim, dtype, seed=2).reshape(t, hkv * head_dim) * v_scale
+    slots = _slots(kv.k_cache.shape[0], bs, t, 21)
+    want_k, want_v = reshape_and_cache_reference(key.cpu(), value.cpu(), kv.k_cache.cpu(), kv.v_cache.cpu(),
+                                                 slots.cpu(), k_scale, v_scale)
+    dk.reshape_and_cache(key, value, kv.k_cache, kv.v_cache, slots, k_scale=k_scale, v_scale=v_scale)
+    torch.cuda.synchronize()
+    assert torch.equal(kv.k_cache.cpu().view(torch.uint8), want_k.view(torch.uint8))
+    assert torch.equal(kv.v_cache.cpu().view(torch.uint8), want_v.view(torch.uint8))
+
+
+@pytest.mark.parametrize("case", ["misaligned_rows", "head_size_36"])
+def test_fp8_cache_write_scalar_path(case):
+    dtype, hkv, t, bs, nb = torch.bfloat16, 2, 40, 16, 8
+    d = 36 if case == "head_size_36" else 64
+    kc = torch.zeros(nb, bs, hkv, d, device="cuda", dtype=FP8)
+    vc = torch.zeros_like(kc)
+    buf = torch.cat([_fp8_rows(t, hkv, d, dtype, seed=3).reshape(t, -1), _fp8_rows(t, hkv, d, dtype, seed=4).reshape(t, -1),
+                     torch.zeros(t, 1, device="cuda", dtype=dtype)], dim=1)
+    off = 1 if case == "misaligned_rows" else 0
+    key = buf[:, off : off + hkv * d]
+    value = buf[:, off + hkv * d : off + 2 * hkv * d]
+    slots = _slots(nb, bs, t, 22)
+    want_k, want_v = reshape_and_cache_reference(key.cpu(), value.cpu(), kc.cpu(), vc.cpu(), slots.cpu(), 0.5, 0.75)
+    dk.reshape_and_cache(key, value, kc, vc, slots, k_scale=0.5, v_scale=0.75)
+    torch.cuda.synchronize()
+    assert torch.equal(kc.cpu().view(torch.uint8), want_k.view(torch.uint8))
+    assert torch.equal(vc.cpu().view(torch.uint8), want_v.view(torch.uint8))
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_fp8_decode_step_writes_then_attends(dtype):
+    """RoPE, the new token quantized into the fp8 cache, then fp8 attention
+    over the grown cache, against the fp32 oracle on the dequantized cache."""
+    hq, hkv, d, bs = 16, 4, 128, 16
+    lens = [5, 300, 1100, 47]
+    kv = make_paged_kv(lens, hkv, d, bs, FP8, "cuda", layout="vllm", seed=23)
+    n = len(lens)
+    qkv, q, k = _qkv(n, hq, hkv, d, dtype, seed=24)
+    v = qkv[:, (hq + hkv) * d :]
+    cache = rope_cos_sin_cache(4096, d).cuda()
+    pos = torch.tensor(lens, device="cuda")
+    dk.rotary_embedding(pos, q, k, d, cache, True)
+    bt = kv.block_tables.cpu()
+    slots = torch.tensor([int(bt[s, lens[s] // bs]) * bs + lens[s] % bs for s in range(n)], device="cuda")
+    ks, vs = 0.05, 0.02
+    want_k, want_v = reshape_and_cache_reference(k.cpu(), v.cpu(), kv.k_cache.cpu(), kv.v_cache.cpu(), slots.cpu(), ks, vs)
+    dk.reshape_and_cache(k, v, kv.k_cache, kv.v_cache, slots, k_scale=ks, v_scale=vs)
+    new_lens = (kv.seq_lens + 1).contiguous()
+    q3 = q.reshape(n, hq, d)
+    out = dk.paged_attention_decode(q3, kv.k_cache, kv.v_cache, kv.block_tables, new_lens, k_scale=ks, v_scale=vs)
+    torch.cuda.synchronize()
+    assert torch.equal(kv.k_cache.cpu().view(torch.uint8), want_k.view(torch.uint8))
+    assert torch.equal(kv.v_cache.cpu().view(torch.uint8), want_v.view(torch.uint8))
+    ref = attention_f32(q3, kv.k_cache.float() * ks, kv.v_cache.float() * vs, kv.block_tables, new_lens)
+    assert_max_abs(out, ref, dtype, "fp8 attention after the fp8 cache write")
