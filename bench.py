@@ -430,6 +430,20 @@ def pmc_workload_gemm(calls: int = 3) -> None:
     print(f"pmc gemm workload done: {calls} calls each at M=4096 N=4096 and M=256 N=6144 (K=4096)", flush=True)
 
 
+def pmc_workload_gemm_skinny(calls: int = 3) -> None:
+    """What the skinny-GEMM counter runs profile: the decode layer's down
+    projection (N=4096, K=14336) at M=1 and M=64, `calls` times each."""
+    g = torch.Generator(device="cuda").manual_seed(1)
+    w = torch.randn(4096, 14336, generator=g, device="cuda", dtype=torch.bfloat16) * 0.02
+    for m in (1, 64):
+        a = torch.randn(m, 14336, generator=g, device="cuda", dtype=torch.bfloat16) * 0.02
+        c = torch.empty(m, 4096, device="cuda", dtype=torch.bfloat16)
+        for _ in range(calls):
+            torch.ops.decode_kernels.gemm_tn(c, a, w, None)
+    torch.cuda.synchronize()
+    print(f"pmc skinny gemm workload done: {calls} calls each at M=1 and M=64 (N=4096, K=14336)", flush=True)
+
+
 def pmc_workload(calls: int = 5) -> None:
     """What the counter runs profile: the headline op `calls` times, then a
     copy of CALIBRATION_BYTES (read once, written once) to scale the counters."""
@@ -463,7 +477,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-extras", action="store_true", help="skip the secondary configs")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline (and its correctness check)")
-    ap.add_argument("--pmc-workload", nargs="?", const="attention", choices=["attention", "gemm"],
+    ap.add_argument("--pmc-workload", nargs="?", const="attention", choices=["attention", "gemm", "gemm_skinny"],
                     help="run only what the rocprofv3 --pmc passes profile (default: attention)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -472,6 +486,9 @@ def main() -> int:
         return 2
     if not dk.is_available():
         raise RuntimeError("decodekernels_amd HIP extension not available (build it with __graft_entry__.build())")
+    if args.pmc_workload == "gemm_skinny":
+        pmc_workload_gemm_skinny()
+        return 0
     if args.pmc_workload == "gemm":
         pmc_workload_gemm()
         return 0
