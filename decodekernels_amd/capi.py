@@ -158,6 +158,11 @@ _SIGNATURES = {
         ctypes.c_int,
         [ctypes.POINTER(RotaryParams), ctypes.POINTER(CacheWriteParams), ctypes.c_int, ctypes.c_void_p],
     ),
+    "dk_rotary_embedding_and_cache_fp8": (
+        ctypes.c_int,
+        [ctypes.POINTER(RotaryParams), ctypes.POINTER(CacheWriteParams), ctypes.c_int, ctypes.c_float, ctypes.c_float]
+        + [ctypes.c_void_p],
+    ),
     "dk_last_error": (ctypes.c_char_p, []),
     "dk_error_string": (ctypes.c_char_p, [ctypes.c_int]),
     "dk_version": (ctypes.c_char_p, []),

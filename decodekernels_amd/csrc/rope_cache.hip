@@ -19,6 +19,7 @@
 // otherwise. Positions outside the table and slots outside the cache are
 // skipped rather than read or written out of bounds.
 #include <cmath>
+#include <type_traits>
 
 #include "../../include/decodekernels_amd.h"
 #include "dk_device.h"
@@ -188,6 +189,17 @@ __global__ __launch_bounds__(kThreads) void reshape_and_cache_kernel(const KPara
 // one byte per element; strides are in elements.
 __device__ __forceinline__ float sat_e4m3(float y) { return y != y ? y : fminf(fmaxf(y, -448.0f), 448.0f); }
 
+// a, b, c, d quantized into the bytes of one word, a in the lowest.
+__device__ __forceinline__ uint32_t e4m3x4(float a, float b, float c, float d, float scale) {
+  int w = __builtin_amdgcn_cvt_pk_fp8_f32(sat_e4m3(a / scale), sat_e4m3(b / scale), 0, false);
+  w = __builtin_amdgcn_cvt_pk_fp8_f32(sat_e4m3(c / scale), sat_e4m3(d / scale), w, true);
+  return static_cast<uint32_t>(w);
+}
+
+__device__ __forceinline__ uint8_t e4m3(float a, float scale) {
+  return static_cast<uint8_t>(__builtin_amdgcn_cvt_pk_fp8_f32(sat_e4m3(a / scale), 0.0f, 0, false) & 0xff);
+}
+
 template <typename E, int VEC>
 __global__ __launch_bounds__(kThreads) void reshape_and_cache_fp8_kernel(const KParams p, float k_scale, float v_scale) {
   const int t = blockIdx.x;
@@ -211,19 +223,10 @@ __global__ __launch_bounds__(kThreads) void reshape_and_cache_fp8_kernel(const K
     const float scale = is_v ? v_scale : k_scale;
     if constexpr (VEC == 8) {
       const u32x4 x = *reinterpret_cast<const u32x4*>(src);
-      u32x2 o;
-#pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        int w = __builtin_amdgcn_cvt_pk_fp8_f32(sat_e4m3(E::lo(x[2 * j]) / scale), sat_e4m3(E::hi(x[2 * j]) / scale), 0,
-                                                false);
-        w = __builtin_amdgcn_cvt_pk_fp8_f32(sat_e4m3(E::lo(x[2 * j + 1]) / scale),
-                                            sat_e4m3(E::hi(x[2 * j + 1]) / scale), w, true);
-        o[j] = static_cast<uint32_t>(w);
-      }
-      *reinterpret_cast<u32x2*>(dst) = o;
+      *reinterpret_cast<u32x2*>(dst) = u32x2{e4m3x4(E::lo(x[0]), E::hi(x[0]), E::lo(x[1]), E::hi(x[1]), scale),
+                                             e4m3x4(E::lo(x[2]), E::hi(x[2]), E::lo(x[3]), E::hi(x[3]), scale)};
     } else {
-      const int w = __builtin_amdgcn_cvt_pk_fp8_f32(sat_e4m3(E::to_float(*src) / scale), 0.0f, 0, false);
-      *dst = static_cast<uint8_t>(w & 0xff);
+      *dst = e4m3(E::to_float(*src), scale);
     }
   }
 }
@@ -246,8 +249,11 @@ struct KParams {
 // sequence: same per-pair arithmetic, and a skipped position (outside the
 // table) caches the unrotated k, a skipped slot rotates without caching.
 // VEC: 4 pairs per rotation step and 16-byte copies; else one element.
-template <typename E, typename CT, bool NEOX, bool VEC>
-__global__ __launch_bounds__(kThreads) void rotary_and_cache_kernel(const KParams p) {
+// FP8: the caches hold e4m3fn bytes and every value is written as the fp8
+// cache write quantizes it, after the rounding to E that the two-op sequence
+// stores in k first.
+template <typename E, typename CT, bool NEOX, bool VEC, bool FP8>
+__global__ __launch_bounds__(kThreads) void rotary_and_cache_kernel(const KParams p, float k_scale, float v_scale) {
   constexpr int VW = VEC ? 4 : 1;
   constexpr int VC = VEC ? 8 : 1;
   const int t = blockIdx.x;
@@ -267,6 +273,10 @@ __global__ __launch_bounds__(kThreads) void rotary_and_cache_kernel(const KParam
   const int tail = (c.d - r.rot_dim) / VC;  // k copy chunks past rot_dim, per head
   const int vrow = c.d / VC;               // v copy chunks per head
   const int copy_items = put ? c.hkv * (tail + vrow) : 0;
+  // Cache rows as element pointers of the cache's own width (fp8: bytes).
+  using CE = std::conditional_t<FP8, uint8_t, uint16_t>;
+  CE* const kcb = reinterpret_cast<CE*>(c.kc) + blk * c.kc_sb + off * c.kc_st;
+  CE* const vcb = reinterpret_cast<CE*>(c.vc) + blk * c.vc_sb + off * c.vc_st;
   for (int it = threadIdx.x; it < rot_items + copy_items; it += kThreads) {
     if (it < rot_items) {
       const int h = it / steps;
@@ -276,7 +286,6 @@ __global__ __launch_bounds__(kThreads) void rotary_and_cache_kernel(const KParam
       if (is_k && !rot && !put) continue;
       const int hk = h - r.hq;
       uint16_t* v = is_k ? r.k + t * r.k_st + hk * r.k_sh : r.q + t * r.q_st + h * r.q_sh;
-      uint16_t* kc = is_k ? c.kc + blk * c.kc_sb + off * c.kc_st + hk * c.kc_sh : nullptr;
       // Element offsets of the VW x / y values: NeoX x at i0.., y at half + i0..; GPT-J interleaved at 2 i0.
       float x[VW], y[VW], ox[VW], oy[VW];
       if constexpr (NEOX) {
@@ -310,12 +319,8 @@ __global__ __launch_bounds__(kThreads) void rotary_and_cache_kernel(const KParam
 #pragma unroll
         for (int j = 0; j < VW; ++j) ox[j] = x[j], oy[j] = y[j];
       }
-      // Destinations: the row itself (rotated only) and, for k, the cache slot.
-      uint16_t* dst[2] = {rot ? v : nullptr, is_k && put ? kc : nullptr};
-#pragma unroll
-      for (int d = 0; d < 2; ++d) {
-        uint16_t* o = dst[d];
-        if (o == nullptr) continue;
+      // The rotated row itself, in E.
+      auto store16 = [&](uint16_t* o) {
         if constexpr (NEOX) {
           if constexpr (VEC) {
             *reinterpret_cast<u32x2*>(o + i0) = u32x2{pack2<E>(ox[0], ox[1]), pack2<E>(ox[2], ox[3])};
@@ -335,6 +340,33 @@ __global__ __launch_bounds__(kThreads) void rotary_and_cache_kernel(const KParam
             o[2 * i0 + 1] = E::from_float(oy[0]);
           }
         }
+      };
+      if (rot) store16(v);
+      if (!(is_k && put)) continue;
+      if constexpr (FP8) {
+        // The value k holds after the rotation (rounded to E), quantized.
+#pragma unroll
+        for (int j = 0; j < VW; ++j) ox[j] = E::to_float(E::from_float(ox[j])), oy[j] = E::to_float(E::from_float(oy[j]));
+        uint8_t* o = kcb + hk * c.kc_sh;
+        if constexpr (NEOX) {
+          if constexpr (VEC) {
+            *reinterpret_cast<uint32_t*>(o + i0) = cache::e4m3x4(ox[0], ox[1], ox[2], ox[3], k_scale);
+            *reinterpret_cast<uint32_t*>(o + half + i0) = cache::e4m3x4(oy[0], oy[1], oy[2], oy[3], k_scale);
+          } else {
+            o[i0] = cache::e4m3(ox[0], k_scale);
+            o[half + i0] = cache::e4m3(oy[0], k_scale);
+          }
+        } else {
+          if constexpr (VEC) {
+            *reinterpret_cast<u32x2*>(o + 2 * i0) = u32x2{cache::e4m3x4(ox[0], oy[0], ox[1], oy[1], k_scale),
+                                                          cache::e4m3x4(ox[2], oy[2], ox[3], oy[3], k_scale)};
+          } else {
+            o[2 * i0] = cache::e4m3(ox[0], k_scale);
+            o[2 * i0 + 1] = cache::e4m3(oy[0], k_scale);
+          }
+        }
+      } else {
+        store16(kcb + hk * c.kc_sh);
       }
     } else {
       // Copies: k columns past rot_dim, then the v row.
@@ -345,9 +377,17 @@ __global__ __launch_bounds__(kThreads) void rotary_and_cache_kernel(const KParam
       const int h = ci / per;
       const int d0 = (is_v ? 0 : r.rot_dim) + (ci - h * per) * VC;
       const uint16_t* src = is_v ? c.value + t * c.v_st + h * c.v_sh + d0 : c.key + t * c.k_st + h * c.k_sh + d0;
-      uint16_t* dst = is_v ? c.vc + blk * c.vc_sb + off * c.vc_st + h * c.vc_sh + d0
-                           : c.kc + blk * c.kc_sb + off * c.kc_st + h * c.kc_sh + d0;
-      if constexpr (VEC) {
+      CE* dst = is_v ? vcb + h * c.vc_sh + d0 : kcb + h * c.kc_sh + d0;
+      if constexpr (FP8) {
+        const float scale = is_v ? v_scale : k_scale;
+        if constexpr (VEC) {
+          const u32x4 a = *reinterpret_cast<const u32x4*>(src);
+          *reinterpret_cast<u32x2*>(dst) = u32x2{cache::e4m3x4(E::lo(a[0]), E::hi(a[0]), E::lo(a[1]), E::hi(a[1]), scale),
+                                                 cache::e4m3x4(E::lo(a[2]), E::hi(a[2]), E::lo(a[3]), E::hi(a[3]), scale)};
+        } else {
+          *dst = cache::e4m3(E::to_float(*src), scale);
+        }
+      } else if constexpr (VEC) {
         *reinterpret_cast<u32x4*>(dst) = *reinterpret_cast<const u32x4*>(src);
       } else {
         *dst = *src;
@@ -356,17 +396,27 @@ __global__ __launch_bounds__(kThreads) void rotary_and_cache_kernel(const KParam
   }
 }
 
-template <typename E, typename CT>
-hipError_t launch(const KParams& kp, bool neox, bool vec, hipStream_t s) {
+template <typename E, typename CT, bool FP8>
+hipError_t launch(const KParams& kp, bool neox, bool vec, float k_scale, float v_scale, hipStream_t s) {
   const dim3 grid(kp.r.num_tokens), block(kThreads);
   if (neox) {
-    if (vec) hipLaunchKernelGGL((rotary_and_cache_kernel<E, CT, true, true>), grid, block, 0, s, kp);
-    else hipLaunchKernelGGL((rotary_and_cache_kernel<E, CT, true, false>), grid, block, 0, s, kp);
+    if (vec) hipLaunchKernelGGL((rotary_and_cache_kernel<E, CT, true, true, FP8>), grid, block, 0, s, kp, k_scale, v_scale);
+    else hipLaunchKernelGGL((rotary_and_cache_kernel<E, CT, true, false, FP8>), grid, block, 0, s, kp, k_scale, v_scale);
   } else {
-    if (vec) hipLaunchKernelGGL((rotary_and_cache_kernel<E, CT, false, true>), grid, block, 0, s, kp);
-    else hipLaunchKernelGGL((rotary_and_cache_kernel<E, CT, false, false>), grid, block, 0, s, kp);
+    if (vec) hipLaunchKernelGGL((rotary_and_cache_kernel<E, CT, false, true, FP8>), grid, block, 0, s, kp, k_scale, v_scale);
+    else hipLaunchKernelGGL((rotary_and_cache_kernel<E, CT, false, false, FP8>), grid, block, 0, s, kp, k_scale, v_scale);
   }
   return hipGetLastError();
+}
+
+template <bool FP8>
+hipError_t launch_any(const KParams& kp, int dtype, int table_dtype, bool neox, bool vec, float k_scale, float v_scale,
+                      hipStream_t s) {
+  if (table_dtype == DK_FLOAT32)
+    return dtype == DK_BFLOAT16 ? launch<Bf16, float, FP8>(kp, neox, vec, k_scale, v_scale, s)
+                                : launch<F16, float, FP8>(kp, neox, vec, k_scale, v_scale, s);
+  return dtype == DK_BFLOAT16 ? launch<Bf16, uint16_t, FP8>(kp, neox, vec, k_scale, v_scale, s)
+                              : launch<F16, uint16_t, FP8>(kp, neox, vec, k_scale, v_scale, s);
 }
 
 }  // namespace rope_cache
@@ -464,6 +514,43 @@ int cache_params(const char* op, const dk_cache_write_params* a, int dtype, cach
   return 0;
 }
 
+// Vector path of a cache write into fp8 caches: 16-byte reads of key /
+// value, 8-byte writes of e4m3 bytes.
+bool fp8_cache_vec(const dk_cache_write_params* a) {
+  return a->head_size % 8 == 0 && aligned_to(a->key, 16) && aligned_to(a->value, 16) && aligned_to(a->key_cache, 8) &&
+         aligned_to(a->value_cache, 8) && a->k_stride_token % 8 == 0 && a->k_stride_head % 8 == 0 &&
+         a->v_stride_token % 8 == 0 && a->v_stride_head % 8 == 0 && a->kc_stride_block % 8 == 0 &&
+         a->kc_stride_token % 8 == 0 && a->kc_stride_head % 8 == 0 && a->vc_stride_block % 8 == 0 &&
+         a->vc_stride_token % 8 == 0 && a->vc_stride_head % 8 == 0;
+}
+
+int check_scales(const char* op, float k_scale, float v_scale) {
+  if (!(k_scale > 0.0f && v_scale > 0.0f && k_scale < INFINITY && v_scale < INFINITY))
+    return fail("%s: k_scale and v_scale must be positive and finite", op);
+  return 0;
+}
+
+// Argument checks of the fused rotary + cache write: both halves as above,
+// then the agreement between them. *vec: the vector path is usable (with
+// 16-bit caches, or with fp8 caches when fp8 is set).
+int fused_params(const char* op, const dk_rotary_params* r, const dk_cache_write_params* c, int dtype, bool fp8,
+                 rope_cache::KParams& kp, bool& neox, bool& vec, bool& empty) {
+  bool rvec = false, cvec = false, cempty = false;
+  if (const int rc = rotary_params(op, r, dtype, kp.r, neox, rvec, empty)) return rc;
+  if (const int rc = cache_params(op, c, dtype, kp.c, cvec, cempty)) return rc;
+  if (r->num_tokens != c->num_tokens) return fail("%s: the rotary and cache token counts differ", op);
+  if (empty) return 0;
+  if (r->key == nullptr || r->key != c->key || r->k_stride_token != c->k_stride_token ||
+      r->k_stride_head != c->k_stride_head)
+    return fail("%s: the rotated key and the cached key must be the same tensor", op);
+  if (r->num_kv_heads != c->num_kv_heads || r->head_size != c->head_size)
+    return fail("%s: the rotary and cache head counts / sizes differ", op);
+  // The vector copies also need rot_dim on an 8-element boundary (the k
+  // columns past it are copied in 8-element chunks).
+  vec = rvec && (fp8 ? fp8_cache_vec(c) : cvec) && r->rot_dim % 8 == 0;
+  return 0;
+}
+
 }  // namespace
 }  // namespace dk
 
@@ -508,15 +595,9 @@ extern "C" int dk_reshape_and_cache_fp8(const dk_cache_write_params* a, int dtyp
   cache::KParams kp;
   bool vec16 = false, empty = false;
   if (const int rc = cache_params(op, a, dtype, kp, vec16, empty)) return rc;
-  if (!(k_scale > 0.0f && v_scale > 0.0f && k_scale < INFINITY && v_scale < INFINITY))
-    return fail("%s: k_scale and v_scale must be positive and finite", op);
+  if (const int rc = check_scales(op, k_scale, v_scale)) return rc;
   if (empty) return hipSuccess;
-  // 8 elements per step: 16-byte reads of key / value, 8-byte writes to the fp8 caches.
-  const bool vec = a->head_size % 8 == 0 && aligned_to(a->key, 16) && aligned_to(a->value, 16) &&
-                   aligned_to(a->key_cache, 8) && aligned_to(a->value_cache, 8) && a->k_stride_token % 8 == 0 &&
-                   a->k_stride_head % 8 == 0 && a->v_stride_token % 8 == 0 && a->v_stride_head % 8 == 0 &&
-                   a->kc_stride_block % 8 == 0 && a->kc_stride_token % 8 == 0 && a->kc_stride_head % 8 == 0 &&
-                   a->vc_stride_block % 8 == 0 && a->vc_stride_token % 8 == 0 && a->vc_stride_head % 8 == 0;
+  const bool vec = fp8_cache_vec(a);
   hipStream_t s = static_cast<hipStream_t>(stream);
   const dim3 grid(a->num_tokens), block(cache::kThreads);
   if (dtype == DK_BFLOAT16) {
@@ -533,29 +614,24 @@ extern "C" int dk_rotary_embedding_and_cache(const dk_rotary_params* r, const dk
                                              void* stream) {
   using namespace dk;
   clear_error();
-  const char* op = "rotary_embedding_and_cache";
   rope_cache::KParams kp;
-  bool neox = false, rvec = false, cvec = false, rempty = false, cempty = false;
-  if (const int rc = rotary_params(op, r, dtype, kp.r, neox, rvec, rempty)) return rc;
-  if (const int rc = cache_params(op, c, dtype, kp.c, cvec, cempty)) return rc;
-  if (r->num_tokens != c->num_tokens) return fail("%s: the rotary and cache token counts differ", op);
-  if (rempty) return hipSuccess;
-  if (r->key == nullptr || r->key != c->key || r->k_stride_token != c->k_stride_token ||
-      r->k_stride_head != c->k_stride_head)
-    return fail("%s: the rotated key and the cached key must be the same tensor", op);
-  if (r->num_kv_heads != c->num_kv_heads || r->head_size != c->head_size)
-    return fail("%s: the rotary and cache head counts / sizes differ", op);
-  // The 16-byte copy path also needs rot_dim on a 16-byte boundary (the k
-  // columns past it are copied in 8-element chunks).
-  const bool vec = rvec && cvec && r->rot_dim % 8 == 0;
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  hipError_t e;
-  if (r->cache_dtype == DK_FLOAT32) {
-    e = dtype == DK_BFLOAT16 ? rope_cache::launch<Bf16, float>(kp, neox, vec, s)
-                             : rope_cache::launch<F16, float>(kp, neox, vec, s);
-  } else {
-    e = dtype == DK_BFLOAT16 ? rope_cache::launch<Bf16, uint16_t>(kp, neox, vec, s)
-                             : rope_cache::launch<F16, uint16_t>(kp, neox, vec, s);
-  }
-  return static_cast<int>(e);
+  bool neox = false, vec = false, empty = false;
+  if (const int rc = fused_params("rotary_embedding_and_cache", r, c, dtype, false, kp, neox, vec, empty)) return rc;
+  if (empty) return hipSuccess;
+  return static_cast<int>(rope_cache::launch_any<false>(kp, dtype, r->cache_dtype, neox, vec, 1.0f, 1.0f,
+                                                        static_cast<hipStream_t>(stream)));
+}
+
+extern "C" int dk_rotary_embedding_and_cache_fp8(const dk_rotary_params* r, const dk_cache_write_params* c, int dtype,
+                                                 float k_scale, float v_scale, void* stream) {
+  using namespace dk;
+  clear_error();
+  const char* op = "rotary_embedding_and_cache_fp8";
+  rope_cache::KParams kp;
+  bool neox = false, vec = false, empty = false;
+  if (const int rc = fused_params(op, r, c, dtype, true, kp, neox, vec, empty)) return rc;
+  if (const int rc = check_scales(op, k_scale, v_scale)) return rc;
+  if (empty) return hipSuccess;
+  return static_cast<int>(rope_cache::launch_any<true>(kp, dtype, r->cache_dtype, neox, vec, k_scale, v_scale,
+                                                       static_cast<hipStream_t>(stream)));
 }

@@ -21,6 +21,7 @@
 
 #include <algorithm>
 #include <optional>
+#include <string>
 #include <tuple>
 #include <utility>
 
@@ -370,33 +371,42 @@ dk_rotary_params rotary_params(const at::Tensor& positions, at::Tensor& query, c
   return p;
 }
 
-// Checked dk_cache_write_params of a reshape_and_cache call (and its dtype code).
+// Checked dk_cache_write_params of a reshape_and_cache call (and its dtype
+// code); fp8: the caches are float8_e4m3fn instead of the key's dtype.
 dk_cache_write_params cache_params(const at::Tensor& key, const at::Tensor& value, at::Tensor& key_cache,
-                                   at::Tensor& value_cache, const at::Tensor& slot_mapping, int& dt) {
-  TORCH_CHECK(key.is_cuda(), "reshape_and_cache: key must be on CUDA");
+                                   at::Tensor& value_cache, const at::Tensor& slot_mapping, int& dt, bool fp8 = false) {
+  const std::string op = fp8 ? "reshape_and_cache_fp8" : "reshape_and_cache";
+  TORCH_CHECK(key.is_cuda(), op, ": key must be on CUDA");
   check_same(key, value, "key/value");
-  check_same(key, key_cache, "key/key_cache");
-  check_same(key, value_cache, "key/value_cache");
+  if (fp8) {
+    TORCH_CHECK(key_cache.scalar_type() == at::ScalarType::Float8_e4m3fn &&
+                    value_cache.scalar_type() == at::ScalarType::Float8_e4m3fn,
+                op, ": caches must be float8_e4m3fn");
+    TORCH_CHECK(key_cache.device() == key.device() && value_cache.device() == key.device(), op,
+                ": tensors must be on the same device");
+  } else {
+    check_same(key, key_cache, "key/key_cache");
+    check_same(key, value_cache, "key/value_cache");
+  }
   TORCH_CHECK(slot_mapping.scalar_type() == at::ScalarType::Long && slot_mapping.is_contiguous() &&
                   slot_mapping.device() == key.device(),
-              "reshape_and_cache: slot_mapping must be contiguous int64 on the key's device");
+              op, ": slot_mapping must be contiguous int64 on the key's device");
   TORCH_CHECK(key_cache.dim() == 4 && value_cache.dim() == 4 && key_cache.sizes() == value_cache.sizes() &&
                   key_cache.stride(3) == 1 && value_cache.stride(3) == 1,
-              "reshape_and_cache: caches must be [num_blocks, block_size, num_kv_heads, head_size] views with "
-              "contiguous head_size");
+              op, ": caches must be [num_blocks, block_size, num_kv_heads, head_size] views with contiguous head_size");
   const int64_t D = key_cache.size(3);
   const int64_t T = slot_mapping.numel();
-  TORCH_CHECK(key.size(0) == T && value.size(0) == T, "reshape_and_cache: one key / value row per slot");
+  TORCH_CHECK(key.size(0) == T && value.size(0) == T, op, ": one key / value row per slot");
   TORCH_CHECK(heads_of(key, D) == key_cache.size(2) && heads_of(value, D) == key_cache.size(2),
-              "reshape_and_cache: key / value heads must match the cache");
+              op, ": key / value heads must match the cache");
   dk_cache_write_params p{};
   p.key = key.data_ptr();
   p.value = value.data_ptr();
   p.key_cache = key_cache.data_ptr();
   p.value_cache = value_cache.data_ptr();
   p.slot_mapping = slot_mapping.data_ptr<int64_t>();
-  std::tie(p.k_stride_token, p.k_stride_head) = token_head_strides(key, D, "reshape_and_cache(key)");
-  std::tie(p.v_stride_token, p.v_stride_head) = token_head_strides(value, D, "reshape_and_cache(value)");
+  std::tie(p.k_stride_token, p.k_stride_head) = token_head_strides(key, D, (op + "(key)").c_str());
+  std::tie(p.v_stride_token, p.v_stride_head) = token_head_strides(value, D, (op + "(value)").c_str());
   p.kc_stride_block = key_cache.stride(0);
   p.kc_stride_token = key_cache.stride(1);
   p.kc_stride_head = key_cache.stride(2);
@@ -408,7 +418,7 @@ dk_cache_write_params cache_params(const at::Tensor& key, const at::Tensor& valu
   p.head_size = static_cast<int32_t>(D);
   p.block_size = static_cast<int32_t>(key_cache.size(1));
   p.num_blocks = static_cast<int32_t>(key_cache.size(0));
-  dt = dtype_code(key.scalar_type(), "reshape_and_cache");
+  dt = dtype_code(key.scalar_type(), op.c_str());
   return p;
 }
 
@@ -433,45 +443,8 @@ void reshape_and_cache(const at::Tensor& key, const at::Tensor& value, at::Tenso
 // reshape_and_cache into fp8 (e4m3fn) caches with per-tensor scales.
 void reshape_and_cache_fp8(const at::Tensor& key, const at::Tensor& value, at::Tensor& key_cache,
                            at::Tensor& value_cache, const at::Tensor& slot_mapping, double k_scale, double v_scale) {
-  TORCH_CHECK(key.is_cuda(), "reshape_and_cache_fp8: key must be on CUDA");
-  check_same(key, value, "key/value");
-  TORCH_CHECK(key_cache.scalar_type() == at::ScalarType::Float8_e4m3fn &&
-                  value_cache.scalar_type() == at::ScalarType::Float8_e4m3fn,
-              "reshape_and_cache_fp8: caches must be float8_e4m3fn");
-  TORCH_CHECK(key_cache.device() == key.device() && value_cache.device() == key.device(),
-              "reshape_and_cache_fp8: tensors must be on the same device");
-  TORCH_CHECK(slot_mapping.scalar_type() == at::ScalarType::Long && slot_mapping.is_contiguous() &&
-                  slot_mapping.device() == key.device(),
-              "reshape_and_cache_fp8: slot_mapping must be contiguous int64 on the key's device");
-  TORCH_CHECK(key_cache.dim() == 4 && value_cache.dim() == 4 && key_cache.sizes() == value_cache.sizes() &&
-                  key_cache.stride(3) == 1 && value_cache.stride(3) == 1,
-              "reshape_and_cache_fp8: caches must be [num_blocks, block_size, num_kv_heads, head_size] views with "
-              "contiguous head_size");
-  const int64_t D = key_cache.size(3);
-  const int64_t T = slot_mapping.numel();
-  TORCH_CHECK(key.size(0) == T && value.size(0) == T, "reshape_and_cache_fp8: one key / value row per slot");
-  TORCH_CHECK(heads_of(key, D) == key_cache.size(2) && heads_of(value, D) == key_cache.size(2),
-              "reshape_and_cache_fp8: key / value heads must match the cache");
-  dk_cache_write_params p{};
-  p.key = key.data_ptr();
-  p.value = value.data_ptr();
-  p.key_cache = key_cache.data_ptr();
-  p.value_cache = value_cache.data_ptr();
-  p.slot_mapping = slot_mapping.data_ptr<int64_t>();
-  std::tie(p.k_stride_token, p.k_stride_head) = token_head_strides(key, D, "reshape_and_cache_fp8(key)");
-  std::tie(p.v_stride_token, p.v_stride_head) = token_head_strides(value, D, "reshape_and_cache_fp8(value)");
-  p.kc_stride_block = key_cache.stride(0);
-  p.kc_stride_token = key_cache.stride(1);
-  p.kc_stride_head = key_cache.stride(2);
-  p.vc_stride_block = value_cache.stride(0);
-  p.vc_stride_token = value_cache.stride(1);
-  p.vc_stride_head = value_cache.stride(2);
-  p.num_tokens = static_cast<int32_t>(T);
-  p.num_kv_heads = static_cast<int32_t>(key_cache.size(2));
-  p.head_size = static_cast<int32_t>(D);
-  p.block_size = static_cast<int32_t>(key_cache.size(1));
-  p.num_blocks = static_cast<int32_t>(key_cache.size(0));
-  const int dt = dtype_code(key.scalar_type(), "reshape_and_cache_fp8");
+  int dt = 0;
+  const dk_cache_write_params p = cache_params(key, value, key_cache, value_cache, slot_mapping, dt, true);
   const DeviceGuard guard(key.device());
   check_status(dk_reshape_and_cache_fp8(&p, dt, static_cast<float>(k_scale), static_cast<float>(v_scale), stream_of(key)),
                "reshape_and_cache_fp8");
@@ -488,6 +461,21 @@ void rotary_embedding_and_cache(const at::Tensor& positions, at::Tensor& query, 
   TORCH_CHECK(key_cache.size(3) == head_size, "rotary_embedding_and_cache: cache head_size must equal head_size");
   const DeviceGuard guard(query.device());
   check_status(dk_rotary_embedding_and_cache(&r, &c, dt, stream_of(query)), "rotary_embedding_and_cache");
+}
+
+// The same into fp8 (e4m3fn) caches with per-tensor scales.
+void rotary_embedding_and_cache_fp8(const at::Tensor& positions, at::Tensor& query, at::Tensor& key,
+                                    const at::Tensor& value, int64_t head_size, const at::Tensor& cos_sin_cache,
+                                    bool is_neox, at::Tensor& key_cache, at::Tensor& value_cache,
+                                    const at::Tensor& slot_mapping, double k_scale, double v_scale) {
+  int dt = 0, dt2 = 0;
+  const dk_rotary_params r = rotary_params(positions, query, key, head_size, cos_sin_cache, is_neox, dt);
+  const dk_cache_write_params c = cache_params(key, value, key_cache, value_cache, slot_mapping, dt2, true);
+  TORCH_CHECK(key_cache.size(3) == head_size, "rotary_embedding_and_cache_fp8: cache head_size must equal head_size");
+  const DeviceGuard guard(query.device());
+  check_status(dk_rotary_embedding_and_cache_fp8(&r, &c, dt, static_cast<float>(k_scale), static_cast<float>(v_scale),
+                                                 stream_of(query)),
+               "rotary_embedding_and_cache_fp8");
 }
 
 // ---------------------------------------------------------------------------
@@ -515,6 +503,10 @@ TORCH_LIBRARY(decode_kernels, m) {
   m.def(
       "rotary_embedding_and_cache(Tensor positions, Tensor! query, Tensor! key, Tensor value, int head_size, "
       "Tensor cos_sin_cache, bool is_neox, Tensor! key_cache, Tensor! value_cache, Tensor slot_mapping) -> ()");
+  m.def(
+      "rotary_embedding_and_cache_fp8(Tensor positions, Tensor! query, Tensor! key, Tensor value, int head_size, "
+      "Tensor cos_sin_cache, bool is_neox, Tensor! key_cache, Tensor! value_cache, Tensor slot_mapping, "
+      "float k_scale, float v_scale) -> ()");
 }
 
 TORCH_LIBRARY_IMPL(decode_kernels, CUDA, m) {
@@ -528,6 +520,7 @@ TORCH_LIBRARY_IMPL(decode_kernels, CUDA, m) {
   m.impl("reshape_and_cache", &reshape_and_cache);
   m.impl("rotary_embedding_and_cache", &rotary_embedding_and_cache);
   m.impl("reshape_and_cache_fp8", &reshape_and_cache_fp8);
+  m.impl("rotary_embedding_and_cache_fp8", &rotary_embedding_and_cache_fp8);
 }
 
 // Python module entry point: an empty module; importing it loads this

@@ -104,6 +104,13 @@ if _AVAILABLE:
         def _(positions, query, key, value, head_size, cos_sin_cache, is_neox, key_cache, value_cache, slot_mapping):
             return None
 
+    if _has_op("rotary_embedding_and_cache_fp8"):
+
+        @torch.library.register_fake("decode_kernels::rotary_embedding_and_cache_fp8")
+        def _(positions, query, key, value, head_size, cos_sin_cache, is_neox, key_cache, value_cache, slot_mapping,
+              k_scale, v_scale):
+            return None
+
 
 # ---------------------------------------------------------------------------
 # Paged attention
@@ -285,12 +292,23 @@ def rotary_embedding_and_cache(
     key_cache: torch.Tensor,
     value_cache: torch.Tensor,
     slot_mapping: torch.Tensor,
+    k_scale: float = 1.0,
+    v_scale: float = 1.0,
 ):
     """``rotary_embedding`` then ``reshape_and_cache`` of the rotated key, in one
     launch: query and key rotated in place, the rotated key and ``value``
-    written to the cache slots. Same results as the two calls in sequence.
+    written to the cache slots. Same results as the two calls in sequence,
+    also into ``torch.float8_e4m3fn`` caches with k_scale / v_scale.
     Returns (query, key)."""
     _require()
+    if key_cache.dtype == torch.float8_e4m3fn:
+        torch.ops.decode_kernels.rotary_embedding_and_cache_fp8(
+            positions, query, key, value, int(head_size), cos_sin_cache, bool(is_neox), key_cache, value_cache,
+            slot_mapping, float(k_scale), float(v_scale)
+        )
+        return query, key
+    if k_scale != 1.0 or v_scale != 1.0:
+        raise ValueError("k_scale / v_scale apply to an fp8 (float8_e4m3fn) KV cache only")
     torch.ops.decode_kernels.rotary_embedding_and_cache(
         positions, query, key, value, int(head_size), cos_sin_cache, bool(is_neox), key_cache, value_cache, slot_mapping
     )

@@ -205,6 +205,16 @@ int dk_reshape_and_cache_fp8(const dk_cache_write_params* p, int dtype, float k_
 int dk_rotary_embedding_and_cache(const dk_rotary_params* r, const dk_cache_write_params* c, int dtype,
                                   void* stream);
 
+/*
+ * dk_rotary_embedding_and_cache into fp8 (e4m3fn) caches: q and k rotated in
+ * place as above, the rotated k (after its rounding to dtype) and v quantized
+ * into the caches as by dk_reshape_and_cache_fp8(c, dtype, k_scale, v_scale).
+ * Results are identical to dk_rotary_embedding then dk_reshape_and_cache_fp8.
+ * No counterpart in DecodeKernels (see dk_reshape_and_cache_fp8).
+ */
+int dk_rotary_embedding_and_cache_fp8(const dk_rotary_params* r, const dk_cache_write_params* c, int dtype,
+                                      float k_scale, float v_scale, void* stream);
+
 /* Description of the last argument error raised on this thread ("" if none).
  * The reference reports these through TORCH_CHECK messages (csrc/ops.cu). */
 const char* dk_last_error(void);

@@ -26,6 +26,7 @@ def test_library_exports_every_declared_symbol():
         "dk_reshape_and_cache",
         "dk_rotary_embedding_and_cache",
         "dk_reshape_and_cache_fp8",
+        "dk_rotary_embedding_and_cache_fp8",
         "dk_last_error",
         "dk_error_string",
         "dk_version",
@@ -234,6 +235,20 @@ def test_capi_fused_rotary_and_cache_validation():
     assert L.dk_rotary_embedding_and_cache(None, None, capi.DK_FLOAT16, None) == capi.HIP_ERROR_INVALID_VALUE
 
 
+def test_capi_fused_rotary_and_cache_fp8_validation():
+    L = capi.lib()
+    r, c = _fused_pair(num_tokens=0)
+    assert L.dk_rotary_embedding_and_cache_fp8(ctypes.byref(r), ctypes.byref(c), capi.DK_BFLOAT16, 0.5, 2.0, None) == 0
+    for ks, vs, message in ((0.0, 1.0, "positive and finite"), (1.0, float("inf"), "positive and finite")):
+        rc = L.dk_rotary_embedding_and_cache_fp8(ctypes.byref(r), ctypes.byref(c), capi.DK_BFLOAT16, ks, vs, None)
+        assert rc == capi.HIP_ERROR_INVALID_VALUE and message in capi.last_error()
+    r, c = _fused_pair()
+    c.key = 0x60000
+    rc = L.dk_rotary_embedding_and_cache_fp8(ctypes.byref(r), ctypes.byref(c), capi.DK_BFLOAT16, 1.0, 1.0, None)
+    assert rc == capi.HIP_ERROR_INVALID_VALUE and "same tensor" in capi.last_error()
+    assert "rotary_embedding_and_cache_fp8" in capi.last_error()
+
+
 @pytest.mark.parametrize("ks,vs", [(0.0, 1.0), (1.0, -2.0), (float("inf"), 1.0), (1.0, float("nan"))])
 def test_capi_fp8_cache_write_rejects_bad_scales(ks, vs):
     c = capi.CacheWriteParams()
@@ -251,6 +266,11 @@ def test_cache_write_scales_need_an_fp8_cache():
     with pytest.raises(ValueError, match="fp8"):
         ops.reshape_and_cache(torch.zeros(2, 1, 8, dtype=torch.bfloat16), torch.zeros(2, 1, 8, dtype=torch.bfloat16), kc,
                               kc.clone(), torch.zeros(2, dtype=torch.long), k_scale=0.5)
+    with pytest.raises(ValueError, match="fp8"):
+        ops.rotary_embedding_and_cache(torch.zeros(2, dtype=torch.long), torch.zeros(2, 8, dtype=torch.bfloat16),
+                                       torch.zeros(2, 8, dtype=torch.bfloat16), torch.zeros(2, 8, dtype=torch.bfloat16),
+                                       8, torch.zeros(4, 8), True, kc, kc.clone(), torch.zeros(2, dtype=torch.long),
+                                       v_scale=2.0)
 
 
 def test_capi_fill_helpers_read_tensor_layouts():
@@ -310,6 +330,9 @@ def test_ops_are_registered_with_reference_schemas():
         "rotary_embedding_and_cache": "rotary_embedding_and_cache(Tensor positions, Tensor(a0!) query, "
         "Tensor(a1!) key, Tensor value, int head_size, Tensor cos_sin_cache, bool is_neox, Tensor(a2!) key_cache, "
         "Tensor(a3!) value_cache, Tensor slot_mapping) -> ()",
+        "rotary_embedding_and_cache_fp8": "rotary_embedding_and_cache_fp8(Tensor positions, Tensor(a0!) query, "
+        "Tensor(a1!) key, Tensor value, int head_size, Tensor cos_sin_cache, bool is_neox, Tensor(a2!) key_cache, "
+        "Tensor(a3!) value_cache, Tensor slot_mapping, float k_scale, float v_scale) -> ()",
     }
     for name, schema in schemas.items():
         got = str(getattr(torch.ops.decode_kernels, name).default._schema).replace("decode_kernels::", "")

@@ -27,6 +27,7 @@ from parity import assert_max_abs, assert_ulp, attention_f32
 pytestmark = pytest.mark.gpu
 
 DTYPES = [torch.float16, torch.bfloat16]
+FP8 = torch.float8_e4m3fn
 
 
 def _stream():
@@ -260,8 +261,9 @@ def test_decode_step_appends_and_attends(dtype, layout):
 # rotary_embedding_and_cache: both steps in one launch, bit-identical to the
 # two ops in sequence and to the oracle
 # ---------------------------------------------------------------------------
-def _fused_inputs(dtype, is_neox, head_size, rot_dim, layout, seed, t=61, hq=8, hkv=2, bs=16, misalign=False):
-    kv = make_paged_kv([700, 300], hkv, head_size, bs, dtype, "cuda", layout=layout, seed=seed)
+def _fused_inputs(dtype, is_neox, head_size, rot_dim, layout, seed, t=61, hq=8, hkv=2, bs=16, misalign=False,
+                  cache_dtype=None):
+    kv = make_paged_kv([700, 300], hkv, head_size, bs, cache_dtype or dtype, "cuda", layout=layout, seed=seed)
     g = torch.Generator(device="cuda").manual_seed(seed + 1)
     width = (hq + 2 * hkv) * head_size
     buf = torch.randn(t, width + 1, generator=g, device="cuda", dtype=dtype)
@@ -275,8 +277,9 @@ def _fused_inputs(dtype, is_neox, head_size, rot_dim, layout, seed, t=61, hq=8, 
     return kv, buf, q, k, v, cache, pos, slots
 
 
-def _run_fused_and_pair(kv, buf, q, k, v, cache, pos, slots, head_size, is_neox):
-    """(fused results, two-op results): q, k, k_cache, v_cache of each."""
+def _run_fused_and_pair(kv, buf, q, k, v, cache, pos, slots, head_size, is_neox, **scales):
+    """(fused results, two-op results): q, k, k_cache, v_cache of each
+    (fp8 caches as their bytes)."""
     kc2, vc2 = kv.k_cache.clone(), kv.v_cache.clone()
     buf2 = buf.clone()
     off = q.data_ptr() - buf.data_ptr()
@@ -285,10 +288,11 @@ def _run_fused_and_pair(kv, buf, q, k, v, cache, pos, slots, head_size, is_neox)
     k2 = buf2.view(-1)[(k.data_ptr() - buf.data_ptr()) // el :].as_strided(k.shape, k.stride())
     v2 = buf2.view(-1)[(v.data_ptr() - buf.data_ptr()) // el :].as_strided(v.shape, v.stride())
     dk.rotary_embedding(pos, q2, k2, head_size, cache, is_neox)
-    dk.reshape_and_cache(k2, v2, kc2, vc2, slots)
-    dk.rotary_embedding_and_cache(pos, q, k, v, head_size, cache, is_neox, kv.k_cache, kv.v_cache, slots)
+    dk.reshape_and_cache(k2, v2, kc2, vc2, slots, **scales)
+    dk.rotary_embedding_and_cache(pos, q, k, v, head_size, cache, is_neox, kv.k_cache, kv.v_cache, slots, **scales)
     torch.cuda.synchronize()
-    return (q, k, kv.k_cache, kv.v_cache), (q2, k2, kc2, vc2)
+    b = lambda c: c.view(torch.uint8) if c.dtype == FP8 else c  # noqa: E731
+    return (q, k, b(kv.k_cache), b(kv.v_cache)), (q2, k2, b(kc2), b(vc2))
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
@@ -347,7 +351,6 @@ def test_fused_rope_and_cache_capi_and_errors():
 # ---------------------------------------------------------------------------
 # Cache write into an fp8 (e4m3fn) cache: x / scale, saturated, nearest even
 # ---------------------------------------------------------------------------
-FP8 = torch.float8_e4m3fn
 
 
 def _fp8_rows(t, hkv, d, dtype, seed):
@@ -426,3 +429,67 @@ def test_fp8_decode_step_writes_then_attends(dtype):
     assert torch.equal(kv.v_cache.cpu().view(torch.uint8), want_v.view(torch.uint8))
     ref = attention_f32(q3, kv.k_cache.float() * ks, kv.v_cache.float() * vs, kv.block_tables, new_lens)
     assert_max_abs(out, ref, dtype, "fp8 attention after the fp8 cache write")
+
+
+# ---------------------------------------------------------------------------
+# rotary_embedding_and_cache into fp8 caches: equal to rotary_embedding then
+# the fp8 cache write, and to the oracle. Small scales push part of k / v
+# past +-448 so the saturation is exercised.
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("is_neox", [True, False])
+@pytest.mark.parametrize("head_size,rot_dim", [(128, 128), (128, 64), (256, 256)])
+@pytest.mark.parametrize("layout", ["nhd", "vllm"])
+@pytest.mark.parametrize("k_scale,v_scale", [(1.0, 1.0), (0.004, 0.01)])
+def test_fused_rope_and_fp8_cache_equals_the_two_ops(dtype, is_neox, head_size, rot_dim, layout, k_scale, v_scale):
+    seed = head_size + rot_dim + 3 * is_neox + 7
+    kv, buf, q, k, v, cache, pos, slots = _fused_inputs(dtype, is_neox, head_size, rot_dim, layout, seed,
+                                                        cache_dtype=FP8)
+    kc0, vc0 = kv.k_cache.cpu(), kv.v_cache.cpu()
+    q0, k0, v0 = q.cpu(), k.cpu(), v.cpu()
+    fused, pair = _run_fused_and_pair(kv, buf, q, k, v, cache, pos, slots, head_size, is_neox, k_scale=k_scale,
+                                      v_scale=v_scale)
+    for name, a, b in zip(("query", "key", "key_cache", "value_cache"), fused, pair):
+        assert torch.equal(a, b), f"fused {name} differs from rotary_embedding + fp8 reshape_and_cache"
+    want_q, want_k = rotary_embedding_reference(pos.cpu(), q0, k0, head_size, cache.cpu(), is_neox)
+    want_kc, want_vc = reshape_and_cache_reference(want_k.reshape(k0.shape[0], -1, head_size), v0, kc0, vc0,
+                                                   slots.cpu(), k_scale, v_scale)
+    assert_ulp(q, want_q, 0, "fused rotary(query)")
+    assert_ulp(k, want_k, 0, "fused rotary(key)")
+    assert torch.equal(fused[2].cpu(), want_kc.view(torch.uint8))
+    assert torch.equal(fused[3].cpu(), want_vc.view(torch.uint8))
+    if k_scale != 1.0:
+        assert (want_kc.float().abs() == 448).any(), "no saturated key in the case"
+
+
+@pytest.mark.parametrize("is_neox", [True, False])
+@pytest.mark.parametrize("case", ["misaligned_rows", "rot_dim_36"])
+def test_fused_rope_and_fp8_cache_scalar_path(is_neox, case):
+    rot = 36 if case == "rot_dim_36" else 64
+    kv, buf, q, k, v, cache, pos, slots = _fused_inputs(torch.bfloat16, is_neox, 64, rot, "vllm", seed=60 + rot,
+                                                        misalign=case == "misaligned_rows", cache_dtype=FP8)
+    fused, pair = _run_fused_and_pair(kv, buf, q, k, v, cache, pos, slots, 64, is_neox, k_scale=0.01, v_scale=0.5)
+    for name, a, b in zip(("query", "key", "key_cache", "value_cache"), fused, pair):
+        assert torch.equal(a, b), f"fused {name} differs ({case})"
+
+
+def test_fused_rope_and_fp8_cache_capi():
+    dtype = torch.float16
+    kv, buf, q, k, v, cache, pos, slots = _fused_inputs(dtype, False, 128, 128, "hnd", seed=70, cache_dtype=FP8)
+    kv2 = make_paged_kv([700, 300], 2, 128, 16, FP8, "cuda", layout="hnd", seed=70)
+    buf2 = buf.clone()
+    q2, k2, v2 = buf2[:, : 8 * 128], buf2[:, 8 * 128 : 10 * 128], buf2[:, 10 * 128 : 12 * 128]
+    r = capi.rotary_params(pos, q2, k2, 128, cache, False)
+    c = capi.cache_write_params(k2, v2, kv2.k_cache, kv2.v_cache, slots)
+    rc = capi.lib().dk_rotary_embedding_and_cache_fp8(ctypes.byref(r), ctypes.byref(c), capi.dtype_code(dtype), 0.02,
+                                                      0.03, _stream())
+    assert rc == 0, capi.last_error()
+    dk.rotary_embedding_and_cache(pos, q, k, v, 128, cache, False, kv.k_cache, kv.v_cache, slots, k_scale=0.02,
+                                  v_scale=0.03)
+    torch.cuda.synchronize()
+    assert torch.equal(buf, buf2)
+    assert torch.equal(kv.k_cache.view(torch.uint8), kv2.k_cache.view(torch.uint8))
+    assert torch.equal(kv.v_cache.view(torch.uint8), kv2.v_cache.view(torch.uint8))
+    with pytest.raises(RuntimeError, match="float8_e4m3fn"):
+        torch.ops.decode_kernels.rotary_embedding_and_cache_fp8(pos, q, k, v, 128, cache, False, kv.k_cache.view(
+            torch.uint8), kv.v_cache.view(torch.uint8), slots, 1.0, 1.0)
