@@ -374,7 +374,11 @@ def extras_layer_step() -> dict:
 # ---------------------------------------------------------------------------
 # CPU baseline (the oracle on the host cores) + pre-report correctness check
 # ---------------------------------------------------------------------------
-def cpu_baseline_and_check(case, budget_s: float = 20.0) -> dict:
+def cpu_baseline_and_check(case, budget_s: float = 20.0, min_s: float = 10.0) -> dict:
+    """The oracle on the host's cores over the same workload, one sequence per
+    call: sequences in order until `budget_s` is spent; if the whole batch
+    takes less than `min_s`, further passes over it until `min_s` is reached
+    (the GPU output is checked on the first pass)."""
     from oracle.reference import paged_attention_reference
 
     cores = len(os.sched_getaffinity(0))
@@ -384,29 +388,34 @@ def cpu_baseline_and_check(case, budget_s: float = 20.0) -> dict:
     gpu_out = case["out"].float().cpu()
     elt = 2
     hkv, d = case["k"].shape[2], case["k"].shape[3]
-    done_bytes, elapsed, seqs = 0, 0.0, 0
+    done_bytes, elapsed, seqs, passes = 0, 0.0, 0, 0
     worst = 0.0
     paged_attention_reference(q[:1], k, v, bt[:1], lens[:1])  # warm-up
-    for s in range(q.shape[0]):
-        t0 = time.perf_counter()
-        ref = paged_attention_reference(q[s : s + 1], k, v, bt[s : s + 1], lens[s : s + 1])
-        elapsed += time.perf_counter() - t0
-        worst = max(worst, (gpu_out[s] - ref[0].float()).abs().max().item())
-        done_bytes += int(lens[s]) * 2 * hkv * d * elt + 2 * q.shape[1] * d * elt
-        seqs += 1
-        if elapsed >= budget_s:
-            break
+    while elapsed < min_s and elapsed < budget_s:
+        for s in range(q.shape[0]):
+            t0 = time.perf_counter()
+            ref = paged_attention_reference(q[s : s + 1], k, v, bt[s : s + 1], lens[s : s + 1])
+            elapsed += time.perf_counter() - t0
+            if passes == 0:
+                worst = max(worst, (gpu_out[s] - ref[0].float()).abs().max().item())
+                seqs += 1
+            done_bytes += int(lens[s]) * 2 * hkv * d * elt + 2 * q.shape[1] * d * elt
+            if elapsed >= budget_s:
+                break
+        passes += 1
     del k, v
     if worst > 2e-2:
         raise AssertionError(f"paged_attention_decode differs from the oracle by {worst:.3e} (> 2e-2)")
+    n = q.shape[0]
+    what = f"the first {seqs} of {n} sequences" if passes == 1 else f"all {n} sequences, {passes} passes"
     return {
         "value": round(done_bytes / elapsed / 1e12, 6),
         "unit": "TB/s",
         "cores": cores,
         "kind": "port",
-        "sample": f"oracle.reference.paged_attention_reference (torch CPU, fp32) on the first {seqs} of 64 "
-        f"sequences of the same workload ({done_bytes / 1e6:.0f} MB of bf16 KV, bf16 inputs), one sequence per call, "
-        f"{elapsed:.1f} s; GPU output matched to {worst:.2e} max abs on those sequences",
+        "sample": f"oracle.reference.paged_attention_reference (torch CPU, fp32) on {what} of the same workload "
+        f"({done_bytes / 1e6:.0f} MB of bf16 KV read in total, bf16 inputs), one sequence per call, {elapsed:.1f} s; "
+        f"GPU output matched to {worst:.2e} max abs on the {seqs} sequences of the first pass",
     }
 
 
