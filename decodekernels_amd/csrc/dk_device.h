@@ -24,12 +24,16 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 
 // ---------------------------------------------------------------------------
 // 16-bit element types
 // ---------------------------------------------------------------------------
 struct Bf16 {
   using mfma_vec = bf16x8;
+  using vec2 = bf16x2;
   static __device__ __forceinline__ float lo(uint32_t w) { return __uint_as_float(w << 16); }
   static __device__ __forceinline__ float hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
   static __device__ __forceinline__ float to_float(uint16_t h) { return __uint_as_float(static_cast<uint32_t>(h) << 16); }
@@ -51,6 +55,7 @@ struct Bf16 {
 
 struct F16 {
   using mfma_vec = f16x8;
+  using vec2 = f16x2;
   static __device__ __forceinline__ float lo(uint32_t w) {
     return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(w & 0xffffu)));
   }
@@ -74,9 +79,12 @@ struct F16 {
   static constexpr uint16_t kOne = 0x3C00;
 };
 
+// (a, b) rounded to nearest even into one word, a in the low half: one
+// two-source v_cvt_pk_{bf16,f16}_f32, the same rounding as from_float on
+// each (converting the halves one by one costs a shift and an or on top).
 template <typename E>
 __device__ __forceinline__ uint32_t pack2(float a, float b) {
-  return static_cast<uint32_t>(E::from_float(a)) | (static_cast<uint32_t>(E::from_float(b)) << 16);
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{a, b}, typename E::vec2));
 }
 
 // ---------------------------------------------------------------------------
