@@ -453,6 +453,20 @@ def pmc_workload_gemm_skinny(calls: int = 3) -> None:
     print(f"pmc skinny gemm workload done: {calls} calls each at M=1 and M=64 (N=4096, K=14336)", flush=True)
 
 
+def pmc_workload_attention_fp8(calls: int = 3) -> None:
+    """What the fp8-cache counter runs profile: the headline batch with a bf16
+    cache, then the same batch with an fp8 (e4m3fn) cache, `calls` times each."""
+    lens = torch.randint(512, 4097, (64,), generator=torch.Generator().manual_seed(0)).tolist()
+    for kv in (torch.bfloat16, torch.float8_e4m3fn):
+        c = attention_case(64, 32, 8, 128, 16, lens, torch.bfloat16, "vllm", seed=60, q_scale=128**-0.5, kv_dtype=kv,
+                           k_scale=0.5, v_scale=0.5)
+        for _ in range(calls):
+            c["run"]()
+        torch.cuda.synchronize()
+        del c
+    print(f"pmc fp8 attention workload done: {calls} calls each with a bf16 and an fp8 cache", flush=True)
+
+
 def pmc_workload(calls: int = 5) -> None:
     """What the counter runs profile: the headline op `calls` times, then a
     copy of CALIBRATION_BYTES (read once, written once) to scale the counters."""
@@ -486,7 +500,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-extras", action="store_true", help="skip the secondary configs")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline (and its correctness check)")
-    ap.add_argument("--pmc-workload", nargs="?", const="attention", choices=["attention", "gemm", "gemm_skinny"],
+    ap.add_argument("--pmc-workload", nargs="?", const="attention", choices=["attention", "attention_fp8", "gemm", "gemm_skinny"],
                     help="run only what the rocprofv3 --pmc passes profile (default: attention)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -495,6 +509,9 @@ def main() -> int:
         return 2
     if not dk.is_available():
         raise RuntimeError("decodekernels_amd HIP extension not available (build it with __graft_entry__.build())")
+    if args.pmc_workload == "attention_fp8":
+        pmc_workload_attention_fp8()
+        return 0
     if args.pmc_workload == "gemm_skinny":
         pmc_workload_gemm_skinny()
         return 0

@@ -263,8 +263,8 @@ __global__ __launch_bounds__(kThreads) void rotary_and_cache_kernel(const KParam
   const bool rot = pos >= 0 && pos < r.max_position;
   const int64_t slot = c.slots[t];
   const int64_t blk = slot >= 0 ? slot / c.block_size : 0;
-  const int64_t off = slot - blk * c.block_size;
   const bool put = slot >= 0 && blk < c.num_blocks;
+  const int64_t off = put ? slot - blk * c.block_size : 0;  // a skipped slot never forms a cache address
   if (!rot && !put) return;
   const int half = r.rot_dim / 2;
   const int64_t crow = pos * r.cache_stride;
