@@ -124,6 +124,25 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
+// v combined over lanes l, l ^ 16, l ^ 32, l ^ 48 (the four 16-lane rows),
+// without an LDS round trip: gfx950's v_permlane16_swap / v_permlane32_swap
+// hand each lane its own value and its partner's (lane l ^ 16, then l ^ 32).
+// The sum is (v[l] + v[l^16]) + (v[l^32] + v[l^48]) for every lane, the same
+// association as two xor-shuffles by 16 and 32.
+__device__ __forceinline__ float rows_max(float v) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+
+__device__ __forceinline__ float rows_sum(float v) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
   for (int off = kWave / 2; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, kWave));

@@ -432,8 +432,7 @@ struct UnitEngine {
       x[i] = valid ? s[i] * p.scale_log2 : -__builtin_huge_valf();
       tmax = fmaxf(tmax, x[i]);
     }
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 16, kWave));
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 32, kWave));
+    tmax = rows_max(tmax);  // over the tile's 16 tokens
     m_true = fmaxf(m_true, tmax);
     if (__any(tmax > m_ref + kLazyMax)) {
       const float m_new = fmaxf(m_ref, tmax);
@@ -529,8 +528,7 @@ struct UnitEngine {
   __device__ __forceinline__ void merge(const Unit& u) {
     const int group = p.group;
     // Exp-sum of head l16 over all four lane groups.
-    float l_tot = l_run + __shfl_xor(l_run, 16, kWave);
-    l_tot += __shfl_xor(l_tot, 32, kWave);
+    const float l_tot = rows_sum(l_run);
     if (lane < 16) {
       sm.m[wave][lane] = m_ref;
       sm.t[wave][lane] = m_true;
