@@ -10,27 +10,35 @@
 //
 // The decomposition is CDNA4-specific:
 //
-// * Workgroup = 4 waves of 64 lanes for one (kv_head, seq, partition). The
-//   partition's tokens are cut into 16-token tiles; wave w takes tiles
-//   w, w+4, ... and keeps its own online-softmax state; the 4 waves merge
-//   through LDS at the end (the same log-sum-exp rule as split-K).
-// * Q·Kᵀ for a tile is 16 tokens x 16 (padded) query heads x head_dim on
+// * A work unit is a token range of one KV head x one sequence with the
+//   KV head's whole query-head group; its tokens form 16-token tiles, wave w
+//   of the workgroup takes tiles w, w + NW, ... (NW = 4, 2 at head_dim > 128)
+//   with its own online-softmax state, and the waves merge through LDS (the
+//   split-K log-sum-exp rule). Two drivers run units: the grid kernel (one
+//   workgroup per 1024-token unit, two 512-token workspace slots) and the
+//   balanced kernel (a resident-sized grid; each workgroup takes an equal
+//   share of all tiles and writes one workspace row per piece). The reduce
+//   kernel merges the rows of each query head.
+// * Q.K^T for a tile is 16 tokens x 16 (padded) query heads x head_dim on
 //   v_mfma_f32_16x16x32_{bf16,f16}. Lane l feeds K row (l % 16) with one
 //   16-byte load per 32-column step, and the query fragment of head (l % 16)
 //   in the model dtype (exact); the fp32 logits come out as
 //   S[token 4*(l/16)+r][head l%16], r = 0..3.
-// * P·V on v_mfma_f32_16x16x16: V is loaded exactly like K and transposed on
-//   the matrix core -- a 16x16x32 MFMA of a V chunk against an identity
-//   fragment returns it in the B-operand layout (lane l: V[token 4*(l/16)+r]
-//   [column l%16]) -- and P, which leaves Q·Kᵀ already in the A-operand
-//   layout, is split into hi + lo parts in the model dtype: two MFMAs per
-//   16-column block keep the products accurate to ~2^-17 relative.
-//   Accumulators: lane l holds O[head 4*(l/16)+i][column 16n + l%16].
+// * P.V on v_mfma_f32_16x16x16, whose A operand is P exactly as Q.K^T leaves
+//   it; P is split into hi + lo parts in the model dtype (two MFMAs per
+//   16-column block keep the products accurate to ~2^-17 relative). V is
+//   loaded like K and brought into the B-operand layout through the wave's
+//   LDS tile with ds_read_b64_tr_b16 transpose reads (or, DK_ATTN_VTR=0, by
+//   MFMAs against an identity operand; the same bits). Accumulators: lane l
+//   holds O[head 4*(l/16)+i][column 16n + l%16].
 // * Logits are kept in log2 units (scale * log2 e folded into one multiply)
-//   and exponentiated with v_exp_f32; max_logits are stored in natural-log
-//   units so the workspace means what the reference's does.
-// * K/V tiles are double-buffered in registers: the loads for tile n+1 are
-//   in flight while tile n is multiplied.
+//   and exponentiated with v_exp_f32 against a lazily moved reference max;
+//   max_logits are stored in natural-log units so the workspace means what
+//   the reference's does.
+// * K/V tiles run through DEPTH-deep register rings of raw buffer loads.
+// * An fp8 (e4m3fn) cache takes the same path with 16-byte loads of 64
+//   columns per lane group, converted exactly to the model dtype when a tile
+//   is consumed; k_scale folds into the logit scale, v_scale into the output.
 #include <atomic>
 #include <cstdlib>
 #include <cstring>

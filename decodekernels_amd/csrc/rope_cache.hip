@@ -17,7 +17,10 @@
 // Both are HBM-bound copies with a little arithmetic: one workgroup per
 // token, 16-byte (or 8-byte) vectors where the layout allows, a scalar path
 // otherwise. Positions outside the table and slots outside the cache are
-// skipped rather than read or written out of bounds.
+// skipped rather than read or written out of bounds. The cache write also
+// fills fp8 (e4m3fn) caches (x / scale, saturated, nearest even), and
+// rotary_embedding_and_cache runs both steps in one launch with the results
+// of the two in sequence, into 16-bit or fp8 caches.
 #include <cmath>
 #include <type_traits>
 

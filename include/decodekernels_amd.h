@@ -10,9 +10,12 @@
  * No entry point allocates device memory, so all of them can be recorded
  * into a HIP graph.
  *
- * Each function replaces one launcher of DecodeKernels (the reference), whose
- * `dk::launch_*<T>` templates take the same argument lists for one element
- * type T in {__half, __nv_bfloat16}; here the type is the `dtype` argument.
+ * The five compute entry points of the reference's hot path each replace one
+ * launcher of DecodeKernels (the reference), whose `dk::launch_*<T>`
+ * templates take the same argument lists for one element type T in
+ * {__half, __nv_bfloat16}; here the type is the `dtype` argument. The other
+ * compute entry points (fp8 KV cache, RoPE, the KV-cache write) have no
+ * counterpart in the reference; each says so and names what it follows.
  */
 #ifndef DECODEKERNELS_AMD_H_
 #define DECODEKERNELS_AMD_H_
