@@ -84,6 +84,9 @@ constexpr int kUnit = 2 * kPart;          // split-K work unit: two slots (its b
 #ifndef DK_ATTN_OCC_D128
 #define DK_ATTN_OCC_D128 2  // waves per SIMD targeted at head_dim 128
 #endif
+#ifndef DK_ATTN_OCC_D256
+#define DK_ATTN_OCC_D256 1  // waves per SIMD targeted at head_dim 192 / 256
+#endif
 #ifndef DK_ATTN_OCC_D64
 #define DK_ATTN_OCC_D64 4  // waves per SIMD targeted at head_dim 64
 #endif
@@ -210,7 +213,7 @@ template <int D, bool KV8 = false>
 constexpr int attn_occupancy() {
   // Classes: D <= 64, 64 < D <= 128 (96, 128), D > 128 (192, 256).
   if constexpr (KV8) return D > 128 ? DK_ATTN_OCC_FP8_D256 : (D > 64 ? DK_ATTN_OCC_FP8_D128 : DK_ATTN_OCC_D64);
-  return D > 128 ? 1 : (D > 64 ? DK_ATTN_OCC_D128 : DK_ATTN_OCC_D64);
+  return D > 128 ? DK_ATTN_OCC_D256 : (D > 64 ? DK_ATTN_OCC_D128 : DK_ATTN_OCC_D64);
 }
 
 // LDS of one work unit: per-wave softmax state and partial outputs, merged at the end.
