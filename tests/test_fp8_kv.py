@@ -55,6 +55,24 @@ def test_fp8_single_pass_and_split(dtype, head_dim, group, layout):
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("head_dim,group", [(192, 4), (192, 8), (128, 16), (64, 16), (256, 16)])
+@pytest.mark.parametrize("schedule", ["grid", "balanced"])
+def test_fp8_head_dim_192_and_group_16(dtype, head_dim, group, schedule, monkeypatch):
+    """Past the reference's limits with an fp8 cache: head_dim 192 (the D=256
+    class) and GQA groups of 16 (the LDS merge in two passes of 8 heads),
+    single pass and split-K under both schedules."""
+    monkeypatch.setenv("DK_ATTN_SCHEDULE", schedule)
+    lens = [1, 17, 300, 512, 513, 1500, 0, 2100]
+    kv = make_paged_kv(lens, 2, head_dim, 16, FP8, "cuda", layout="vllm", seed=head_dim + group + 7)
+    q = _q(len(lens), 2 * group, head_dim, dtype, seed=3)
+    out = _check(q, kv, 0.3, 0.4, dtype)
+    assert (out[6] == 0).all(), "an empty sequence gives zeros"
+    short = [1, 17, 300, 512]
+    kv_s = make_paged_kv(short, 2, head_dim, 16, FP8, "cuda", layout="nhd", seed=head_dim + group + 8)
+    _check(_q(len(short), 2 * group, head_dim, dtype, seed=4), kv_s, 0.3, 0.4, dtype)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("schedule", ["grid", "balanced"])
 def test_fp8_long_contexts_both_schedules(dtype, schedule, monkeypatch):
     monkeypatch.setenv("DK_ATTN_SCHEDULE", schedule)

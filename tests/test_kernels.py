@@ -259,6 +259,28 @@ def test_paged_attention_split_k_schedules(case, monkeypatch):
         assert torch.equal(out, again), f"{schedule} schedule is not deterministic"
 
 
+@pytest.mark.parametrize("num_seqs", [2048, 2049])
+def test_paged_attention_split_k_many_sequences(num_seqs, monkeypatch):
+    """Split-K at the balanced schedule's sequence limit (its length scan holds
+    2048 sequences in LDS) and one past it, where the grid schedule takes over
+    even when the balanced one is asked for: both against the oracle, and
+    deterministic."""
+    g = torch.Generator().manual_seed(num_seqs)
+    lens = torch.randint(0, 1101, (num_seqs,), generator=g)
+    lens[0] = 1100
+    lens = lens.tolist()
+    kv = make_paged_kv(lens, 1, 64, 16, torch.bfloat16, "cuda", layout="nhd", seed=3)
+    q = _q(num_seqs, 4, 64, torch.bfloat16)
+    ref = attention_f32(q, kv.k_cache, kv.v_cache, kv.block_tables, kv.seq_lens)
+    monkeypatch.setenv("DK_ATTN_SCHEDULE", "balanced")
+    out = dk.paged_attention_decode(q, kv.k_cache, kv.v_cache, kv.block_tables, kv.seq_lens, max_seq_len=1100)
+    again = dk.paged_attention_decode(q, kv.k_cache, kv.v_cache, kv.block_tables, kv.seq_lens, max_seq_len=1100)
+    torch.cuda.synchronize()
+    assert_max_abs(out, ref, torch.bfloat16, f"{num_seqs} sequences")
+    assert torch.equal(out, again)
+    assert (out[kv.seq_lens == 0] == 0).all()
+
+
 # (lens, num_kv_heads, max_seq_len): shapes whose tile shares end inside short
 # streams, a single long stream, a two-row workspace and mostly-empty batches.
 BALANCED_CASES = [
