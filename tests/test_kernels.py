@@ -376,6 +376,8 @@ GEMM_SHAPES = [
     (512, 6144, 1032),  # 128x128 tiles
     (512, 11008, 4096),
     (1000, 1000, 136),
+    (274, 10917, 520),  # 256x128 tiles, partial in M and N
+    (2000, 6000, 264),  # 256x256 tiles, partial in M and N
 ]
 
 
