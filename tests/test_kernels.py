@@ -492,7 +492,7 @@ def test_rms_norm(dtype, rows, H):
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
-@pytest.mark.parametrize("rows,H", [(1, 4096), (17, 2048), (5, 100), (64, 4096)])
+@pytest.mark.parametrize("rows,H", [(1, 4096), (17, 2048), (5, 100), (64, 4096), (128, 8192), (2, 16384), (3, 40000)])
 def test_fused_add_rms_norm(dtype, rows, H):
     x = torch.randn(rows, H, device="cuda", dtype=dtype)
     r = torch.randn(rows, H, device="cuda", dtype=dtype)
