@@ -684,7 +684,13 @@ constexpr int kMinShareTiles = 64;
 #ifndef DK_ATTN_STREAM_COST
 #define DK_ATTN_STREAM_COST 8  // per-stream overhead, in tiles, of the share balance
 #endif
-constexpr int kStreamCost = DK_ATTN_STREAM_COST;
+#ifndef DK_ATTN_STREAM_COST_FP8
+#define DK_ATTN_STREAM_COST_FP8 12  // the same with an fp8 cache (its tiles take about half the time)
+#endif
+template <bool KV8>
+constexpr int stream_cost() {
+  return KV8 ? DK_ATTN_STREAM_COST_FP8 : DK_ATTN_STREAM_COST;
+}
 #ifndef DK_ATTN_PAIR_RATIO
 #define DK_ATTN_PAIR_RATIO 180  // with two workgroups per CU: first-half share / second-half share, x100
 #endif
@@ -703,6 +709,7 @@ void paged_attention_balanced_kernel(const KParams p) {
   const int P = p.max_partitions;
   const int max_tokens = P * kPart;  // tokens past the workspace are ignored
   auto tiles_of = [&](int s) { return (len[s] + kTile - 1) / kTile; };
+  constexpr int kStreamCost = stream_cost<KV8>();
   auto cost_of_len = [](int l) { return l > 0 ? (l + kTile - 1) / kTile + kStreamCost : 0; };
 
   // Per-thread chunk of sequences -> block-wide inclusive scan of stream costs.
