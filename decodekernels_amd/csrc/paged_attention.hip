@@ -692,7 +692,7 @@ constexpr int stream_cost() {
   return KV8 ? DK_ATTN_STREAM_COST_FP8 : DK_ATTN_STREAM_COST;
 }
 #ifndef DK_ATTN_PAIR_RATIO
-#define DK_ATTN_PAIR_RATIO 180  // with two workgroups per CU: first-half share / second-half share, x100
+#define DK_ATTN_PAIR_RATIO 200  // with two workgroups per CU: first-half share / second-half share, x100
 #endif
 
 template <typename E, int D, bool BS16, int ALIGN, int NW, bool KV8>
