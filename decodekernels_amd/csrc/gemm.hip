@@ -222,7 +222,10 @@ __global__ __launch_bounds__(WN * WK * kWave) void gemm_skinny_lds_kernel(const 
 // the ~32 workgroups resident on one XCD share A rows and B rows in its L2.
 constexpr int kDmaBK = 64;
 constexpr int kXcds = 8;
-constexpr int kGroupM = 4;
+#ifndef DK_GEMM_GROUP_M
+#define DK_GEMM_GROUP_M 4  // tile rows per group of the XCD-contiguous tile order
+#endif
+constexpr int kGroupM = DK_GEMM_GROUP_M;
 
 __device__ __forceinline__ int swz(int r) { return r & 7; }
 
