@@ -18,7 +18,11 @@ handle, with counters so a silent fallback cannot pass for a result.
 
 Prefill and mixed batches, sliding windows, ALiBi, soft-capping, attention
 sinks, context parallelism, cross/encoder attention and graph capture all go to
-vLLM's implementation (reference: decode_kernels/vllm_patch.py:60-99). Unlike
+vLLM's implementation (reference: decode_kernels/vllm_patch.py:60-99), and so
+does every call on a backend whose impl has no ``do_kv_cache_update`` step: the
+reference relies on vLLM writing the new token's K/V into the cache before
+``forward`` runs (decode_kernels/vllm_patch.py:11-12), and a backend that writes
+it inside ``forward`` must keep its own. Unlike
 the reference, an fp8 KV cache (``kv_cache_dtype`` "fp8" / "fp8_e4m3", OCP
 e4m3fn -- vLLM's fp8 on gfx950) with float scales on the layer runs
 ``paged_attention_decode_fp8``; other quantized caches (e4m3fnuz, e5m2, ...)
@@ -125,6 +129,12 @@ def _attention_eligible(impl, query, kv_cache, attn_metadata, output, output_sca
     if query.is_cuda and torch.cuda.is_current_stream_capturing():
         # The single-pass / split-K choice depends on the host-side max_seq_len,
         # which a captured graph would freeze.
+        return False
+    # The new tokens' K/V must already be in the cache: vLLM writes them in a
+    # separate do_kv_cache_update step before forward (what the reference
+    # relies on). A backend without that step writes them inside its own
+    # forward, which must then run.
+    if not callable(getattr(impl, "do_kv_cache_update", None)):
         return False
     if getattr(impl, "attn_type", _decoder_attention_type()) != _decoder_attention_type():
         return False

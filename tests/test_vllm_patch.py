@@ -30,7 +30,8 @@ def fresh_state():
 
 def _impl(**over):
     base = dict(attn_type="decoder", dcp_world_size=1, kv_cache_dtype="auto", alibi_slopes=None, logits_soft_cap=None,
-                sliding_window=None, sinks=None, head_size=D, num_heads=HQ, num_kv_heads=HKV, scale=D**-0.5)
+                sliding_window=None, sinks=None, head_size=D, num_heads=HQ, num_kv_heads=HKV, scale=D**-0.5,
+                do_kv_cache_update=lambda *a, **k: None)
     base.update(over)
     return SimpleNamespace(**base)
 
@@ -64,6 +65,7 @@ def test_attention_eligible_base_case():
 @pytest.mark.parametrize(
     "impl_over,meta_over,other",
     [
+        (dict(do_kv_cache_update=None), {}, None),  # the backend writes the cache inside forward
         (dict(attn_type="encoder"), {}, None),
         (dict(dcp_world_size=2), {}, None),
         (dict(kv_cache_dtype="fp8"), {}, None),
@@ -230,6 +232,21 @@ def test_attention_patch_routes_decode_batches(fake_vllm):
     impl.forward(None, q, None, None, kv, meta, out)
     assert fake_vllm.calls[-1] == "vllm_attention"
     assert vllm_patch.stats()["attention_kernel_calls"] == 1
+    assert vllm_patch.stats()["attention_fallback_calls"] == 1
+
+
+def test_attention_patch_keeps_backends_that_write_the_cache_in_forward(fake_vllm):
+    """Without a separate do_kv_cache_update step the backend's forward writes
+    the new token's K/V itself, so it must run: every call falls back."""
+    vllm_patch.apply(["attention"])
+    impl = fake_vllm.FlashAttentionImpl()
+    for k, v in vars(_impl()).items():
+        if k != "do_kv_cache_update":
+            setattr(impl, k, v)
+    q, kv, meta, out = _inputs()
+    assert impl.forward(None, q, None, None, kv, meta, out) is out
+    assert fake_vllm.calls == ["vllm_attention"]
+    assert vllm_patch.stats()["attention_kernel_calls"] == 0
     assert vllm_patch.stats()["attention_fallback_calls"] == 1
 
 
