@@ -14,6 +14,7 @@ in one launch.
 from .ops import (
     MAX_GQA_GROUP,
     PARTITION_SIZE,
+    SUPPORTED_FP8_HEAD_DIMS,
     SUPPORTED_HEAD_DIMS,
     alloc_workspace,
     fused_add_rms_norm,
@@ -31,6 +32,7 @@ from .ops import (
 __all__ = [
     "MAX_GQA_GROUP",
     "PARTITION_SIZE",
+    "SUPPORTED_FP8_HEAD_DIMS",
     "SUPPORTED_HEAD_DIMS",
     "alloc_workspace",
     "fused_add_rms_norm",

@@ -17,6 +17,7 @@ import torch
 PARTITION_SIZE = 512  # tokens per split-K workspace slot (DK_PARTITION_SIZE in the C ABI)
 MAX_GQA_GROUP = 16  # query heads per KV head (DK_MAX_GQA_GROUP; the reference stops at 8)
 SUPPORTED_HEAD_DIMS = (64, 96, 128, 192, 256)  # the reference: 64, 128, 256
+SUPPORTED_FP8_HEAD_DIMS = (64, 128, 192, 256)  # an fp8 cache row loads 64 columns per 16-byte lane group
 
 try:
     from . import _C  # noqa: F401  (registers torch.ops.decode_kernels.*)

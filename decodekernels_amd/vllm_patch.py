@@ -11,8 +11,9 @@ handle, with counters so a silent fallback cannot pass for a result.
   vLLM the decode path may live in the ROCm or Triton backend instead, so every
   known backend class that exists is patched. The cache layout is read from
   the tensor: the interleaved ``[blocks, kv_heads, block_size, 2*head_dim]``
-  buffer (viewed as strided K and V, as the reference does) or a stacked
-  ``[2, blocks, block_size, kv_heads, head_dim]`` pair.
+  buffer (viewed as strided K and V, as the reference does), a stacked
+  ``[2, blocks, block_size, kv_heads, head_dim]`` pair or the Triton
+  backend's block-major ``[blocks, 2, block_size, kv_heads, head_dim]``.
 * ``RMSNorm.forward_cuda`` -- rms_norm / fused_add_rms_norm.
 * ``SiluAndMul.forward_cuda`` -- silu_and_mul.
 
@@ -82,16 +83,29 @@ def _decoder_attention_type():
         return "decoder"
 
 
-def split_kv_cache(kv_cache: torch.Tensor, head_size: int):
+def split_kv_cache(kv_cache: torch.Tensor, head_size: int, num_kv_heads: int | None = None):
     """K and V views [blocks, block_size, kv_heads, head_dim] of vLLM's cache, or None
-    for a layout the kernels do not read."""
+    for a layout the kernels do not read.
+
+    * [blocks, kv_heads, block_size, 2*D]: the interleaved buffer, viewed as two
+      strided NHD tensors (reference: vllm_patch.py:121-122);
+    * [2, blocks, block_size, kv_heads, D]: a K/V-major stacked pair;
+    * [blocks, 2, block_size, kv_heads, D]: a block-major pair (vLLM's Triton backend).
+
+    The two 5-D pairs cannot be told apart when both leading dims are 2, so
+    that shape falls back. With ``num_kv_heads`` the head axis must match it
+    (a token-major buffer, say, would otherwise be read with its axes swapped)."""
     if kv_cache.dim() == 4 and kv_cache.shape[-1] == 2 * head_size:
-        # [blocks, kv_heads, block_size, 2*D] -> two strided NHD views (reference: vllm_patch.py:121-122).
         k, v = kv_cache.transpose(1, 2).split(head_size, dim=-1)
-        return k, v
-    if kv_cache.dim() == 5 and kv_cache.shape[0] == 2 and kv_cache.shape[-1] == head_size:
-        return kv_cache[0], kv_cache[1]
-    return None
+    elif kv_cache.dim() == 5 and kv_cache.shape[-1] == head_size and 2 in kv_cache.shape[:2]:
+        if kv_cache.shape[0] == 2 and kv_cache.shape[1] == 2:
+            return None
+        k, v = (kv_cache[0], kv_cache[1]) if kv_cache.shape[0] == 2 else (kv_cache[:, 0], kv_cache[:, 1])
+    else:
+        return None
+    if num_kv_heads is not None and k.shape[2] != num_kv_heads:
+        return None
+    return k, v
 
 
 def _platform_fp8_is_e4m3fn() -> bool:
@@ -155,7 +169,8 @@ def _attention_eligible(impl, query, kv_cache, attn_metadata, output, output_sca
         return False
     if getattr(impl, "sinks", None) is not None:
         return False
-    if impl.head_size not in dk_ops.SUPPORTED_HEAD_DIMS:
+    fp8 = str(getattr(impl, "kv_cache_dtype", "auto")) not in ("auto", "float16", "bfloat16")
+    if impl.head_size not in (dk_ops.SUPPORTED_FP8_HEAD_DIMS if fp8 else dk_ops.SUPPORTED_HEAD_DIMS):
         return False
     if impl.num_heads % impl.num_kv_heads or impl.num_heads // impl.num_kv_heads > dk_ops.MAX_GQA_GROUP:
         return False
@@ -170,7 +185,7 @@ def _attention_eligible(impl, query, kv_cache, attn_metadata, output, output_sca
         return False
     if not output.is_contiguous():
         return False
-    if split_kv_cache(kv_cache, impl.head_size) is None:
+    if split_kv_cache(kv_cache, impl.head_size, impl.num_kv_heads) is None:
         return False
     return True
 
@@ -182,7 +197,7 @@ def _make_attention_forward(original):
             self, query, kv_cache, attn_metadata, output, output_scale, output_block_scale, layer
         ):
             n = attn_metadata.num_actual_tokens
-            key_cache, value_cache = split_kv_cache(kv_cache, self.head_size)
+            key_cache, value_cache = split_kv_cache(kv_cache, self.head_size, self.num_kv_heads)
             scales = {}
             fp8 = fp8_kv_scales(self, kv_cache, layer)
             if fp8 is not None:  # uint8 storage read as e4m3fn, in place

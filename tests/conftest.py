@@ -23,3 +23,31 @@ def pytest_collection_modifyitems(config, items):
     for item in items:
         if "gpu" in item.keywords:
             item.add_marker(skip)
+
+
+def pytest_terminal_summary(terminalreporter, exitstatus, config):
+    """Achieved max abs error of the parity checks that ran: the full-size
+    configurations one by one, and the checks closest to their bar."""
+    try:
+        from parity import ERRORS
+    except ImportError:
+        return
+    if not ERRORS:
+        return
+    import json
+    import os
+
+    path = os.environ.get("DK_PARITY_REPORT")
+    if path:
+        with open(path, "w") as f:
+            for rec in ERRORS:
+                f.write(json.dumps(rec) + "\n")
+    tr = terminalreporter
+    tr.section("parity: achieved max abs error (bar: max(2e-2 bf16 / 5e-3 fp16, half an ulp))")
+    full = [r for r in ERRORS if "test_full_size" in r["test"]]
+    for r in full:
+        tr.write_line(f"  {r['what']:<48} {r['dtype']:<9} max err {r['max_abs_err']:.3e}  "
+                      f"worst err/bar {r['worst_err_over_bar']:.3f}")
+    tr.write_line(f"  {len(ERRORS)} checks; closest to the bar:")
+    for r in sorted(ERRORS, key=lambda r: -r["worst_err_over_bar"])[:8]:
+        tr.write_line(f"  {r['worst_err_over_bar']:.3f}  {r['max_abs_err']:.3e} {r['dtype']:<9} {r['what']}  [{r['test']}]")

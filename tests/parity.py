@@ -2,16 +2,19 @@
 tolerances of the acceptance bar.
 
 * attention and GEMM: abs error against the *unrounded* fp32 oracle of at
-  most 2e-2 for bf16 and 5e-3 for fp16, plus half an ulp of the model dtype at
-  the reference value -- the final rounding to bf16/fp16 that the reference
-  itself performs (``.to(q.dtype)``), which alone exceeds 5e-3 once |out| >= 16
-  in fp16 (e.g. attention over outlier V rows). For |ref| < 1 the extra term is
-  at most 2.4e-4 (fp16) / 2e-3 (bf16);
+  most max(2e-2, half an ulp) for bf16 and max(5e-3, half an ulp) for fp16,
+  the ulp of the model dtype taken at the reference value. Half an ulp is the
+  final rounding to bf16/fp16 that the reference itself performs
+  (``.to(q.dtype)``); it exceeds 5e-3 only once |out| >= 16 in fp16 (attention
+  over outlier V rows), where a correctly rounded result may sit that far from
+  the fp32 value;
 * norms and activation: at most 1 ulp of the model dtype from the oracle's
   (rounded) output; the fused residual is bit-exact.
 """
 
 from __future__ import annotations
+
+import os
 
 import torch
 
@@ -24,6 +27,11 @@ from oracle.reference import (
 )
 
 MAX_ABS = {torch.bfloat16: 2e-2, torch.float16: 5e-3}
+
+# Every assert_max_abs call appends (what, dtype, max abs error, worst error / bar);
+# tests/conftest.py prints them at the end of the run and, when DK_PARITY_REPORT
+# names a file, writes them there as JSON lines.
+ERRORS: list[dict] = []
 
 
 def attention_f32(q, k_cache, v_cache, block_tables, seq_lens, scale=None) -> torch.Tensor:
@@ -43,18 +51,27 @@ def half_ulp(ref_f32: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
     return 0.5 * (torch.nextafter(a, torch.full_like(a, float("inf"))) - a).float()
 
 
+def bar(ref_f32: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
+    """Elementwise acceptance bar: max(MAX_ABS[dtype], half an ulp of dtype at |ref|)."""
+    return half_ulp(ref_f32, dtype).clamp(min=MAX_ABS[dtype])
+
+
 def assert_max_abs(got: torch.Tensor, ref_f32: torch.Tensor, dtype: torch.dtype, what: str = "") -> float:
-    """Asserts |got - ref| <= MAX_ABS[dtype] + half_ulp(ref) elementwise; returns the max abs error."""
+    """Asserts |got - ref| <= max(MAX_ABS[dtype], half_ulp(ref)) elementwise; returns the max abs error."""
     assert torch.isfinite(got).all(), f"{what} non-finite output"
     if got.numel() == 0:
         return 0.0
     ref = ref_f32.float().cpu()
     diff = (got.float().cpu() - ref).abs()
-    excess = diff - (MAX_ABS[dtype] + half_ulp(ref, dtype))
-    worst = int(excess.argmax())
-    assert excess.max().item() <= 0, (
+    tol = bar(ref, dtype)
+    ratio = diff / tol
+    worst = int(ratio.argmax())
+    ERRORS.append({"what": what or "(unnamed)", "dtype": str(dtype).replace("torch.", ""),
+                   "max_abs_err": diff.max().item(), "worst_err_over_bar": ratio.flatten()[worst].item(),
+                   "test": os.environ.get("PYTEST_CURRENT_TEST", "").split(" ")[0]})
+    assert ratio.flatten()[worst].item() <= 1.0, (
         f"{what} abs error {diff.flatten()[worst].item():.3e} at |ref| = {ref.flatten()[worst].abs().item():.3g} "
-        f"exceeds {MAX_ABS[dtype]:.0e} + half an ulp ({dtype})"
+        f"exceeds max({MAX_ABS[dtype]:.0e}, half an ulp) = {tol.flatten()[worst].item():.3e} ({dtype})"
     )
     return diff.max().item()
 
@@ -78,7 +95,9 @@ def assert_ulp(got: torch.Tensor, ref: torch.Tensor, max_ulp: int = 1, what: str
 
 
 __all__ = [
+    "ERRORS",
     "MAX_ABS",
+    "bar",
     "assert_max_abs",
     "assert_ulp",
     "attention_f32",

@@ -81,6 +81,52 @@ def test_fp8_long_contexts_both_schedules(dtype, schedule, monkeypatch):
     _check(_q(len(lens), 32, 128, dtype, seed=3), kv, 0.031, 0.25, dtype)
 
 
+@pytest.mark.parametrize("schedule", ["grid", "balanced"])
+def test_fp8_128k_batch_1(schedule, monkeypatch):
+    """The long-context split-K shape with an fp8 cache: one 131072-token
+    sequence, 32 query / 8 KV heads, head_dim 128, HND cache, 1% of rows
+    scaled up (to 8x the others before the fp8 rounding), bf16 queries. Under
+    the balanced schedule each KV stream spans more than 64 workspace rows."""
+    monkeypatch.setenv("DK_ATTN_SCHEDULE", schedule)
+    L = 131072
+    kv = make_paged_kv([L], 8, 128, 16, FP8, "cuda", layout="hnd", seed=17)
+    g = torch.Generator(device="cuda").manual_seed(18)
+    rows = torch.rand(kv.k_cache.shape[0], 16, 8, 1, generator=g, device="cuda") < 0.01
+    big = torch.where(rows, 8.0, 1.0)
+    kv.k_cache.copy_((kv.k_cache.float() * big).to(FP8))
+    kv.v_cache.copy_((kv.v_cache.float() * big).to(FP8))
+    q = _q(1, 32, 128, torch.bfloat16, seed=19) * 128**-0.5
+    ws = dk.alloc_workspace(1, 32, 128, L, "cuda")
+    for t in ws:
+        t.fill_(float("nan"))
+    out = dk.paged_attention_decode(q, kv.k_cache, kv.v_cache, kv.block_tables, kv.seq_lens, max_seq_len=L,
+                                    workspace=ws, k_scale=0.5, v_scale=0.5)
+    torch.cuda.synchronize()
+    ref = attention_f32(q, kv.k_cache.float() * 0.5, kv.v_cache.float() * 0.5, kv.block_tables, kv.seq_lens)
+    assert_max_abs(out, ref, torch.bfloat16, f"fp8 cache, 128K batch 1 ({schedule})")
+    if schedule == "balanced":
+        es = ws[2].cpu()
+        filled = ~torch.isnan(es) & (es != 0)
+        rows_used = int(torch.cumprod(filled.to(torch.int32), dim=-1).sum(dim=-1).max())
+        assert rows_used > 64, f"the longest stream spans {rows_used} rows"
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("hq,hkv,head_dim", [(28, 4, 128), (14, 2, 64), (6, 2, 128), (10, 2, 64), (12, 2, 256)])
+@pytest.mark.parametrize("schedule", ["grid", "balanced"])
+def test_fp8_odd_gqa_groups(dtype, hq, hkv, head_dim, schedule, monkeypatch):
+    """GQA groups 3, 5, 6 and 7 (Qwen2.5-7B: 28 / 4, Qwen2.5-0.5B: 14 / 2) over an
+    fp8 cache, single pass and split-K."""
+    monkeypatch.setenv("DK_ATTN_SCHEDULE", schedule)
+    lens = [1, 100, 512, 0, 37, 4000, 513, 9000]
+    kv = make_paged_kv(lens, hkv, head_dim, 16, FP8, "cuda", layout="vllm", seed=hq + head_dim)
+    out = _check(_q(len(lens), hq, head_dim, dtype, seed=hq), kv, 0.2, 0.7, dtype)
+    assert (out[3] == 0).all()
+    short = [1, 100, 512, 0]
+    kv_s = make_paged_kv(short, hkv, head_dim, 16, FP8, "cuda", layout="hnd", seed=hq + 1)
+    _check(_q(len(short), hq, head_dim, dtype, seed=hq + 1), kv_s, 0.2, 0.7, dtype)
+
+
 @pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("split", [False, True])
 def test_fp8_equals_16bit_path_on_the_converted_cache(dtype, split):

@@ -63,12 +63,90 @@ def test_paged_attention_short(dtype, head_dim, group, block_size):
 
 @pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("head_dim", [64, 128])
-@pytest.mark.parametrize("group", [1, 8])
+@pytest.mark.parametrize("group", [1, 4, 8])
 def test_paged_attention_split_k(dtype, head_dim, group):
     """Split-K: partition boundaries and sequences much shorter than the maximum."""
     seq_lens = [1, 511, 512, 513, 1024, 1025, 3000, 8192]
     kv = make_paged_kv(seq_lens, 2, head_dim, 16, dtype, "cuda")
     _check_attention(_q(len(seq_lens), 2 * group, head_dim, dtype), kv, dtype)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("schedule", ["auto", "grid", "balanced"])
+def test_paged_attention_c1_shape(dtype, schedule, monkeypatch):
+    """BASELINE configs[0] on the HIP path: 4 sequences of {1, 511, 512, 513}
+    tokens, 8 query / 2 KV heads, head_dim 128, block 16, NHD cache of 160
+    physical blocks (98 used + extra_blocks=62), split-K (max_seq_len 513)."""
+    if schedule != "auto":
+        monkeypatch.setenv("DK_ATTN_SCHEDULE", schedule)
+    lens = [1, 511, 512, 513]
+    kv = make_paged_kv(lens, 2, 128, 16, dtype, "cuda", layout="nhd", extra_blocks=62, seed=0)
+    assert kv.k_cache.shape[0] == 160
+    q = _q(4, 8, 128, dtype)
+    out = _check_attention(q, kv, dtype, max_seq_len=513)
+    ws = dk.alloc_workspace(4, 8, 128, 513, "cuda")
+    assert ws[0].shape == (4, 8, 2, 128)
+    again = dk.paged_attention_decode(q, kv.k_cache, kv.v_cache, kv.block_tables, kv.seq_lens, max_seq_len=513,
+                                      workspace=ws)
+    assert torch.equal(out, again)
+
+
+def _workspace_rows(exp_sums: torch.Tensor) -> torch.Tensor:
+    """Rows a balanced-schedule call filled per (sequence, query head): the
+    workspace starts as NaN, pieces fill rows 0 .. n-1 and the stream's last
+    piece marks row n empty (exp-sum 0) when n < max_partitions."""
+    es = exp_sums.cpu()
+    filled = ~torch.isnan(es) & (es != 0)
+    # rows before the first unfilled one
+    return torch.cumprod(filled.to(torch.int32), dim=-1).sum(dim=-1)
+
+
+@pytest.mark.parametrize("seq_len,min_rows", [(140000, 64), (270000, 128)])
+@pytest.mark.parametrize("schedule", ["grid", "balanced"])
+def test_paged_attention_reduce_many_rows(seq_len, min_rows, schedule, monkeypatch):
+    """One KV head of one long sequence: under the balanced schedule the stream
+    is cut into one piece per workgroup share, so the reduce merges more than
+    64 (140K tokens) and more than 128 (270K tokens) workspace rows per query
+    head -- its second and third lane-parallel passes over the exp-sums. The
+    grid schedule merges ceil(L / 1024) + 1 rows. Both against the oracle."""
+    monkeypatch.setenv("DK_ATTN_SCHEDULE", schedule)
+    dtype = torch.bfloat16
+    kv = make_paged_kv([seq_len], 1, 128, 16, dtype, "cuda", layout="nhd", seed=seq_len % 1000)
+    q = _q(1, 4, 128, dtype, seed=3)
+    ws = dk.alloc_workspace(1, 4, 128, seq_len, "cuda")
+    for t in ws:
+        t.fill_(float("nan"))
+    out = dk.paged_attention_decode(q, kv.k_cache, kv.v_cache, kv.block_tables, kv.seq_lens, max_seq_len=seq_len,
+                                    workspace=ws)
+    torch.cuda.synchronize()
+    assert_max_abs(out, attention_f32(q, kv.k_cache, kv.v_cache, kv.block_tables, kv.seq_lens), dtype,
+                   f"{seq_len} tokens, one KV head ({schedule})")
+    if schedule == "balanced":
+        rows = _workspace_rows(ws[2])
+        assert (rows == rows[0, 0]).all(), "every query head of a stream uses the same rows"
+        assert int(rows[0, 0]) > min_rows, f"the stream spans {int(rows[0, 0])} rows, expected > {min_rows}"
+        assert int(rows[0, 0]) <= ws[2].shape[-1]
+
+
+# Qwen2.5-7B (28 query / 4 KV heads, group 7, head_dim 128), Qwen2.5-0.5B
+# (14 / 2, group 7, head_dim 64) and groups 3, 5 and 6.
+ODD_GROUP_CASES = [(28, 4, 128), (14, 2, 64), (6, 2, 128), (10, 2, 64), (12, 2, 256), (21, 3, 96)]
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("hq,hkv,head_dim", ODD_GROUP_CASES, ids=lambda v: str(v))
+@pytest.mark.parametrize("schedule", ["grid", "balanced"])
+def test_paged_attention_odd_gqa_groups(dtype, hq, hkv, head_dim, schedule, monkeypatch):
+    """GQA groups that are not powers of two (the reference's benchmark models,
+    benchmarks/bench_kernels.py:38-42), single pass and split-K."""
+    monkeypatch.setenv("DK_ATTN_SCHEDULE", schedule)
+    short = [1, 100, 512, 0, 37]
+    kv = make_paged_kv(short, hkv, head_dim, 16, dtype, "cuda", layout="vllm", seed=hq)
+    out = _check_attention(_q(len(short), hq, head_dim, dtype, seed=hq), kv, dtype)
+    assert (out[3] == 0).all()
+    lens = _log_uniform_lens(20, 9000, seed=hq + head_dim, zeros=2)
+    kv = make_paged_kv(lens, hkv, head_dim, 16, dtype, "cuda", layout="hnd", seed=hq + 1)
+    _check_attention(_q(len(lens), hq, head_dim, dtype, seed=hq + 2), kv, dtype, max_seq_len=9000)
 
 
 @pytest.mark.parametrize("dtype", DTYPES)

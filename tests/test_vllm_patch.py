@@ -13,6 +13,7 @@ from types import SimpleNamespace
 import pytest
 import torch
 
+import fake_vllm as fake_vllm_modules
 from decodekernels_amd import ops as dk_ops
 from decodekernels_amd import vllm_patch, vllm_plugin
 from decodekernels_amd.testing import make_paged_kv
@@ -52,9 +53,24 @@ def test_split_kv_cache_layouts():
     assert torch.equal(k, kv.k_cache) and torch.equal(v, kv.v_cache)
     assert k.stride() == kv.k_cache.stride()
     stacked = torch.randn(2, 7, BS, HKV, D)
-    k2, v2 = vllm_patch.split_kv_cache(stacked, D)
+    k2, v2 = vllm_patch.split_kv_cache(stacked, D, HKV)
     assert torch.equal(k2, stacked[0]) and torch.equal(v2, stacked[1])
+    block_major = torch.randn(7, 2, BS, HKV, D)  # vLLM's Triton backend
+    k3, v3 = vllm_patch.split_kv_cache(block_major, D, HKV)
+    assert torch.equal(k3, block_major[:, 0]) and torch.equal(v3, block_major[:, 1])
     assert vllm_patch.split_kv_cache(torch.randn(7, BS * HKV * D), D) is None
+
+
+def test_split_kv_cache_rejects_ambiguous_and_mismatched_layouts():
+    # [2, 2, ...]: a stacked pair of 2 blocks or 2 blocks of a block-major pair
+    assert vllm_patch.split_kv_cache(torch.randn(2, 2, BS, HKV, D), D, HKV) is None
+    # a token-major interleaved buffer [blocks, block_size, kv_heads, 2*D] would
+    # be read with block_size as the head axis
+    assert vllm_patch.split_kv_cache(torch.randn(10, BS, HKV, 2 * D), D, HKV) is None
+    assert vllm_patch.split_kv_cache(torch.randn(2, 7, BS, HKV + 1, D), D, HKV) is None
+    q, _, meta, out = _inputs()
+    token_major = torch.randn(10, BS, HKV, 2 * D, dtype=q.dtype)
+    assert not vllm_patch._attention_eligible(_impl(), q, token_major, meta, out, None, None)
 
 
 def test_attention_eligible_base_case():
@@ -139,6 +155,23 @@ def test_fp8_cache_eligible_on_e4m3fn_platform(monkeypatch):
     assert vllm_patch._attention_eligible(_impl(kv_cache_dtype="fp8_e4m3"), q, kv8, meta, out, None, None, layer)
 
 
+def test_fp8_cache_head_dim_96_falls_back(monkeypatch):
+    """head_dim 96 runs with a 16-bit cache but not an fp8 one (its rows load
+    64 columns per lane group): the fp8 call must fall back, not raise."""
+    _platform(monkeypatch, torch.float8_e4m3fn)
+    d = 96
+    kv = torch.randn(10, HKV, BS, 2 * d).to(torch.float8_e4m3fn)
+    q = torch.randn(3, HQ * d, dtype=torch.float16)
+    out = torch.zeros_like(q)
+    meta = SimpleNamespace(max_query_len=1, num_actual_tokens=3, seq_lens=torch.tensor([5] * 3, dtype=torch.int32),
+                           block_table=torch.zeros(3, 2, dtype=torch.int32), max_seq_len=5, causal=True)
+    layer = SimpleNamespace(_k_scale_float=0.5, _v_scale_float=2.0)
+    assert not vllm_patch._attention_eligible(_impl(kv_cache_dtype="fp8", head_size=d, scale=d**-0.5), q, kv, meta,
+                                              out, None, None, layer)
+    kv16 = torch.randn(10, HKV, BS, 2 * d, dtype=torch.float16)
+    assert vllm_patch._attention_eligible(_impl(head_size=d, scale=d**-0.5), q, kv16, meta, out, None, None)
+
+
 @pytest.mark.parametrize("case", ["fnuz_platform", "no_platform", "no_scales", "tensor_scales", "zero_scale", "e5m2",
                                   "fnuz_tensor", "auto_with_uint8"])
 def test_fp8_cache_fallbacks(monkeypatch, case):
@@ -171,50 +204,16 @@ def test_fp8_cache_fallbacks(monkeypatch, case):
 # ---------------------------------------------------------------------------
 @pytest.fixture
 def fake_vllm(monkeypatch):
-    calls = []
-
-    def module(name, **attrs):
-        m = types.ModuleType(name)
-        for k, v in attrs.items():
-            setattr(m, k, v)
-        monkeypatch.setitem(sys.modules, name, m)
-        return m
-
-    class FlashAttentionImpl:
-        def forward(self, layer, query, key, value, kv_cache, attn_metadata, output, output_scale=None,
-                    output_block_scale=None):
-            calls.append("vllm_attention")
-            return output
-
-    class RMSNorm:
-        def forward_cuda(self, x, residual=None):
-            calls.append("vllm_rms_norm")
-            return x
-
-    class SiluAndMul:
-        def forward_cuda(self, x):
-            calls.append("vllm_silu")
-            return x
-
-    for name in ("vllm", "vllm.v1", "vllm.v1.attention", "vllm.v1.attention.backends", "vllm.model_executor",
-                 "vllm.model_executor.layers"):
-        module(name)
-    module("vllm.v1.attention.backends.flash_attn", FlashAttentionImpl=FlashAttentionImpl)
-    module("vllm.envs", VLLM_BATCH_INVARIANT=False)
-    module("vllm.model_executor.layers.layernorm", RMSNorm=RMSNorm)
-    module("vllm.model_executor.layers.activation", SiluAndMul=SiluAndMul)
-
+    """Fake vLLM modules with the decode ops replaced by recorders (the GPU
+    counterpart, tests/test_vllm_patch_gpu.py, keeps the real ops)."""
+    fake = fake_vllm_modules.install(monkeypatch)
+    calls = fake.calls
     monkeypatch.setattr(dk_ops, "is_available", lambda: True)
     monkeypatch.setattr(dk_ops, "paged_attention_decode", lambda *a, **k: calls.append(("dk_attention", a, k)))
     monkeypatch.setattr(dk_ops, "rms_norm", lambda *a: calls.append("dk_rms_norm"))
     monkeypatch.setattr(dk_ops, "fused_add_rms_norm", lambda *a: calls.append("dk_fused_add"))
     monkeypatch.setattr(dk_ops, "silu_and_mul", lambda *a: calls.append("dk_silu"))
-    # Patching replaces class attributes: restore them after the test.
-    for cls in (FlashAttentionImpl, RMSNorm, SiluAndMul):
-        for attr in ("forward", "forward_cuda"):
-            if attr in vars(cls):
-                monkeypatch.setattr(cls, attr, vars(cls)[attr])
-    return SimpleNamespace(calls=calls, FlashAttentionImpl=FlashAttentionImpl, RMSNorm=RMSNorm, SiluAndMul=SiluAndMul)
+    return fake
 
 
 def test_attention_patch_routes_decode_batches(fake_vllm):
