@@ -121,6 +121,10 @@ _SIGNATURES = {
         [ctypes.POINTER(PagedAttnParams), ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_float, ctypes.c_float]
         + [ctypes.c_void_p],
     ),
+    "dk_paged_attention_decode_noalloc": (
+        ctypes.c_int,
+        [ctypes.POINTER(PagedAttnParams), ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p],
+    ),
     "dk_gemm_tn": (
         ctypes.c_int,
         [ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p]

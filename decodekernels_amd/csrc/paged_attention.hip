@@ -1316,12 +1316,84 @@ int paged_attention_entry(const dk_paged_attn_params* a, int dtype, int head_dim
   return static_cast<int>(e);
 }
 
+// Split-K workspace of the allocation-free entry point: one array per GPU,
+// held by every device the library runs on until the process ends, shared
+// by all calls on that device (overlapping calls on one GPU race). Nothing in
+// it has to start at zero: the kernels read only rows written by the same call.
+static __device__ __align__(256) unsigned char scratch[DK_NOALLOC_SCRATCH_BYTES];
+
+// Device address of this device's `scratch` (host code must not use the
+// array's name, a host-side stand-in): looked up with hipGetSymbolAddress on
+// the first call on each device, with that device current, then cached.
+void* scratch_address(int* err) {
+  static std::atomic<void*> addr[kMaxDevices];
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) {
+    *err = static_cast<int>(e);
+    return nullptr;
+  }
+  if (dev < 0 || dev >= kMaxDevices) {
+    *err = fail("paged_attention_decode_noalloc: device %d is beyond the %d devices supported", dev, kMaxDevices);
+    return nullptr;
+  }
+  void* p = addr[dev].load(std::memory_order_acquire);
+  if (p == nullptr) {
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr) {
+      *err = e != hipSuccess ? static_cast<int>(e) : static_cast<int>(hipErrorInvalidSymbol);
+      return nullptr;
+    }
+    addr[dev].store(p, std::memory_order_release);  // every thread finds the same address
+  }
+  return p;
+}
+
+int paged_attention_noalloc(const dk_paged_attn_params* a, int dtype, int head_dim, int max_seq_len, void* stream) {
+  clear_error();
+  if (a == nullptr) return fail("paged_attention_decode_noalloc: params must not be NULL");
+  if (a->num_seqs <= 0 || max_seq_len <= kPart) {
+    // No split-K: nothing goes through the workspace.
+    dk_paged_attn_params b = *a;
+    b.tmp_out = b.max_logits = b.exp_sums = nullptr;
+    b.max_partitions = 0;
+    return paged_attention_entry(&b, dtype, head_dim, max_seq_len, false, 1.0f, 1.0f, stream);
+  }
+  if (a->num_q_heads <= 0 || head_dim <= 0) return paged_attention_entry(a, dtype, head_dim, max_seq_len, false, 1.0f, 1.0f, stream);
+  // Workspace of the reference's shape in the scratch array, each part 256-byte aligned:
+  // tmp_out [S, Hq, P, D], then max_logits and exp_sums [S, Hq, P], all fp32.
+  const int64_t parts = ceil_div64(max_seq_len, kPart);
+  const int64_t rows = static_cast<int64_t>(a->num_seqs) * a->num_q_heads * parts;
+  auto up256 = [](int64_t b) { return (b + 255) / 256 * 256; };
+  const int64_t tmp_bytes = up256(rows * head_dim * 4);
+  const int64_t vec_bytes = up256(rows * 4);
+  const int64_t need = tmp_bytes + 2 * vec_bytes;
+  if (need > static_cast<int64_t>(DK_NOALLOC_SCRATCH_BYTES))
+    return fail("paged_attention_decode_noalloc: the split-K workspace needs %lld bytes (num_seqs x num_q_heads x "
+                "ceil(max_seq_len / 512) x (head_dim + 2) x 4), more than the %lld-byte scratch",
+                static_cast<long long>(need), static_cast<long long>(DK_NOALLOC_SCRATCH_BYTES));
+  int err = 0;
+  unsigned char* base = static_cast<unsigned char*>(scratch_address(&err));
+  if (base == nullptr) return err;
+  dk_paged_attn_params b = *a;
+  b.tmp_out = reinterpret_cast<float*>(base);
+  b.max_logits = reinterpret_cast<float*>(base + tmp_bytes);
+  b.exp_sums = reinterpret_cast<float*>(base + tmp_bytes + vec_bytes);
+  b.max_partitions = static_cast<int32_t>(parts);
+  return paged_attention_entry(&b, dtype, head_dim, max_seq_len, false, 1.0f, 1.0f, stream);
+}
+
 }  // namespace attn
 }  // namespace dk
 
 extern "C" int dk_paged_attention_decode(const dk_paged_attn_params* a, int dtype, int head_dim, int max_seq_len,
                                          void* stream) {
   return dk::attn::paged_attention_entry(a, dtype, head_dim, max_seq_len, false, 1.0f, 1.0f, stream);
+}
+
+extern "C" int dk_paged_attention_decode_noalloc(const dk_paged_attn_params* a, int dtype, int head_dim,
+                                                 int max_seq_len, void* stream) {
+  return dk::attn::paged_attention_noalloc(a, dtype, head_dim, max_seq_len, stream);
 }
 
 extern "C" int dk_paged_attention_decode_fp8(const dk_paged_attn_params* a, int dtype, int head_dim, int max_seq_len,

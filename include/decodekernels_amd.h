@@ -98,6 +98,30 @@ int dk_paged_attention_decode(const dk_paged_attn_params* p, int dtype, int head
 int dk_paged_attention_decode_fp8(const dk_paged_attn_params* p, int dtype, int head_dim, int max_seq_len,
                                   float k_scale, float v_scale, void* stream);
 
+/* Size of the device array that dk_paged_attention_decode_noalloc uses as its
+ * split-K workspace (64 MiB per GPU the library runs on). */
+#define DK_NOALLOC_SCRATCH_BYTES 67108864
+
+/*
+ * dk_paged_attention_decode without a caller-provided workspace: the split-K
+ * partial results go to a library-owned, statically allocated device array of
+ * DK_NOALLOC_SCRATCH_BYTES per GPU instead of p->tmp_out / max_logits /
+ * exp_sums (those fields and p->max_partitions are ignored). Same kernels, so
+ * the same results bit for bit. It allocates nothing (no hipMalloc, no
+ * allocating library call); the array's address is looked up once per device
+ * on the first call there. The workspace needs
+ * num_seqs * num_q_heads * ceil(max_seq_len / 512) * (head_dim + 2) * 4 bytes
+ * (each of its three parts rounded up to 256); larger calls fail with
+ * hipErrorInvalidValue and a dk_last_error() message. Every call on one GPU
+ * shares that GPU's array: calls that overlap in time on one GPU (different
+ * streams, concurrent graph replays) race and must not be issued.
+ * No counterpart in DecodeKernels: it is for callers that cannot allocate
+ * device memory at all -- code under HIP-graph capture, tight serving loops,
+ * harnesses that forbid allocation.
+ */
+int dk_paged_attention_decode_noalloc(const dk_paged_attn_params* p, int dtype, int head_dim, int max_seq_len,
+                                      void* stream);
+
 /*
  * C[M,N] = A[M,K] * B[N,K]^T (+ bias[N]), fp32 accumulation, one rounding.
  * Replaces dk::launch_gemm_tn<T> (csrc/gemm_wmma.cuh:209-219).
