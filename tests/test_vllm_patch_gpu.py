@@ -29,7 +29,7 @@ from oracle.reference import silu_and_mul_reference
 
 pytestmark = pytest.mark.gpu
 
-NB, BS = 64, 16
+NB, BS = 160, 16
 
 
 @pytest.fixture
