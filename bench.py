@@ -584,6 +584,26 @@ def pmc_workload_attention_fp8(calls: int = 3) -> None:
     print(f"pmc fp8 attention workload done: {calls} calls each with a bf16 and an fp8 cache", flush=True)
 
 
+def pmc_workload_attention_cold(calls: int = 3) -> None:
+    """What the cold-cache attention profiles cover: the headline batch, then the
+    128K-token batch-1 and batch-4 cases (fp16, HND, 1% outlier rows), `calls`
+    times each, every call after a 1 GiB cache flush (the flush is its own
+    kernel, `amax`)."""
+    lens = torch.randint(512, 4097, (64,), generator=torch.Generator().manual_seed(0)).tolist()
+    cases = (("llama3_8b_b64", (64, 32, 8, 128, 16, lens, torch.bfloat16, "vllm"), dict(seed=0, q_scale=128**-0.5)),
+             ("128k_b1", (1, 32, 8, 128, 16, [131072], torch.float16, "hnd"), dict(seed=11, outlier_frac=0.01)),
+             ("128k_b4", (4, 32, 8, 128, 16, [131072] * 4, torch.float16, "hnd"), dict(seed=14, outlier_frac=0.01)))
+    for name, args, kw in cases:
+        c = attention_case(*args, **kw)
+        for _ in range(calls):
+            flush_caches()
+            c["run"]()
+        torch.cuda.synchronize()
+        print(f"pmc cold attention workload: {calls} calls of {name}", flush=True)
+        del c
+        torch.cuda.empty_cache()
+
+
 def pmc_workload(calls: int = 5) -> None:
     """What the counter runs profile: the headline op `calls` times, then a
     copy of CALIBRATION_BYTES (read once, written once) to scale the counters."""
@@ -628,7 +648,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-extras", action="store_true", help="skip the secondary configs")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline (and its correctness check)")
-    ap.add_argument("--pmc-workload", nargs="?", const="attention", choices=["attention", "attention_fp8", "gemm", "gemm_skinny"],
+    ap.add_argument("--pmc-workload", nargs="?", const="attention",
+                    choices=["attention", "attention_cold", "attention_fp8", "gemm", "gemm_skinny"],
                     help="run only what the rocprofv3 --pmc passes profile (default: attention)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -637,6 +658,9 @@ def main() -> int:
         return 2
     if not dk.is_available():
         raise RuntimeError("decodekernels_amd HIP extension not available (build it with __graft_entry__.build())")
+    if args.pmc_workload == "attention_cold":
+        pmc_workload_attention_cold()
+        return 0
     if args.pmc_workload == "attention_fp8":
         pmc_workload_attention_fp8()
         return 0

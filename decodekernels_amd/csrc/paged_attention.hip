@@ -79,7 +79,13 @@ constexpr int kUnit = 2 * kPart;          // split-K work unit: two slots (its b
 #define DK_ATTN_OCC_FP8_D256 1  // waves per SIMD targeted at head_dim 256 with an fp8 cache
 #endif
 #ifndef DK_ATTN_LOAD_AUX
-#define DK_ATTN_LOAD_AUX 0  // cache-policy bits of the K/V buffer loads
+#define DK_ATTN_LOAD_AUX 0  // cache-policy bits of the K/V buffer loads in the MFMA-operand layout
+#endif
+#ifndef DK_ATTN_ROWLOAD
+#define DK_ATTN_ROWLOAD 1  // 16-bit caches: K and V tiles load row-contiguous (whole 128-byte lines) through LDS
+#endif
+#ifndef DK_ATTN_ROW_AUX
+#define DK_ATTN_ROW_AUX 2  // cache-policy bits of the row-contiguous K/V loads (2 = nt, non-temporal)
 #endif
 #ifndef DK_ATTN_OCC_D128
 #define DK_ATTN_OCC_D128 2  // waves per SIMD targeted at head_dim 128
@@ -124,9 +130,8 @@ constexpr int kRsrcWord3 = 0x00020000;
 
 // Raw buffer loads of 8 / 4 consecutive 16-bit elements at byte offset `off`
 // of the resource; the resource's num_records bounds the access (0 = none).
-template <int ALIGN>
+template <int ALIGN, int A = DK_ATTN_LOAD_AUX>
 __device__ __forceinline__ u32x4 bload8(__amdgpu_buffer_rsrc_t r, int off) {
-  constexpr int A = DK_ATTN_LOAD_AUX;
   if constexpr (ALIGN >= 16) {
     return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, A);
   } else if constexpr (ALIGN == 8) {
@@ -140,9 +145,8 @@ __device__ __forceinline__ u32x4 bload8(__amdgpu_buffer_rsrc_t r, int off) {
 }
 
 // Raw buffer load of 16 bytes at byte offset `off`, aligned to ALIGN (16 or 8).
-template <int ALIGN>
+template <int ALIGN, int A = DK_ATTN_LOAD_AUX>
 __device__ __forceinline__ u32x4 bload16b(__amdgpu_buffer_rsrc_t r, int off) {
-  constexpr int A = DK_ATTN_LOAD_AUX;
   if constexpr (ALIGN >= 16) {
     return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, A);
   } else {
@@ -225,16 +229,44 @@ constexpr int vt_pitch() {
   return D + 16;
 }
 
-template <int D, int NW>
+// Row-contiguous tile loads (whole 128-byte lines per load instruction, K
+// brought into the MFMA layout through LDS) apply when a 16-token tile lies
+// inside one cache block.
+template <bool BS16, bool KV8>
+constexpr bool row_load() {
+  return DK_ATTN_ROWLOAD && BS16 && !KV8;
+}
+
+template <int D, int NW, bool ROW = false>
 struct UnitSmem {
-  float m[NW][16];              // reference max per head (log2 units)
-  float t[NW][16];              // true max per head
-  float l[NW][16];              // exp-sum against the reference max
-  float o[NW][kMergeHeads][D];  // partial outputs of one merge pass
-#if DK_ATTN_VTR
-  uint16_t vt[NW][16 * vt_pitch<D>()];  // each wave's current V tile (model dtype)
-#endif
+  float m[NW][16];  // reference max per head (log2 units)
+  float t[NW][16];  // true max per head
+  float l[NW][16];  // exp-sum against the reference max
+  // A wave's current tiles (model dtype), 16-byte aligned rows.
+  struct __attribute__((aligned(16))) Tiles {
+    uint16_t vt[DK_ATTN_VTR ? 16 * vt_pitch<D>() : 1];  // V tile
+    uint16_t kt[ROW ? 16 * vt_pitch<D>() : 1];          // K tile (row loads)
+  };
+  // At head_dim 64 a wave's partial outputs of a merge pass share its region
+  // with its tiles, which keeps four workgroups per CU: a wave writes its
+  // outputs only after its last tile's LDS reads were issued (LDS operations
+  // of one wave complete in order) and the merge ends with a barrier before
+  // any wave writes tiles again. Larger head dims keep them apart (two
+  // workgroups per CU either way).
+  struct __attribute__((aligned(16))) Shared {
+    union {
+      float o[kMergeHeads][D];
+      Tiles tile;
+    };
+  };
+  struct __attribute__((aligned(16))) Separate {
+    float o[kMergeHeads][D];
+    Tiles tile;
+  };
+  typename std::conditional<(D <= 64), Shared, Separate>::type w[NW];
 };
+static_assert(sizeof(UnitSmem<96, 4, false>::Tiles) % 16 == 0 && sizeof(UnitSmem<64, 4, true>::Shared) % 16 == 0,
+              "tile rows must stay 16-byte aligned in every wave's region");
 
 // A work unit: tokens [start, end) of sequence `seq` (end > start, at most
 // 1024 tokens) for KV head `kv_head` and its query-head group. Split-K writes
@@ -268,10 +300,14 @@ struct UnitEngine {
   static constexpr int NB = D / 16;  // 16-column output blocks
   static constexpr int DEPTH = KV8 ? DK_ATTN_DEPTH_FP8 : (D > 128 ? DK_ATTN_DEPTH_D256 : DK_ATTN_DEPTH);
   static constexpr int NT = NW * kWave;
+  static constexpr bool ROW = row_load<BS16, KV8>();
+  static constexpr int RB = KV8 ? D : 2 * D;     // bytes of one K (or V) row
+  static constexpr int NI = 16 * RB / 1024;      // row-contiguous 1 KB loads per K (or V) tile
+  static_assert(!ROW || DK_ATTN_VTR, "row loads bring V into LDS for the transpose read");
   using Tile = TileRegs<CH, KV8>;
 
   const KParams& p;
-  UnitSmem<D, NW>& sm;
+  UnitSmem<D, NW, ROW>& sm;
   int tid, lane, wave, l16, lg;
   u32x4 eye0, eye1;  // identity fragments (see process)
   u32x4 qf[CH];      // query fragments of the current unit
@@ -281,7 +317,7 @@ struct UnitEngine {
   float m_true;  // exact running max of head l16
   float l_run;   // this lane's share of the exp-sum against m_ref
 
-  __device__ __forceinline__ UnitEngine(const KParams& params, UnitSmem<D, NW>& smem) : p(params), sm(smem) {
+  __device__ __forceinline__ UnitEngine(const KParams& params, UnitSmem<D, NW, ROW>& smem) : p(params), sm(smem) {
     tid = threadIdx.x;
     lane = tid % kWave;
     wave = __builtin_amdgcn_readfirstlane(tid / kWave);
@@ -325,7 +361,7 @@ struct UnitEngine {
   // in the model dtype; heads past the group are zero.
   // First column of this lane's 8 columns of MFMA chunk c.
   __device__ __forceinline__ int chunk_col(int c) const {
-    return KV8 ? 64 * (c / 2) + 16 * lg + 8 * (c % 2) : 32 * c + 8 * lg;
+    return KV8 && !ROW ? 64 * (c / 2) + 16 * lg + 8 * (c % 2) : 32 * c + 8 * lg;
   }
 
   __device__ __forceinline__ void load_q(const Unit& u) {
@@ -368,7 +404,29 @@ struct UnitEngine {
       const int nrec = live ? 0x7fffffff : 0;
       const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(const_cast<KvT*>(kt), 0, nrec, kRsrcWord3);
       const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(const_cast<KvT*>(vt), 0, nrec, kRsrcWord3);
-      if constexpr (KV8) {
+      if constexpr (ROW) {
+        // Load j covers bytes [1024 j, 1024 j + 1024) of the tile's rows laid
+        // end to end: lane l reads 16 bytes of row (1024 j + 16 l) / RB, so
+        // every instruction reads whole lines of consecutive rows. Rows past
+        // the sequence end re-read its last row.
+        const int last = u.end - 1 - t0;
+        const int kst = kElt * static_cast<int>(p.k_st);
+        const int vst = kElt * static_cast<int>(p.v_st);
+#pragma unroll
+        for (int j = 0; j < NI; ++j) {
+          const int o = 1024 * j + 16 * lane;
+          const int rr = min(o / RB, last);
+          if constexpr (KV8) r.k[j] = bload16b<ALIGN, DK_ATTN_ROW_AUX>(rk, rr * kst + o % RB);
+          else r.k[j] = bload8<ALIGN, DK_ATTN_ROW_AUX>(rk, rr * kst + o % RB);
+        }
+#pragma unroll
+        for (int j = 0; j < NI; ++j) {
+          const int o = 1024 * j + 16 * lane;
+          const int rr = min(o / RB, last);
+          if constexpr (KV8) r.v[j] = bload16b<ALIGN, DK_ATTN_ROW_AUX>(rv, rr * vst + o % RB);
+          else r.v[j] = bload8<ALIGN, DK_ATTN_ROW_AUX>(rv, rr * vst + o % RB);
+        }
+      } else if constexpr (KV8) {
         const int koff = row * static_cast<int>(p.k_st) + 16 * lg;
         const int voff = row * static_cast<int>(p.v_st) + 16 * lg;
 #pragma unroll
@@ -431,8 +489,36 @@ struct UnitEngine {
   __device__ __forceinline__ void process(const Unit& u, int tile, const Tile& r) {
     // Q·Kᵀ: S[token 4*lg + i][head l16].
     f32x4 s = {0.f, 0.f, 0.f, 0.f};
+    if constexpr (ROW) {
+      // Both row-contiguous tiles go to this wave's LDS tiles at their
+      // [row][column] places (fp8 converted to the model dtype); K comes back
+      // in the A-operand layout of v_mfma_f32_16x16x32 (row l16, columns
+      // 8 lg + 32 c ...), V through the transpose reads below.
+      uint16_t* kt = sm.w[wave].tile.kt;
+      uint16_t* vt = sm.w[wave].tile.vt;
 #pragma unroll
-    for (int c = 0; c < CH; ++c) s = E::mfma_16x16x32(k_operand(r, c), qf[c], s);
+      for (int j = 0; j < NI; ++j) {
+        const int o = 1024 * j + 16 * lane;
+        const int at = (o / RB) * vt_pitch<D>() + (KV8 ? o % RB : (o % RB) / 2);
+        if constexpr (KV8) {
+          *reinterpret_cast<u32x4*>(kt + at) = fp8x8_to<E>(u32x2{r.k[j][0], r.k[j][1]});
+          *reinterpret_cast<u32x4*>(kt + at + 8) = fp8x8_to<E>(u32x2{r.k[j][2], r.k[j][3]});
+          *reinterpret_cast<u32x4*>(vt + at) = fp8x8_to<E>(u32x2{r.v[j][0], r.v[j][1]});
+          *reinterpret_cast<u32x4*>(vt + at + 8) = fp8x8_to<E>(u32x2{r.v[j][2], r.v[j][3]});
+        } else {
+          *reinterpret_cast<u32x4*>(kt + at) = r.k[j];
+          *reinterpret_cast<u32x4*>(vt + at) = r.v[j];
+        }
+      }
+#pragma unroll
+      for (int c = 0; c < CH; ++c) {
+        const u32x4 ka = *reinterpret_cast<const u32x4*>(kt + l16 * vt_pitch<D>() + 8 * lg + 32 * c);
+        s = E::mfma_16x16x32(ka, qf[c], s);
+      }
+    } else {
+#pragma unroll
+      for (int c = 0; c < CH; ++c) s = E::mfma_16x16x32(k_operand(r, c), qf[c], s);
+    }
 
     const int t0 = u.start + tile * kTile;
     float x[4];
@@ -476,8 +562,10 @@ struct UnitEngine {
     // j of a 16-lane group element j % 4 of group lane 4 k + (j % 16) / 4 as
     // its element k (measured on the device), so group lane s reads the four
     // columns 16 nb + 4 (s % 4) ... of token 4 lg + (s % 16) / 4.
-    uint16_t* vt = sm.vt[wave];
-    if constexpr (KV8) {
+    uint16_t* vt = sm.w[wave].tile.vt;
+    if constexpr (ROW) {
+      // written above with K
+    } else if constexpr (KV8) {
 #pragma unroll
       for (int j = 0; j < CH / 2; ++j) {
         const u32x4 w = r.v[j];
@@ -537,6 +625,11 @@ struct UnitEngine {
   // Merges the waves' states through LDS and writes the unit's result; ends
   // with a barrier, after which the LDS may be reused.
   __device__ __forceinline__ void merge(const Unit& u) {
+    // The outputs below overwrite this wave's tile region. The hardware runs a
+    // wave's LDS operations in order, but the compiler sees float stores and
+    // 16-bit tile reads of other types and could move them past each other:
+    // keep program order here.
+    __asm__ volatile("" ::: "memory");
     const int group = p.group;
     // Exp-sum of head l16 over all four lane groups.
     const float l_tot = rows_sum(l_run);
@@ -554,7 +647,7 @@ struct UnitEngine {
         const int h = 4 * lg + i - h0;
         if (h >= 0 && h < hn) {
 #pragma unroll
-          for (int n = 0; n < NB; ++n) sm.o[wave][h][16 * n + l16] = acc[n][i];
+          for (int n = 0; n < NB; ++n) sm.w[wave].o[h][16 * n + l16] = acc[n][i];
         }
       }
       lds_barrier();
@@ -580,7 +673,7 @@ struct UnitEngine {
       for (int w = 0; w < NW; ++w) {
         const float f = __builtin_amdgcn_exp2f(sm.m[w][h] - M);
         L += f * sm.l[w][h];
-        O += f * sm.o[w][hh][d];
+        O += f * sm.w[w].o[hh][d];
       }
       const float res = O / L * p.v_scale;
       const int q_head = u.kv_head * group + h;
@@ -618,7 +711,7 @@ template <typename E, int D, bool SPLIT, bool BS16, int ALIGN, int NW, bool KV8>
 __global__ __launch_bounds__(NW * kWave) __attribute__((amdgpu_waves_per_eu(attn_occupancy<D, KV8>(),
                                                                             attn_occupancy<D, KV8>())))
 void paged_attention_kernel(const KParams p) {
-  __shared__ UnitSmem<D, NW> sm;
+  __shared__ UnitSmem<D, NW, row_load<BS16, KV8>()> sm;
   const int per_plane = p.num_seqs * p.num_kv_heads;
   const int plane = static_cast<int>(blockIdx.x) / per_plane;
   const int rot = static_cast<int>(blockIdx.x) - plane * per_plane;
@@ -700,10 +793,12 @@ __global__ __launch_bounds__(NW * kWave) __attribute__((amdgpu_waves_per_eu(attn
                                                                             attn_occupancy<D, KV8>())))
 void paged_attention_balanced_kernel(const KParams p) {
   constexpr int NT = NW * kWave;
-  __shared__ UnitSmem<D, NW> sm;
+  __shared__ UnitSmem<D, NW, row_load<BS16, KV8>()> sm;
   __shared__ int pre[kMaxBalancedSeqs + 1];  // cost per KV head of sequences 0 .. s-1
   __shared__ int len[kMaxBalancedSeqs];      // lengths, clamped to the workspace
-  __shared__ int scan[NT];
+  // Block-wide scan of the set-up, in wave 0's region (no tile is processed before the set-up's last barrier).
+  static_assert(sizeof(sm.w[0]) >= NT * sizeof(int), "scan space");
+  int* scan = reinterpret_cast<int*>(&sm.w[0]);
   const int tid = threadIdx.x;
   const int S = p.num_seqs;
   const int P = p.max_partitions;
