@@ -1,7 +1,8 @@
 """Oracle for the decode hot path -- TEST INFRASTRUCTURE ONLY.
 
-Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s CPU-baseline leg
-import this package, and only as the checker (or, for the CPU baseline, as the
+Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s CPU leg (the CPU
+baseline, and the check of every timed op's output before it is timed) import
+this package, and only as the checker (or, for the CPU baseline, as the
 reference's CPU path being timed). The product (``decodekernels_amd``) never
 imports it and has no CPU fallback: without the HIP libraries its ops raise.
 

@@ -4,8 +4,10 @@ fused_add_rms_norm -> qkv gemm_tn -> rotary_embedding on the q and k columns
 of the qkv output -> reshape_and_cache of the new token's k and v columns ->
 paged_attention_decode (q is a strided view of the qkv output, as a serving
 engine passes it) -> o gemm_tn -> fused_add_rms_norm -> gate_up gemm_tn ->
-silu_and_mul -> down gemm_tn, at the head-dim-256 / group-8 attention shape
-with a reduced MLP width. ``seq_lens`` counts the new token, which sits at
+silu_and_mul -> down gemm_tn, at the head-dim-256 / group-8 attention shape,
+with a reduced MLP width (1024) and, as BASELINE.json's C5 names it, at full
+size (256 sequences of log-uniform lengths up to 32768, Llama-3-8B's MLP width
+14336; the GEMMs there are checked against an fp32 GEMM on the GPU). ``seq_lens`` counts the new token, which sits at
 position len - 1; an empty sequence is a padding row (position and slot -1).
 Each stage is checked against the oracle applied to the previous stage's
 actual output (the bar of each op's own parity test), then the whole step is
@@ -38,7 +40,7 @@ EPS = 1e-5
 
 
 class Layer:
-    def __init__(self, seq_lens, dtype, seed=0, fused_rope_cache=False):
+    def __init__(self, seq_lens, dtype, seed=0, fused_rope_cache=False, inter=INTER):
         self.fused_rope_cache = fused_rope_cache
         g = torch.Generator(device="cuda").manual_seed(seed)
         kw = dict(device="cuda", dtype=dtype)
@@ -46,8 +48,8 @@ class Layer:
         self.n = len(seq_lens)
         self.w_qkv = torch.randn((HQ + 2 * HKV) * D, HIDDEN, generator=g, **kw) * 0.02
         self.w_o = torch.randn(HIDDEN, HIDDEN, generator=g, **kw) * 0.02
-        self.w_gu = torch.randn(2 * INTER, HIDDEN, generator=g, **kw) * 0.02
-        self.w_down = torch.randn(HIDDEN, INTER, generator=g, **kw) * 0.02
+        self.w_gu = torch.randn(2 * inter, HIDDEN, generator=g, **kw) * 0.02
+        self.w_down = torch.randn(HIDDEN, inter, generator=g, **kw) * 0.02
         self.ln1 = (1 + 0.1 * torch.randn(HIDDEN, generator=g, device="cuda")).to(dtype)
         self.ln2 = (1 + 0.1 * torch.randn(HIDDEN, generator=g, device="cuda")).to(dtype)
         self.kv = make_paged_kv(seq_lens, HKV, D, BS, dtype, "cuda", layout="nhd", seed=seed + 1)
@@ -58,14 +60,14 @@ class Layer:
         self.qkv = torch.empty(self.n, self.w_qkv.shape[0], **kw)
         self.attn = torch.empty(self.n, HQ, D, **kw)
         self.o = torch.empty(self.n, HIDDEN, **kw)
-        self.gu = torch.empty(self.n, 2 * INTER, **kw)
-        self.act = torch.empty(self.n, INTER, **kw)
+        self.gu = torch.empty(self.n, 2 * inter, **kw)
+        self.act = torch.empty(self.n, inter, **kw)
         self.down = torch.empty(self.n, HIDDEN, **kw)
         self.ws = dk.alloc_workspace(self.n, HQ, D, self.max_len, "cuda")
         self.q = self.qkv[:, : HQ * D].view(self.n, HQ, D)
         self.k_new = self.qkv[:, HQ * D : (HQ + HKV) * D]
         self.v_new = self.qkv[:, (HQ + HKV) * D :]
-        self.rope = rope_cos_sin_cache(4096, D, base=1e6).cuda()
+        self.rope = rope_cos_sin_cache(max(4096, self.max_len), D, base=1e6).cuda()
         self.positions = torch.empty(self.n, dtype=torch.long, device="cuda")
         self.slots = torch.empty(self.n, dtype=torch.long, device="cuda")
         self.set_lens(seq_lens)
@@ -122,18 +124,43 @@ class Layer:
 SEQ_LENS = [0, 1, 600, 1500, 33, 2049, 512, 513]
 
 
+def _gemm_f32_gpu(a, b):
+    """fp32 GEMM on the GPU (the reference for GEMMs too large for the CPU oracle in a test)."""
+    return a.float() @ b.float().t()
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("fused", [False, True])
 def test_layer_step_stages_match_oracle(dtype, fused):
     L = Layer(SEQ_LENS, dtype, fused_rope_cache=fused)
     L.step(keep=True)
     torch.cuda.synchronize()
+    _check_stages(L, dtype, gemm_f32)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_layer_step_full_width_c5(dtype):
+    """BASELINE.json's C5 step at full size: 256 sequences (lengths log-uniform
+    in [1, 32768], 8 empty), 16 query / 2 KV heads of 256, block 32, hidden 4096,
+    MLP 2 x 14336; every stage against its oracle."""
+    import math
+
+    g = torch.Generator().manual_seed(5)
+    lens = torch.exp(torch.rand(256, generator=g) * math.log(32768)).long().clamp(1, 32768)
+    lens[torch.randperm(256, generator=g)[:8]] = 0
+    L = Layer(lens.tolist(), dtype, seed=11, fused_rope_cache=True, inter=14336)
+    L.step(keep=True)
+    torch.cuda.synchronize()
+    _check_stages(L, dtype, _gemm_f32_gpu)
+
+
+def _check_stages(L, dtype, gemm_ref):
     x1, r1 = L.saved["norm1"]
     want_x, want_r = fused_add_rms_norm_reference(L.x0.cpu(), L.r0.cpu(), L.ln1.cpu(), EPS)
     assert torch.equal(r1.cpu(), want_r), "residual of the first fused_add_rms_norm is not bit-exact"
     assert_ulp(x1, want_x, 1, "fused_add_rms_norm")
     qkv = L.saved["qkv"]
-    assert_max_abs(qkv, gemm_f32(x1, L.w_qkv), dtype, "qkv gemm")
+    assert_max_abs(qkv, gemm_ref(x1, L.w_qkv), dtype, "qkv gemm")
     hq_d, kv_d = HQ * D, (HQ + HKV) * D
     want_q, want_k = rotary_embedding_reference(L.positions.cpu(), qkv[:, :hq_d].cpu(), qkv[:, hq_d:kv_d].cpu(), D,
                                                 L.rope.cpu(), True)
@@ -145,14 +172,14 @@ def test_layer_step_stages_match_oracle(dtype, fused):
     assert torch.equal(L.kv.k_cache.cpu(), want_kc) and torch.equal(L.kv.v_cache.cpu(), want_vc)
     ref_attn = attention_f32(L.q, L.kv.k_cache, L.kv.v_cache, L.kv.block_tables, L.kv.seq_lens)
     assert_max_abs(L.attn, ref_attn, dtype, "attention on the qkv view")
-    assert (L.attn[0] == 0).all(), "zero-length sequence must give zeros"
-    assert_max_abs(L.saved["o"], gemm_f32(L.attn.view(L.n, HIDDEN), L.w_o), dtype, "o gemm")
+    assert (L.attn[L.kv.seq_lens == 0] == 0).all(), "zero-length sequences must give zeros"
+    assert_max_abs(L.saved["o"], gemm_ref(L.attn.view(L.n, HIDDEN), L.w_o), dtype, "o gemm")
     want_o, want_r2 = fused_add_rms_norm_reference(L.saved["o"].cpu(), L.saved["resid1"].cpu(), L.ln2.cpu(), EPS)
     assert torch.equal(L.resid.cpu(), want_r2)
     assert_ulp(L.o, want_o, 1, "second fused_add_rms_norm")
-    assert_max_abs(L.gu, gemm_f32(L.o, L.w_gu), dtype, "gate_up gemm")
+    assert_max_abs(L.gu, gemm_ref(L.o, L.w_gu), dtype, "gate_up gemm")
     assert_ulp(L.act, silu_and_mul_reference(L.gu.cpu()), 1, "silu_and_mul")
-    assert_max_abs(L.down, gemm_f32(L.act, L.w_down), dtype, "down gemm")
+    assert_max_abs(L.down, gemm_ref(L.act, L.w_down), dtype, "down gemm")
 
 
 @pytest.mark.parametrize("fused", [False, True])
