@@ -84,6 +84,9 @@ constexpr int kUnit = 2 * kPart;          // split-K work unit: two slots (its b
 #ifndef DK_ATTN_ROWLOAD
 #define DK_ATTN_ROWLOAD 1  // 16-bit caches: K and V tiles load row-contiguous (whole 128-byte lines) through LDS
 #endif
+#ifndef DK_REDUCE_PRE
+#define DK_REDUCE_PRE 2  // workspace rows per wave loaded in the reduce's first round trip
+#endif
 #ifndef DK_ATTN_ROW_AUX
 #define DK_ATTN_ROW_AUX 2  // cache-policy bits of the row-contiguous K/V loads (2 = nt, non-temporal)
 #endif
@@ -1024,7 +1027,7 @@ __global__ __launch_bounds__(reduce_waves<WPH>() * kWave) void paged_attention_r
     // the first 64 (exp-sum, max-logit) pairs (lane j holds row j's) and the
     // first kPre rows this wave merges (rows are in the workspace whatever n
     // is; values past n are never used).
-    constexpr int kPre = 2;
+    constexpr int kPre = DK_REDUCE_PRE;
     const int seq_len = p.seq_lens[seq];
     const bool in0 = lane < P;
     const float e_l = in0 ? es[lane] : 0.0f;
