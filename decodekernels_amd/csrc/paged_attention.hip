@@ -799,8 +799,8 @@ void paged_attention_balanced_kernel(const KParams p) {
   __shared__ UnitSmem<D, NW, row_load<BS16, KV8>()> sm;
   __shared__ int pre[kMaxBalancedSeqs + 1];  // cost per KV head of sequences 0 .. s-1
   __shared__ int len[kMaxBalancedSeqs];      // lengths, clamped to the workspace
-  // Block-wide scan of the set-up, in wave 0's region (no tile is processed before the set-up's last barrier).
-  static_assert(sizeof(sm.w[0]) >= NT * sizeof(int), "scan space");
+  // Wave totals of the set-up scan, in wave 0's region (no tile is processed before the set-up's last barrier).
+  static_assert(sizeof(sm.w[0]) >= NW * sizeof(int), "scan space");
   int* scan = reinterpret_cast<int*>(&sm.w[0]);
   const int tid = threadIdx.x;
   const int S = p.num_seqs;
@@ -810,7 +810,7 @@ void paged_attention_balanced_kernel(const KParams p) {
   constexpr int kStreamCost = stream_cost<KV8>();
   auto cost_of_len = [](int l) { return l > 0 ? (l + kTile - 1) / kTile + kStreamCost : 0; };
 
-  // Per-thread chunk of sequences -> block-wide inclusive scan of stream costs.
+  // Per-thread chunk of sequences -> workgroup-wide inclusive scan of stream costs.
   const int per = (S + NT - 1) / NT;
   const int s0 = min(tid * per, S);
   const int s1 = min(s0 + per, S);
@@ -820,20 +820,25 @@ void paged_attention_balanced_kernel(const KParams p) {
     len[s] = l;
     cnt += cost_of_len(l);
   }
-  scan[tid] = cnt;
-  __syncthreads();
-  for (int off = 1; off < NT; off <<= 1) {
-    const int add = tid >= off ? scan[tid - off] : 0;
-    __syncthreads();
-    scan[tid] += add;
-    __syncthreads();
+  // Inclusive scan: within each wave by shuffles, then the wave totals
+  // through LDS (two barriers instead of two per doubling step).
+  const int lane = tid % kWave;
+  const int wv = tid / kWave;
+  int incl = cnt;
+#pragma unroll
+  for (int off = 1; off < kWave; off <<= 1) {
+    const int y = __shfl_up(incl, off, kWave);
+    if (lane >= off) incl += y;
   }
-  int run = scan[tid] - cnt;
+  if (lane == kWave - 1) scan[wv] = incl;
+  __syncthreads();
+  for (int w = 0; w < wv; ++w) incl += scan[w];
+  int run = incl - cnt;
   for (int s = s0; s < s1; ++s) {
     pre[s] = run;
     run += cost_of_len(len[s]);
   }
-  if (tid == NT - 1) pre[S] = scan[NT - 1];
+  if (tid == NT - 1) pre[S] = incl;
   __syncthreads();
 
   const int hkv = p.num_kv_heads;
