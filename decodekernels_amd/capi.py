@@ -131,6 +131,17 @@ _SIGNATURES = {
         + [ctypes.c_int] * 6
         + [ctypes.c_void_p],
     ),
+    "dk_gemm_tn_workspace_bytes": (ctypes.c_int64, [ctypes.c_int, ctypes.c_int, ctypes.c_int]),
+    "dk_gemm_tn_plan": (
+        ctypes.c_int,
+        [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.POINTER(ctypes.c_int)],
+    ),
+    "dk_gemm_tn_ws": (
+        ctypes.c_int,
+        [ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p]
+        + [ctypes.c_int] * 6
+        + [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p],
+    ),
     "dk_rms_norm": (
         ctypes.c_int,
         [ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_int]
@@ -192,6 +203,16 @@ def declared_functions() -> list[str]:
     """Names of every function the C header declares."""
     text = HEADER_PATH.read_text()
     return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\*?\s+\*?(dk_\w+)\s*\(", text, flags=re.M)))
+
+
+def gemm_plan(M: int, N: int, K: int, with_workspace: bool = True) -> tuple[int, int, int, int]:
+    """(waves along N, waves along K, K splits, columns per split) of gemm_tn's
+    skinny kernel for this shape (all 0 for M > 64); host arithmetic only."""
+    out = (ctypes.c_int * 4)()
+    rc = lib().dk_gemm_tn_plan(M, N, K, int(with_workspace), out)
+    if rc != 0:
+        raise ValueError(last_error())
+    return tuple(out)
 
 
 def last_error() -> str:

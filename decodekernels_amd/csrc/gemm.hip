@@ -12,16 +12,20 @@
 //   therefore go straight to registers (each weight byte is used once), while
 //   activation tiles are loaded once per workgroup with contiguous 16-byte
 //   loads into LDS and shared by the waves that own different output columns.
-//   8 waves per workgroup, split between N (16 columns each) and K so that a
-//   launch keeps >= 384 (M <= 16) or >= 192 workgroups; buffer loads with
-//   descriptor bounds make rows past M/N and columns past K read as zero, and
-//   DEPTH-deep register rings of weights and activations keep loads in flight
-//   across the per-step barrier.
+//   Up to 14 waves per workgroup, split between N (16 columns each) and K; the
+//   grid is planned at one workgroup per CU, with wide column tiles to cut the
+//   activation re-reads and, given a workspace, the K reduction split over
+//   workgroups (fp32 partial tiles summed in order by a second kernel). Buffer
+//   loads with descriptor bounds make rows past M/N and columns past K read as
+//   zero, and DEPTH-deep register rings of weights and activations keep loads
+//   in flight across the per-step barrier.
 // * LDS-DMA (M > 64, batched decode and prefill): A and B tiles go from HBM
 //   straight into LDS (buffer_load ... lds), bank-conflict-free XOR-swizzled,
 //   through a multi-stage ring; five tile shapes from 256x256 down to 64x64,
 //   picked per call by a throughput model so that batches of a few hundred
 //   rows still fill all 256 CUs.
+#include <algorithm>
+
 #include "../../include/decodekernels_amd.h"
 #include "dk_device.h"
 #include "dk_host.h"
@@ -71,11 +75,16 @@ __global__ __launch_bounds__(WN * WK * kWave) void gemm_skinny_lds_kernel(const 
                                                                           const uint16_t* __restrict__ B,
                                                                           const uint16_t* __restrict__ bias,
                                                                           uint16_t* __restrict__ C, int M, int N,
-                                                                          int K, int lda, int ldb, int ldc) {
+                                                                          int K, int lda, int ldb, int ldc,
+                                                                          float* __restrict__ part, int k_split) {
   constexpr int NT = WN * WK * kWave;
   constexpr int KS = kLdsBK / 32;  // k-steps per chunk
+  // Split-K (part != nullptr): workgroup row blockIdx.y covers K columns
+  // [kb, ke) (k_split a multiple of kLdsBK) and writes its fp32 partial tile to
+  // part[blockIdx.y][M][N], without the bias; a second kernel sums the splits.
+  const int kb = part != nullptr ? static_cast<int>(blockIdx.y) * k_split : 0;
+  const int ke = part != nullptr ? min(K, kb + k_split) : K;
   using AR = ARegs<MT, WN>;
-  static_assert(!AR::kPartial || AR::kPerLane == 1, "a partial activation load is one vector per lane");
   // The activation tiles and, after the K loop's last barrier, the partial
   // output tiles share one LDS allocation.
   constexpr size_t kBytesA = sizeof(uint16_t) * WK * 2 * 16 * MT * kLdsARow;
@@ -100,7 +109,7 @@ __global__ __launch_bounds__(WN * WK * kWave) void gemm_skinny_lds_kernel(const 
   const __amdgpu_buffer_rsrc_t r_none = rsrc(A, 0);
   const int boff = l16 * ldb * 2 + 16 * lg;
 
-  const int n_chunks = (K + kLdsBK - 1) / kLdsBK;
+  const int n_chunks = (ke - kb + kLdsBK - 1) / kLdsBK;
   const int steps = (n_chunks + WK - 1) / WK;  // chunk steps of the whole workgroup
 
   // Activation tile of chunk c: vector v of the group covers row v / 8, columns 8 (v % 8) ...
@@ -112,8 +121,8 @@ __global__ __launch_bounds__(WN * WK * kWave) void gemm_skinny_lds_kernel(const 
     for (int j = 0; j < AR::kPerLane; ++j) {
       const int v = gl + j * WN * kWave;
       const int row = v / 8;
-      const int k = c * kLdsBK + 8 * (v % 8);
-      const bool in = k < K && (!AR::kPartial || v < AR::kVecs);
+      const int k = kb + c * kLdsBK + 8 * (v % 8);
+      const bool in = k < ke && (!AR::kPartial || v < AR::kVecs);
       r.v[j] = __builtin_amdgcn_raw_buffer_load_b128(rr, in ? row * lda * 2 + 2 * k : kOutOfRange, 0, 0);
     }
   };
@@ -131,8 +140,9 @@ __global__ __launch_bounds__(WN * WK * kWave) void gemm_skinny_lds_kernel(const 
     const __amdgpu_buffer_rsrc_t rr = live ? rb : r_none;
 #pragma unroll
     for (int s = 0; s < KS; ++s) {
-      const int k = c * kLdsBK + 32 * s + 8 * lg;
-      bf[s] = __builtin_amdgcn_raw_buffer_load_b128(rr, k < K ? boff + 2 * (c * kLdsBK + 32 * s) : kOutOfRange, 0, 0);
+      const int k = kb + c * kLdsBK + 32 * s + 8 * lg;
+      bf[s] = __builtin_amdgcn_raw_buffer_load_b128(rr, k < ke ? boff + 2 * (kb + c * kLdsBK + 32 * s) : kOutOfRange, 0,
+                                                    0);
     }
   };
 
@@ -194,8 +204,49 @@ __global__ __launch_bounds__(WN * WK * kWave) void gemm_skinny_lds_kernel(const 
     float v = 0.0f;
 #pragma unroll
     for (int w = 0; w < WK; ++w) v += red[w][cn / 16][i][src_lane][m % 4];
+    if (part != nullptr) {
+      part[(static_cast<int64_t>(blockIdx.y) * M + m) * N + n] = v;
+      continue;
+    }
     if (bias != nullptr) v += E::to_float(bias[n]);
     C[static_cast<int64_t>(m) * ldc + n] = E::from_float(v);
+  }
+}
+
+// Sums the split-K partial tiles of the skinny kernel in split order, adds
+// the bias in fp32 and rounds once: C[m][n] = round(sum_s part[s][m][n] + bias[n]).
+// One thread per 4 consecutive columns of a row; 16-byte loads when N % 4 == 0
+// (every partial row then starts 16-byte aligned).
+template <typename E>
+__global__ __launch_bounds__(256) void gemm_splitk_reduce_kernel(const float* __restrict__ part, int splits, int M,
+                                                                 int N, const uint16_t* __restrict__ bias,
+                                                                 uint16_t* __restrict__ C, int ldc) {
+  const int n4 = (N + 3) / 4;
+  const int64_t idx = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (idx >= static_cast<int64_t>(M) * n4) return;
+  const int m = static_cast<int>(idx / n4);
+  const int n = static_cast<int>(idx % n4) * 4;
+  const int64_t plane = static_cast<int64_t>(M) * N;
+  const float* p = part + static_cast<int64_t>(m) * N + n;
+  float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  if (N % 4 == 0) {
+    for (int sp = 0; sp < splits; ++sp) {
+      const f32x4 x = *reinterpret_cast<const f32x4*>(p + sp * plane);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) v[r] += x[r];
+    }
+  } else {
+    for (int sp = 0; sp < splits; ++sp) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        if (n + r < N) v[r] += p[sp * plane + r];
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    if (n + r >= N) break;
+    if (bias != nullptr) v[r] += E::to_float(bias[n + r]);
+    C[static_cast<int64_t>(m) * ldc + n + r] = E::from_float(v[r]);
   }
 }
 
@@ -415,53 +466,177 @@ hipError_t launch_dma(const uint16_t* A, const uint16_t* B, const uint16_t* bias
   return hipGetLastError();
 }
 
-#ifndef DK_SKINNY_WAVES
-#define DK_SKINNY_WAVES 8  // waves per skinny workgroup
-#endif
 #ifndef DK_SKINNY_DEPTH
 #define DK_SKINNY_DEPTH 2  // k-steps of weights and activations in flight per wave
 #endif
 #ifndef DK_SKINNY_MIN_WGS
-#define DK_SKINNY_MIN_WGS 192  // fewest workgroups the N split may leave, M > 16
+#define DK_SKINNY_MIN_WGS 192  // wide plan (N > 32768): fewest workgroups the N split may leave, M > 16
 #endif
 #ifndef DK_SKINNY_MIN_WGS_M16
 #define DK_SKINNY_MIN_WGS_M16 384  // the same for M <= 16
 #endif
 
+// Launch shape of the skinny kernel: MT 16-row activation tiles, WN x WK
+// waves per workgroup (WN along N, 16 columns each; WK along K), and, with a
+// workspace, the K reduction split over `splits` workgroup rows of k_split
+// columns each.
+struct SkinnyPlan {
+  int mt, wn, wk, splits, k_split;
+};
+
+// Plan of grids with more than one workgroup per CU (N > 32768): as many waves
+// along N as keep >= 384 (M <= 16) or >= 192 workgroups, the rest along K.
+inline SkinnyPlan skinny_plan_wide(int M, int N, int K) {
+  SkinnyPlan p{};
+  p.mt = M <= 16 ? 1 : (M <= 32 ? 2 : 4);
+  const int min_wgs = p.mt == 1 ? DK_SKINNY_MIN_WGS_M16 : DK_SKINNY_MIN_WGS;
+  p.wn = (M > 32 && N >= 24576) ? 8 : (N >= 64 * min_wgs ? 4 : (N >= 32 * min_wgs ? 2 : 1));
+  p.wk = 8 / p.wn;
+  p.splits = 1;
+  p.k_split = K;
+  return p;
+}
+
+// Workgroup shapes (WN, WK) of the plans below, narrowest first.
+constexpr int kSkinnyShapes[][2] = {{1, 8}, {2, 4}, {4, 2}, {6, 2}, {7, 2}, {8, 1}};
+constexpr int kSkinnyCus = 256;
+
+// The widest unsplit grid that fits one workgroup per CU (the narrowest shape
+// with <= 256 column tiles); wn = 0 when none does.
+inline SkinnyPlan skinny_plan_unsplit(int M, int N, int K) {
+  SkinnyPlan p{};
+  p.mt = M <= 16 ? 1 : (M <= 32 ? 2 : 4);
+  p.splits = 1;
+  p.k_split = K;
+  for (const auto& sh : kSkinnyShapes) {
+    if (ceil_div64(N, 16 * sh[0]) <= kSkinnyCus) {
+      p.wn = sh[0];
+      p.wk = sh[1];
+      return p;
+    }
+  }
+  return p;
+}
+
+// Every workgroup re-reads the activation rows of its K range (M x k_split
+// elements) for its 16 WN x k_split weights, so wide column tiles cut that
+// traffic; splitting K over workgroup rows then keeps the grid at the CU
+// count, at the price of an fp32 partial tile per split and a second kernel
+// that sums them. The plan, fitted to interleaved cold timings of every
+// candidate shape at M = 1 ... 64 on the Llama-3-8B projections (bf16,
+// MI355X):
+//  1. the widest unsplit grid of at most one workgroup per CU, if it fills
+//     >= 3/4 of the CUs and each workgroup re-reads <= 256 KiB of activations;
+//  2. else, with a workspace, the grids of 2 ... 8 K splits (>= 512 columns
+//     each, <= 256 workgroups) within 10% of the fullest one: the fewest
+//     splits whose workgroups re-read at most max(128 KiB, half their weight
+//     bytes) of activations, or failing that the fewest activation bytes;
+//  3. else the unsplit grid of 1, or for N > 32768 (no grid of one workgroup
+//     per CU) the wide plan.
+// Picks (waves along N x along K, splits; us cold, vs hipBLASLt): qkv (N 6144,
+// K 4096) M <= 32: 2 x 4, unsplit (15.2 at M = 1, 18.2 at M = 32; 0.90 /
+// 1.01x), M = 48/64: 6 x 2, 4 splits (20.0 / 21.0; 0.98 / 1.02x); o (N 4096)
+// M <= 32: 1 x 8, unsplit (12.3 ... 15.0; 0.68 ... 0.94x), M = 48/64: 4 x 2,
+// 4 splits (16.5 / 16.8; 0.97 / 0.94x); down (N 4096, K 14336) M <= 8: 1 x 8
+// (24.8 / 25.0; 0.94x), M = 16/32: 2 x 4 / 4 x 2 with 2 / 4 splits (27.6 /
+// 29.6; 1.02 / 0.91x), M = 48/64: 8 x 1, 8 splits (32.0 / 33.1; 0.84 /
+// 0.66x); gate_up (N 28672): 7 x 2, unsplit. Each pick was the fastest
+// candidate of its shape and M except gate_up at M <= 32, where 4 x 2 (448
+// workgroups) was 6-8% faster on one of four machines and 7 x 2 7% faster on
+// two. A 257th workgroup puts two on one CU and doubles that CU's time.
+inline SkinnyPlan skinny_plan(int M, int N, int K, bool split_ok) {
+  constexpr int64_t kKiB = 1024;
+  SkinnyPlan u = skinny_plan_unsplit(M, N, K);
+  if (u.wn > 0 && static_cast<int64_t>(M) * K * 2 <= 256 * kKiB &&
+      4 * ceil_div64(N, 16 * u.wn) >= 3 * kSkinnyCus)
+    return u;
+  if (split_ok && K > 0) {
+    struct Cand {
+      int wn, wk, splits, k_split;
+      int64_t wgs;
+    };
+    Cand cand[sizeof(kSkinnyShapes) / sizeof(kSkinnyShapes[0]) * 7];
+    int nc = 0;
+    int64_t max_wgs = 0;
+    for (const auto& sh : kSkinnyShapes) {
+      const int64_t tiles = ceil_div64(N, 16 * sh[0]);
+      for (int s = 2; s <= 8; ++s) {
+        if (K / s < 512) break;
+        const int per = (K + s - 1) / s;
+        const int ks = (per + kLdsBK - 1) / kLdsBK * kLdsBK;
+        if ((K + ks - 1) / ks != s) continue;  // every split non-empty
+        if (tiles * s > kSkinnyCus) break;
+        cand[nc++] = Cand{sh[0], sh[1], s, ks, tiles * s};
+        max_wgs = std::max(max_wgs, tiles * s);
+      }
+    }
+    const Cand* best = nullptr;
+    bool best_ok = false;
+    for (int i = 0; i < nc; ++i) {
+      const Cand& c = cand[i];
+      if (10 * c.wgs < 9 * max_wgs) continue;  // within 10% of the fullest grid
+      const int64_t act = static_cast<int64_t>(M) * c.k_split * 2;
+      const int64_t wts = int64_t{16} * c.wn * c.k_split * 2;
+      const bool ok = act <= std::max<int64_t>(128 * kKiB, wts / 2);
+      if (best == nullptr || (ok && !best_ok)) {
+        best = &c;
+        best_ok = ok;
+        continue;
+      }
+      if (ok != best_ok) continue;
+      const int64_t best_act = static_cast<int64_t>(M) * best->k_split;
+      const bool better = ok ? (c.splits < best->splits)
+                             : (static_cast<int64_t>(M) * c.k_split < best_act ||
+                                (static_cast<int64_t>(M) * c.k_split == best_act && c.splits < best->splits));
+      if (better) best = &c;
+    }
+    if (best != nullptr) {
+      SkinnyPlan p = u;
+      p.wn = best->wn;
+      p.wk = best->wk;
+      p.splits = best->splits;
+      p.k_split = best->k_split;
+      return p;
+    }
+  }
+  return u.wn > 0 ? u : skinny_plan_wide(M, N, K);
+}
+
+inline int64_t skinny_workspace_bytes(const SkinnyPlan& p, int M, int N) {
+  return p.splits > 1 ? static_cast<int64_t>(p.splits) * M * N * static_cast<int64_t>(sizeof(float)) : 0;
+}
+
 template <typename E>
 hipError_t launch(const uint16_t* A, const uint16_t* B, const uint16_t* bias, uint16_t* C, int M, int N, int K,
-                  int lda, int ldb, int ldc, hipStream_t s) {
+                  int lda, int ldb, int ldc, void* workspace, int64_t workspace_bytes, hipStream_t s) {
   if (M <= 64) {
-    {
-      // DK_SKINNY_WAVES waves; as many along N as keep enough workgroups
-      // (more columns per workgroup share each activation tile), the rest
-      // split K. Measured: with one 16-row activation tile (M <= 16) the
-      // activation traffic is small and 384 workgroups beat 192 (qkv, N =
-      // 6144); with 32 or 64 rows the activation tile reloads cost more.
-      constexpr int kW = DK_SKINNY_WAVES;
-      const int mt = M <= 16 ? 1 : (M <= 32 ? 2 : 4);
-      const int min_wgs = mt == 1 ? DK_SKINNY_MIN_WGS_M16 : DK_SKINNY_MIN_WGS;
-      int wn = (M > 32 && N >= 24576) ? 8 : (N >= 64 * min_wgs ? 4 : (N >= 32 * min_wgs ? 2 : 1));
-      wn = wn > kW ? kW : wn;
-      const dim3 g2(static_cast<unsigned>(ceil_div64(N, 16 * wn)));
-#define DK_SKINNY_LDS(MT_, WN_)                                                                          \
-  hipLaunchKernelGGL((gemm_skinny_lds_kernel<E, MT_, WN_, (kW / WN_ > 0 ? kW / WN_ : 1), DK_SKINNY_DEPTH>), g2, \
-                     dim3(WN_ * (kW / WN_ > 0 ? kW / WN_ : 1) * kWave), 0, s, A, B, bias, C, M, N, K, lda, ldb, ldc)
-      switch (mt * 10 + wn) {
-        case 11: DK_SKINNY_LDS(1, 1); break;
-        case 12: DK_SKINNY_LDS(1, 2); break;
-        case 14: DK_SKINNY_LDS(1, 4); break;
-        case 21: DK_SKINNY_LDS(2, 1); break;
-        case 22: DK_SKINNY_LDS(2, 2); break;
-        case 24: DK_SKINNY_LDS(2, 4); break;
-        case 18: DK_SKINNY_LDS(1, 8); break;
-        case 28: DK_SKINNY_LDS(2, 8); break;
-        case 41: DK_SKINNY_LDS(4, 1); break;
-        case 42: DK_SKINNY_LDS(4, 2); break;
-        case 44: DK_SKINNY_LDS(4, 4); break;
-        default: DK_SKINNY_LDS(4, 8); break;
-      }
+    SkinnyPlan p = skinny_plan(M, N, K, true);
+    if (p.splits > 1 && (workspace == nullptr || skinny_workspace_bytes(p, M, N) > workspace_bytes))
+      p = skinny_plan(M, N, K, false);
+    float* part = p.splits > 1 ? static_cast<float*>(workspace) : nullptr;
+    const dim3 g2(static_cast<unsigned>(ceil_div64(N, 16 * p.wn)), static_cast<unsigned>(p.splits));
+#define DK_SKINNY_LDS(MT_, WN_, WK_)                                                                 \
+  case MT_ * 100 + WN_ * 10 + WK_:                                                                   \
+    hipLaunchKernelGGL((gemm_skinny_lds_kernel<E, MT_, WN_, WK_, DK_SKINNY_DEPTH>), g2, dim3(WN_ * WK_ * kWave), 0, s, \
+                       A, B, bias, C, M, N, K, lda, ldb, ldc, part, p.k_split);                            \
+    break;
+#define DK_SKINNY_MT(MT_)                                                                                 \
+  DK_SKINNY_LDS(MT_, 1, 8) DK_SKINNY_LDS(MT_, 2, 4) DK_SKINNY_LDS(MT_, 4, 2) DK_SKINNY_LDS(MT_, 6, 2)     \
+  DK_SKINNY_LDS(MT_, 7, 2) DK_SKINNY_LDS(MT_, 8, 1)
+    switch (p.mt * 100 + p.wn * 10 + p.wk) {
+      DK_SKINNY_MT(1)
+      DK_SKINNY_MT(2)
+      DK_SKINNY_MT(4)
+      default: return hipErrorInvalidValue;  // not a shape the plans produce
+    }
+#undef DK_SKINNY_MT
 #undef DK_SKINNY_LDS
+    if (part != nullptr) {
+      const hipError_t e = hipGetLastError();
+      if (e != hipSuccess) return e;
+      const int64_t threads = static_cast<int64_t>(M) * ((N + 3) / 4);
+      hipLaunchKernelGGL((gemm_splitk_reduce_kernel<E>), dim3(static_cast<unsigned>((threads + 255) / 256)), dim3(256),
+                         0, s, part, p.splits, M, N, bias, C, ldc);
     }
     return hipGetLastError();
   }
@@ -498,8 +673,10 @@ hipError_t launch(const uint16_t* A, const uint16_t* B, const uint16_t* bias, ui
 }  // namespace gemm
 }  // namespace dk
 
-extern "C" int dk_gemm_tn(int dtype, const void* A, const void* B, const void* bias, void* C, int M, int N, int K,
-                          int lda, int ldb, int ldc, void* stream) {
+namespace {
+
+int gemm_tn_checked(int dtype, const void* A, const void* B, const void* bias, void* C, int M, int N, int K, int lda,
+                    int ldb, int ldc, void* workspace, int64_t workspace_bytes, void* stream) {
   using namespace dk;
   clear_error();
   if (dtype != DK_FLOAT16 && dtype != DK_BFLOAT16)
@@ -510,6 +687,8 @@ extern "C" int dk_gemm_tn(int dtype, const void* A, const void* B, const void* b
     return fail("gemm_tn: K and row strides of a/b must be multiples of 8");
   if (!aligned_to(A, 16) || !aligned_to(B, 16)) return fail("gemm_tn: a and b must be 16-byte aligned");
   if (C == nullptr || (K > 0 && (A == nullptr || B == nullptr))) return fail("gemm_tn: pointers must not be NULL");
+  if (workspace != nullptr && !aligned_to(workspace, 16)) return fail("gemm_tn: workspace must be 16-byte aligned");
+  if (workspace_bytes < 0) return fail("gemm_tn: workspace_bytes must be non-negative");
   if (M > 64 && ceil_div64(M, 64) * ceil_div64(N, 64) >= (int64_t{1} << 31)) return fail("gemm_tn: M x N is too large");
   if (M > 64 && int64_t{256} * std::max(lda, ldb) * 2 >= (int64_t{1} << 31))
     return fail("gemm_tn: row strides too large for 32-bit buffer offsets");
@@ -520,7 +699,43 @@ extern "C" int dk_gemm_tn(int dtype, const void* A, const void* B, const void* b
   const auto* b = static_cast<const uint16_t*>(B);
   const auto* bi = static_cast<const uint16_t*>(bias);
   auto* c = static_cast<uint16_t*>(C);
-  const hipError_t e = dtype == DK_BFLOAT16 ? gemm::launch<Bf16>(a, b, bi, c, M, N, K, lda, ldb, ldc, s)
-                                            : gemm::launch<F16>(a, b, bi, c, M, N, K, lda, ldb, ldc, s);
+  const hipError_t e =
+      dtype == DK_BFLOAT16
+          ? gemm::launch<Bf16>(a, b, bi, c, M, N, K, lda, ldb, ldc, workspace, workspace_bytes, s)
+          : gemm::launch<F16>(a, b, bi, c, M, N, K, lda, ldb, ldc, workspace, workspace_bytes, s);
   return static_cast<int>(e);
+}
+
+}  // namespace
+
+extern "C" int dk_gemm_tn(int dtype, const void* A, const void* B, const void* bias, void* C, int M, int N, int K,
+                          int lda, int ldb, int ldc, void* stream) {
+  return gemm_tn_checked(dtype, A, B, bias, C, M, N, K, lda, ldb, ldc, nullptr, 0, stream);
+}
+
+extern "C" int64_t dk_gemm_tn_workspace_bytes(int M, int N, int K) {
+  if (M <= 0 || N <= 0 || K <= 0 || M > 64) return 0;
+  const dk::gemm::SkinnyPlan p = dk::gemm::skinny_plan(M, N, K, true);
+  return dk::gemm::skinny_workspace_bytes(p, M, N);
+}
+
+extern "C" int dk_gemm_tn_plan(int M, int N, int K, int with_workspace, int* plan) {
+  dk::clear_error();
+  if (plan == nullptr) return dk::fail("gemm_tn_plan: plan must not be NULL");
+  if (M <= 0 || N <= 0 || K < 0) return dk::fail("gemm_tn_plan: M and N must be positive, K non-negative");
+  if (M > 64) {
+    for (int i = 0; i < 4; ++i) plan[i] = 0;
+    return hipSuccess;
+  }
+  const dk::gemm::SkinnyPlan p = dk::gemm::skinny_plan(M, N, K, with_workspace != 0);
+  plan[0] = p.wn;
+  plan[1] = p.wk;
+  plan[2] = p.splits;
+  plan[3] = p.k_split;
+  return hipSuccess;
+}
+
+extern "C" int dk_gemm_tn_ws(int dtype, const void* A, const void* B, const void* bias, void* C, int M, int N, int K,
+                             int lda, int ldb, int ldc, void* workspace, int64_t workspace_bytes, void* stream) {
+  return gemm_tn_checked(dtype, A, B, bias, C, M, N, K, lda, ldb, ldc, workspace, workspace_bytes, stream);
 }

@@ -227,6 +227,10 @@ void gemm_tn(at::Tensor& c, const at::Tensor& a, const at::Tensor& b, const std:
   const int64_t M = a.size(0), K = a.size(1), N = b.size(0);
   TORCH_CHECK(b.size(1) == K, "gemm_tn: K mismatch");
   TORCH_CHECK(c.size(0) == M && c.size(1) == N, "gemm_tn: c must be [M, N]");
+  TORCH_CHECK(M < (int64_t{1} << 31) && N < (int64_t{1} << 31) && K < (int64_t{1} << 31) &&
+                  a.stride(0) < (int64_t{1} << 31) && b.stride(0) < (int64_t{1} << 31) &&
+                  c.stride(0) < (int64_t{1} << 31),
+              "gemm_tn: sizes and row strides must fit in 32 bits");
   TORCH_CHECK(a.stride(1) == 1 && b.stride(1) == 1 && c.stride(1) == 1, "gemm_tn: last dims must be contiguous");
   TORCH_CHECK(K % 8 == 0 && a.stride(0) % 8 == 0 && b.stride(0) % 8 == 0,
               "gemm_tn: K and row strides of a/b must be multiples of 8");
@@ -239,9 +243,17 @@ void gemm_tn(at::Tensor& c, const at::Tensor& a, const at::Tensor& b, const std:
   }
   const int dt = dtype_code(a.scalar_type(), "gemm_tn");
   const DeviceGuard guard(a.device());
-  check_status(dk_gemm_tn(dt, a.data_ptr(), b.data_ptr(), bias_ptr, c.data_ptr(), static_cast<int>(M),
-                          static_cast<int>(N), static_cast<int>(K), static_cast<int>(a.stride(0)),
-                          static_cast<int>(b.stride(0)), static_cast<int>(c.stride(0)), stream_of(a)),
+  // Decode shapes that split K take an fp32 workspace from the caching
+  // allocator (freed back to it when this call returns; the stream order keeps
+  // it alive for the kernels).
+  const int64_t ws_bytes =
+      dk_gemm_tn_workspace_bytes(static_cast<int>(M), static_cast<int>(N), static_cast<int>(K));
+  at::Tensor ws;
+  if (ws_bytes > 0) ws = at::empty({ws_bytes / 4}, a.options().dtype(at::kFloat));
+  check_status(dk_gemm_tn_ws(dt, a.data_ptr(), b.data_ptr(), bias_ptr, c.data_ptr(), static_cast<int>(M),
+                             static_cast<int>(N), static_cast<int>(K), static_cast<int>(a.stride(0)),
+                             static_cast<int>(b.stride(0)), static_cast<int>(c.stride(0)),
+                             ws_bytes > 0 ? ws.data_ptr() : nullptr, ws_bytes, stream_of(a)),
                "gemm_tn");
 }
 

@@ -1,0 +1,160 @@
+"""CPU tests of gemm_tn's skinny launch plan (M <= 64), through
+``dk_gemm_tn_plan`` / ``dk_gemm_tn_workspace_bytes`` (host arithmetic, no
+kernel launch).
+
+``skinny_plan`` (decodekernels_amd/csrc/gemm.hip) picks the workgroup shape
+(waves along N, 16 columns each, x waves along K) and the number of K splits:
+the widest unsplit grid of <= 256 workgroups when it fills >= 3/4 of the 256
+CUs and each workgroup re-reads <= 256 KiB of activations; else, with a
+workspace, the grid of 2..8 K splits (>= 512 columns each, <= 256
+workgroups, within 10% of the fullest) with the fewest splits whose
+workgroups re-read <= max(128 KiB, half their weight bytes) of activations
+(else the fewest activation bytes); else the unsplit grid, or the wide plan
+for N > 32768. This file restates that arithmetic and checks, over random
+shapes, that the library plans exactly the same, plus the invariants the
+kernels rely on: every split non-empty and a multiple of 64 columns, at most
+256 workgroups whenever K is split, the workspace size, and a workgroup
+shape the launcher instantiates. The Llama-3-8B decode projections map to
+the shapes measured fastest.
+"""
+
+import random
+
+import pytest
+
+from decodekernels_amd import capi
+
+SHAPES = [(1, 8), (2, 4), (4, 2), (6, 2), (7, 2), (8, 1)]
+KIB = 1024
+
+
+def _wide(M, N, K):
+    mt = 1 if M <= 16 else (2 if M <= 32 else 4)
+    min_wgs = 384 if mt == 1 else 192
+    wn = 8 if (M > 32 and N >= 24576) else (4 if N >= 64 * min_wgs else (2 if N >= 32 * min_wgs else 1))
+    return (wn, 8 // wn, 1, K)
+
+
+def replica_plan(M, N, K, with_workspace=True, mistake=None):
+    """(wn, wk, splits, k_split) as skinny_plan computes it. ``mistake``
+    plants an error: "fill" drops the 3/4-fill condition of the unsplit grid,
+    "limit" compares activation bytes with the weight bytes instead of half
+    of them."""
+    u = None
+    for wn, wk in SHAPES:
+        if -(-N // (16 * wn)) <= 256:
+            u = (wn, wk, 1, K)
+            break
+    if u is not None and M * K * 2 <= 256 * KIB and (mistake == "fill" or 4 * -(-N // (16 * u[0])) >= 3 * 256):
+        return u
+    cands = []
+    if with_workspace and K > 0:
+        for wn, wk in SHAPES:
+            tiles = -(-N // (16 * wn))
+            for s in range(2, 9):
+                if K // s < 512:
+                    break
+                per = -(-K // s)
+                ks = -(-per // 64) * 64
+                if -(-K // ks) != s:
+                    continue
+                if tiles * s > 256:
+                    break
+                cands.append((wn, wk, s, ks, tiles * s))
+    if cands:
+        mx = max(c[4] for c in cands)
+        near = [c for c in cands if 10 * c[4] >= 9 * mx]
+        div = 1 if mistake == "limit" else 2
+        ok = [c for c in near if M * c[3] * 2 <= max(128 * KIB, 16 * c[0] * c[3] * 2 // div)]
+        best = min(ok, key=lambda c: (c[2], near.index(c))) if ok else min(near, key=lambda c: (M * c[3], c[2], near.index(c)))
+        return best[:4]
+    return u if u is not None else _wide(M, N, K)
+
+
+def _random_shapes(n, seed):
+    rng = random.Random(seed)
+    for _ in range(n):
+        M = rng.randint(1, 64)
+        N = rng.choice([rng.randint(1, 600), rng.randint(1, 8192), rng.randint(1, 40000)])
+        K = 8 * rng.choice([rng.randint(0, 64), rng.randint(0, 3000)])
+        yield M, N, K
+
+
+def test_library_plans_like_the_replica():
+    for M, N, K in _random_shapes(20000, 3):
+        for ws in (True, False):
+            assert capi.gemm_plan(M, N, K, ws) == replica_plan(M, N, K, ws), (M, N, K, ws)
+
+
+def test_plan_invariants_and_workspace_size():
+    L = capi.lib()
+    for M, N, K in _random_shapes(20000, 4):
+        wn, wk, s, ks = capi.gemm_plan(M, N, K)
+        assert (wn, wk) in SHAPES, (M, N, K)
+        nbytes = L.dk_gemm_tn_workspace_bytes(M, N, K)
+        if s == 1:
+            assert ks == K and nbytes == 0
+            continue
+        assert 2 <= s <= 8 and ks % 64 == 0 and ks >= 512, (M, N, K, s, ks)
+        assert (s - 1) * ks < K <= s * ks, "a split is empty or K is not covered"
+        assert -(-N // (16 * wn)) * s <= 256, "a split plan over-fills the CUs"
+        assert nbytes == s * M * N * 4
+        # without a workspace the same shape is planned unsplit
+        assert capi.gemm_plan(M, N, K, False)[2] == 1
+    assert capi.gemm_plan(65, 4096, 4096) == (0, 0, 0, 0)
+    assert L.dk_gemm_tn_workspace_bytes(65, 4096, 14336) == 0
+
+
+# (M, N, K) -> (waves along N, waves along K, splits): the measured-fastest
+# shapes of the Llama-3-8B decode projections.
+LLAMA_PICKS = {
+    (1, 6144, 4096): (2, 4, 1), (32, 6144, 4096): (2, 4, 1), (48, 6144, 4096): (6, 2, 4), (64, 6144, 4096): (6, 2, 4),
+    (1, 4096, 4096): (1, 8, 1), (32, 4096, 4096): (1, 8, 1), (48, 4096, 4096): (4, 2, 4), (64, 4096, 4096): (4, 2, 4),
+    (8, 4096, 14336): (1, 8, 1), (16, 4096, 14336): (2, 4, 2), (32, 4096, 14336): (4, 2, 4),
+    (48, 4096, 14336): (8, 1, 8), (64, 4096, 14336): (8, 1, 8),
+    (1, 28672, 4096): (7, 2, 1), (64, 28672, 4096): (7, 2, 1),
+}
+
+
+@pytest.mark.parametrize("shape", sorted(LLAMA_PICKS))
+def test_llama_projections_get_the_measured_shapes(shape):
+    assert capi.gemm_plan(*shape)[:3] == LLAMA_PICKS[shape]
+
+
+@pytest.mark.parametrize("mistake", ["fill", "limit"])
+def test_planted_mistake_is_caught(mistake):
+    """A replica with one condition changed must disagree with the library on
+    some shape: the comparison above can see both conditions."""
+    diffs = sum(capi.gemm_plan(M, N, K) != replica_plan(M, N, K, mistake=mistake) for M, N, K in _random_shapes(5000, 5))
+    assert diffs > 0
+
+
+def test_plan_validation():
+    L = capi.lib()
+    assert L.dk_gemm_tn_plan(0, 8, 64, 1, None) == capi.HIP_ERROR_INVALID_VALUE
+    with pytest.raises(ValueError, match="positive"):
+        capi.gemm_plan(0, 8, 64)
+    with pytest.raises(ValueError, match="positive"):
+        capi.gemm_plan(4, 8, -8)
+
+
+# One shape per (row tiles, workgroup shape, split or not) the plan reaches,
+# each with N not a multiple of the workgroup's columns; run on the GPU
+# against the oracle by tests/test_gemm_splitk.py.
+COVERAGE_SHAPES = [
+    (1, 8, 520), (1, 8, 1032), (1, 4101, 520), (1, 2050, 1032), (1, 8200, 520), (1, 4101, 1032),
+    (1, 20000, 520), (1, 8200, 1032), (1, 28600, 520), (1, 8200, 2056), (1, 28680, 520), (16, 6150, 8200),
+    (17, 8, 520), (17, 8, 1032), (17, 4101, 520), (17, 2050, 1032), (17, 8200, 520), (17, 4101, 1032),
+    (17, 20000, 520), (17, 8200, 1032), (17, 28600, 520), (17, 8200, 2056), (17, 28680, 520), (32, 6150, 4104),
+    (33, 8, 520), (33, 8, 1032), (33, 4101, 520), (33, 2050, 1032), (33, 8200, 520), (33, 4101, 1032),
+    (33, 20000, 520), (33, 8200, 1032), (33, 28600, 520), (64, 6150, 2056), (33, 28680, 520), (64, 8, 8200),
+]
+
+
+def test_coverage_shapes_reach_every_plan():
+    reached = set()
+    for M, N, K in COVERAGE_SHAPES:
+        wn, wk, s, _ = capi.gemm_plan(M, N, K)
+        assert N % (16 * wn) != 0, (M, N, K)
+        reached.add((1 if M <= 16 else (2 if M <= 32 else 4), wn, wk, s > 1))
+    assert reached == {(mt, wn, wk, split) for mt in (1, 2, 4) for wn, wk in SHAPES for split in (False, True)}

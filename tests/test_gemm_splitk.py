@@ -1,0 +1,167 @@
+"""GPU tests of gemm_tn's skinny plans (``dk_gemm_tn_ws`` and the torch op
+``gemm_tn``, which passes it a workspace from the caching allocator).
+
+Decode shapes run one workgroup per CU, with wide column tiles and, where
+that leaves too few tiles, the K reduction split over workgroups writing fp32
+partial tiles that a second kernel sums in a fixed order. Checks: every
+(row tiles, workgroup shape, split or not) plan against the fp32 oracle with
+a bias and a ragged N, in fp16 and bf16; every partial entry written
+(workspace pre-filled with NaN); determinism (two calls equal bit for bit); a
+missing or undersized workspace runs exactly ``dk_gemm_tn``; the torch op
+equals the C-ABI call; graph replays equal the eager result.
+"""
+
+import ctypes
+
+import pytest
+import torch
+
+import decodekernels_amd as dk
+from decodekernels_amd import capi
+from parity import assert_max_abs, gemm_f32
+from test_gemm_plan import COVERAGE_SHAPES
+
+pytestmark = pytest.mark.gpu
+
+
+def _stream():
+    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+# The Llama-3-8B decode projections that split K, and ragged splits.
+SPLIT_SHAPES = [
+    (64, 4096, 14336),  # MLP down projection: 8 waves along N, 8 splits
+    (32, 4096, 14336),  # 4 splits
+    (16, 4096, 14336),  # 2 splits
+    (64, 4096, 4096),  # attention output projection: 4 splits
+    (48, 6144, 4096),  # fused qkv projection: 6 x 2 waves, 4 splits
+    (17, 1000, 8200),  # ragged N and K, the last split shorter
+    (33, 4101, 4104),  # N not a multiple of 4 (scalar reduce)
+    (64, 8, 1024),  # one N tile
+]
+
+
+def _operands(M, N, K, dtype, seed):
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    a = torch.randn(M, K, generator=g, device="cuda", dtype=dtype)
+    b = torch.randn(N, K, generator=g, device="cuda", dtype=dtype) / K**0.5
+    bias = torch.randn(N, generator=g, device="cuda", dtype=dtype)
+    return a, b, bias
+
+
+def _call(fn, a, b, bias, c, *ws):
+    M, K = a.shape
+    N = b.shape[0]
+    rc = fn(capi.dtype_code(a.dtype), a.data_ptr(), b.data_ptr(), None if bias is None else bias.data_ptr(),
+            c.data_ptr(), M, N, K, a.stride(0), b.stride(0), c.stride(0), *ws, _stream())
+    assert rc == 0, capi.last_error()
+
+
+def _ws_call(a, b, bias, c, ws, nbytes):
+    _call(capi.lib().dk_gemm_tn_ws, a, b, bias, c, None if ws is None else ws.data_ptr(), nbytes)
+
+
+@pytest.mark.parametrize("M,N,K", COVERAGE_SHAPES)
+def test_every_plan_against_the_oracle(M, N, K):
+    dtype = torch.bfloat16 if (M + N) % 2 else torch.float16
+    a, b, bias = _operands(M, N, K, dtype, M * 131 + N)
+    plan = capi.gemm_plan(M, N, K)
+    print(f"gemm plan {M}x{N}x{K}: {plan}", flush=True)
+    assert_max_abs(dk.gemm(a, b, bias), gemm_f32(a, b, bias), dtype, f"gemm {M}x{N}x{K} plan {plan}")
+    if plan[2] > 1:  # the same shape unsplit (no workspace)
+        c = torch.empty(M, N, device="cuda", dtype=dtype)
+        _call(capi.lib().dk_gemm_tn, a, b, bias, c)
+        assert_max_abs(c, gemm_f32(a, b, bias), dtype, f"gemm {M}x{N}x{K} unsplit")
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("M,N,K", SPLIT_SHAPES)
+def test_split_k_parity_and_determinism(dtype, M, N, K):
+    L = capi.lib()
+    splits = capi.gemm_plan(M, N, K)[2]
+    assert splits > 1
+    nbytes = L.dk_gemm_tn_workspace_bytes(M, N, K)
+    assert nbytes == splits * M * N * 4
+    a, b, bias = _operands(M, N, K, dtype, M * 31 + K)
+    ws = torch.full((nbytes // 4,), float("nan"), device="cuda")
+    c1 = torch.empty(M, N, device="cuda", dtype=dtype)
+    c2 = torch.empty_like(c1)
+    _ws_call(a, b, bias, c1, ws, nbytes)
+    ws.fill_(float("nan"))
+    _ws_call(a, b, bias, c2, ws, nbytes)
+    torch.cuda.synchronize()
+    assert torch.equal(c1, c2), "split-K result is not deterministic"
+    assert_max_abs(c1, gemm_f32(a, b, bias), dtype, f"gemm split-K {M}x{N}x{K}")
+    # the torch op takes its workspace from the caching allocator: same kernels
+    assert torch.equal(dk.gemm(a, b, bias), c1)
+    _ws_call(a, b, None, c2, ws, nbytes)
+    assert_max_abs(c2, gemm_f32(a, b), dtype, f"gemm split-K {M}x{N}x{K} no bias")
+
+
+@pytest.mark.parametrize("M,N,K", SPLIT_SHAPES[:4])
+def test_missing_or_small_workspace_runs_the_unsplit_kernel(M, N, K):
+    L = capi.lib()
+    dtype = torch.bfloat16
+    nbytes = L.dk_gemm_tn_workspace_bytes(M, N, K)
+    a, b, bias = _operands(M, N, K, dtype, 5)
+    want = torch.empty(M, N, device="cuda", dtype=dtype)
+    _call(L.dk_gemm_tn, a, b, bias, want)
+    ws = torch.empty(nbytes // 4, device="cuda")
+    for buf, size in [(None, 0), (None, nbytes), (ws, nbytes - 4)]:
+        got = torch.empty_like(want)
+        _ws_call(a, b, bias, got, buf, size)
+        torch.cuda.synchronize()
+        assert torch.equal(got, want), (buf is None, size)
+
+
+def test_unsplit_shapes_ignore_the_workspace():
+    """Shapes planned unsplit (any workspace) run dk_gemm_tn's kernel."""
+    L = capi.lib()
+    ws = torch.empty(1 << 20, device="cuda")
+    for M, N, K in [(8, 4096, 14336), (32, 6144, 4096), (64, 28672, 4096), (40, 33000, 1032), (128, 4096, 4096)]:
+        assert L.dk_gemm_tn_workspace_bytes(M, N, K) == 0
+        a, b, bias = _operands(M, N, K, torch.bfloat16, M + N)
+        want = torch.empty(M, N, device="cuda", dtype=torch.bfloat16)
+        got = torch.empty_like(want)
+        _call(L.dk_gemm_tn, a, b, bias, want)
+        _ws_call(a, b, bias, got, ws, ws.numel() * 4)
+        torch.cuda.synchronize()
+        assert torch.equal(got, want), (M, N, K)
+
+
+def test_split_k_strided_rows_and_ldc():
+    """Row strides past K for A and B, and an output of odd row stride."""
+    M, N, K = 40, 1500, 8192
+    g = torch.Generator(device="cuda").manual_seed(9)
+    a_buf = torch.randn(M, K + 64, generator=g, device="cuda", dtype=torch.bfloat16)
+    b_buf = torch.randn(N, K + 8, generator=g, device="cuda", dtype=torch.bfloat16) / K**0.5
+    a, b = a_buf[:, :K], b_buf[:, :K]
+    c_buf = torch.full((M, N + 3), 3.0, device="cuda", dtype=torch.bfloat16)
+    assert capi.lib().dk_gemm_tn_workspace_bytes(M, N, K) > 0
+    torch.ops.decode_kernels.gemm_tn(c_buf[:, :N], a, b, None)
+    assert_max_abs(c_buf[:, :N], gemm_f32(a, b), torch.bfloat16, f"gemm split-K {M}x{N}x{K} strided")
+    assert (c_buf[:, N:] == 3.0).all()
+
+
+def test_split_k_graph_replay():
+    """The torch op (workspace from the caching allocator) captured in a graph:
+    every replay, with eager work between replays, equals the eager result."""
+    M, N, K = 64, 4096, 14336
+    a, b, bias = _operands(M, N, K, torch.bfloat16, 77)
+    want = dk.gemm(a, b, bias)
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        dk.gemm(a, b, bias)  # warm the allocator on this stream
+    torch.cuda.current_stream().wait_stream(s)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out = dk.gemm(a, b, bias)
+    for i in range(3):
+        out.fill_(float("nan"))
+        noise = torch.randn(M, N, device="cuda", dtype=torch.bfloat16)  # eager work between replays
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, want), f"replay {i}"
+        del noise

@@ -19,6 +19,9 @@ def test_library_exports_every_declared_symbol():
         "dk_paged_attention_decode",
         "dk_paged_attention_decode_fp8",
         "dk_gemm_tn",
+        "dk_gemm_tn_workspace_bytes",
+        "dk_gemm_tn_plan",
+        "dk_gemm_tn_ws",
         "dk_rms_norm",
         "dk_fused_add_rms_norm",
         "dk_silu_and_mul",
@@ -128,6 +131,25 @@ def test_capi_gemm_validation():
     assert L.dk_gemm_tn(capi.DK_BFLOAT16, 0x1000, 0x1000, None, 0x1000, 4, 0, 64, 64, 64, 8, None) == 0
     rc = L.dk_gemm_tn(5, 0x1000, 0x1000, None, 0x1000, 4, 8, 64, 64, 64, 8, None)
     assert rc == capi.HIP_ERROR_INVALID_VALUE and "float16 or bfloat16" in capi.last_error()
+
+
+def test_capi_gemm_workspace_sizes_and_validation():
+    """Split-K workspace sizes (splits x M x N fp32) for decode shapes the plan
+    splits, 0 for the rest; argument errors of dk_gemm_tn_ws."""
+    L = capi.lib()
+    for M, N, K, splits in [(64, 4096, 14336, 8), (32, 4096, 14336, 4), (16, 4096, 14336, 2), (64, 4096, 4096, 4),
+                            (64, 6144, 4096, 4), (17, 1000, 8200, 4), (8, 4096, 14336, 0), (32, 4096, 4096, 0),
+                            (32, 6144, 4096, 0), (64, 28672, 4096, 0), (65, 4096, 14336, 0), (0, 8, 64, 0)]:
+        assert L.dk_gemm_tn_workspace_bytes(M, N, K) == splits * M * N * 4, (M, N, K)
+    rc = L.dk_gemm_tn_ws(capi.DK_BFLOAT16, 0x1000, 0x1000, None, 0x1000, 64, 4096, 14336, 14336, 14336, 4096,
+                         0x1008, 1 << 23, None)
+    assert rc == capi.HIP_ERROR_INVALID_VALUE and "workspace must be 16-byte aligned" in capi.last_error()
+    rc = L.dk_gemm_tn_ws(capi.DK_BFLOAT16, 0x1000, 0x1000, None, 0x1000, 64, 4096, 14336, 14336, 14336, 4096,
+                         0x1000, -1, None)
+    assert rc == capi.HIP_ERROR_INVALID_VALUE and "non-negative" in capi.last_error()
+    rc = L.dk_gemm_tn_ws(capi.DK_FLOAT16, 0x1000, 0x1000, None, 0x1000, 4, 8, 100, 100, 100, 8, None, 0, None)
+    assert rc == capi.HIP_ERROR_INVALID_VALUE and "multiples of 8" in capi.last_error()
+    assert L.dk_gemm_tn_ws(capi.DK_FLOAT16, 0x1000, 0x1000, None, 0x1000, 0, 8, 64, 64, 64, 8, None, 0, None) == 0
 
 
 def test_capi_norm_validation():

@@ -470,7 +470,7 @@ def test_gemm(dtype, M, N, K, with_bias):
     assert_max_abs(dk.gemm(a, b, bias), gemm_f32(a, b, bias), dtype, f"gemm {M}x{N}x{K}")
 
 
-@pytest.mark.parametrize("M", [1, 8, 32, 64, 4096])
+@pytest.mark.parametrize("M", [1, 8, 16, 32, 48, 64, 4096])
 @pytest.mark.parametrize("N", [6144, 4096, 28672])
 def test_gemm_decode_layer_shapes(M, N):
     """The bf16 decode-layer projections (K=4096, A and B ~ N(0, 0.02)); the
@@ -488,7 +488,7 @@ def _gemm_f32_gpu(a, b):
     return torch.mm(a.float(), b.float().t().contiguous())
 
 
-@pytest.mark.parametrize("M", [1, 64, 4096])
+@pytest.mark.parametrize("M", [1, 16, 32, 48, 64, 4096])
 def test_gemm_down_projection_k14336(M):
     """The decode layer's down projection (N = 4096, K = 14336), bf16."""
     g = torch.Generator(device="cuda").manual_seed(M + 14336)
@@ -498,19 +498,19 @@ def test_gemm_down_projection_k14336(M):
     assert_max_abs(dk.gemm(a, b), ref, torch.bfloat16, f"gemm down {M}x4096x14336")
 
 
-# Every (row tiles, waves along N) pair the skinny launch policy picks, with
-# ragged N and K: M <= 16 splits N into >= 384 workgroups (1/2/4 waves along
-# N at N < 12288 / < 24576 / above), 16 < M <= 64 into >= 192 (1/2/4 waves,
-# and 8 for M > 32 with N >= 24576).
+# Skinny shapes with ragged N and K around the plan's boundaries (unsplit
+# grids of 1 ... 8 waves along N, the wide plan past N = 32768 at M = 64);
+# tests/test_gemm_splitk.py runs one shape per plan the launcher can pick.
 SKINNY_POLICY_SHAPES = [
-    (1, 12328, 520),  # 1 row tile, 2 waves along N
-    (16, 24600, 136),  # 1 row tile, 4 waves along N
-    (17, 6152, 1032),  # 2 row tiles, 2 waves along N
-    (32, 12296, 136),  # 2 row tiles, 4 waves along N
-    (33, 1000, 4104),  # 4 row tiles, 1 wave along N
-    (40, 6168, 520),  # 4 row tiles, 2 waves along N
-    (63, 12304, 136),  # 4 row tiles, 4 waves along N
-    (64, 24584, 136),  # 4 row tiles, 8 waves along N
+    (1, 12328, 520),
+    (16, 24600, 136),
+    (17, 6152, 1032),
+    (32, 12296, 136),
+    (33, 1000, 4104),
+    (40, 6168, 520),
+    (63, 12304, 136),
+    (64, 24584, 136),
+    (64, 33000, 136),
 ]
 
 
