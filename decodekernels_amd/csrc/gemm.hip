@@ -60,6 +60,9 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base, int64_t
 // DEPTH-deep register rings. All waves step through the chunks together (one
 // barrier per step); the WK partial tiles are summed through LDS at the end.
 constexpr int kLdsBK = 64;
+#ifndef DK_SKINNY_ROT
+#define DK_SKINNY_ROT 5  // unsplit K walk of workgroup x starts at chunk (x * DK_SKINNY_ROT) mod chunks
+#endif
 constexpr int kLdsARow = kLdsBK + 8;  // padded LDS row (elements)
 
 template <int MT, int WN>
@@ -111,17 +114,31 @@ __global__ __launch_bounds__(WN * WK * kWave) void gemm_skinny_lds_kernel(const 
 
   const int n_chunks = (ke - kb + kLdsBK - 1) / kLdsBK;
   const int steps = (n_chunks + WK - 1) / WK;  // chunk steps of the whole workgroup
+  // Unsplit, every workgroup walks the whole K range in lockstep with the
+  // others: at a given moment they read the same column offset of rows a
+  // fixed stride apart, which at some base addresses lands on few HBM
+  // channels (measured: qkv M=1 18.3 us at 11 of 12 weight placements, 14.9 at
+  // the twelfth). Starting workgroup x's walk at chunk x * DK_SKINNY_ROT mod
+  // n_chunks spreads the concurrent reads: 14.3-14.6 us at every placement,
+  // gate_up M=16 54.5 -> 44.0 us. Split workgroups already start at different
+  // K offsets (rotating them measured 1-5% slower). Chunk c of the walk reads
+  // K chunk (c + rot) mod n_chunks; the partial sums are deterministic.
+  const int rot = DK_SKINNY_ROT > 0 && part == nullptr && n_chunks > 0
+                      ? static_cast<int>((blockIdx.x * static_cast<unsigned>(DK_SKINNY_ROT)) % n_chunks)
+                      : 0;
+  auto chunk = [&](int c) { return c + rot >= n_chunks ? c + rot - n_chunks : c + rot; };
 
   // Activation tile of chunk c: vector v of the group covers row v / 8, columns 8 (v % 8) ...
   auto load_a = [&](int step, AR& r) {
     const int c = step * WK + wk;
     const bool live = step < steps && c < n_chunks;
     const __amdgpu_buffer_rsrc_t rr = live ? ra : r_none;
+    const int cc = chunk(c);
 #pragma unroll
     for (int j = 0; j < AR::kPerLane; ++j) {
       const int v = gl + j * WN * kWave;
       const int row = v / 8;
-      const int k = kb + c * kLdsBK + 8 * (v % 8);
+      const int k = kb + cc * kLdsBK + 8 * (v % 8);
       const bool in = k < ke && (!AR::kPartial || v < AR::kVecs);
       r.v[j] = __builtin_amdgcn_raw_buffer_load_b128(rr, in ? row * lda * 2 + 2 * k : kOutOfRange, 0, 0);
     }
@@ -138,10 +155,11 @@ __global__ __launch_bounds__(WN * WK * kWave) void gemm_skinny_lds_kernel(const 
     const int c = step * WK + wk;
     const bool live = step < steps && c < n_chunks;
     const __amdgpu_buffer_rsrc_t rr = live ? rb : r_none;
+    const int cc = chunk(c);
 #pragma unroll
     for (int s = 0; s < KS; ++s) {
-      const int k = kb + c * kLdsBK + 32 * s + 8 * lg;
-      bf[s] = __builtin_amdgcn_raw_buffer_load_b128(rr, k < ke ? boff + 2 * (kb + c * kLdsBK + 32 * s) : kOutOfRange, 0,
+      const int k = kb + cc * kLdsBK + 32 * s + 8 * lg;
+      bf[s] = __builtin_amdgcn_raw_buffer_load_b128(rr, k < ke ? boff + 2 * (kb + cc * kLdsBK + 32 * s) : kOutOfRange, 0,
                                                     0);
     }
   };
