@@ -22,7 +22,8 @@ sample before anything is reported.
 
 ``extras``: the other BASELINE configs -- 128K-token split-K decode (fp16,
 batch 1 and 4, HND cache, 1% outlier rows), the head-dim-256 / group-8 stress
-batch, gemm_tn at the decode-layer shapes next to hipBLASLt (``F.linear``),
+batch, gemm_tn at the decode-layer shapes next to hipBLASLt (``F.linear``; the
+two timed interleaved, call by call, so that drift moves both alike),
 the norm / activation ops, and one Llama-3-8B decoder layer's decode step
 end to end, RoPE and the cache write included (eager and HIP graph) -- each op timed as the median of cold-cache calls
 (a 1 GiB buffer is read before every call, 4x the 256 MB Infinity
@@ -186,6 +187,33 @@ def time_cold(fn, iters: int = 30, warmup: int = 3) -> dict:
             "p90_us": round(us[int(0.9 * (iters - 1))], 2), "mean_us": round(statistics.fmean(us), 2)}
 
 
+def time_cold_interleaved(fns: dict, iters: int = 30, warmup: int = 3) -> dict:
+    """time_cold for several ops at once, the calls interleaved (one call of
+    each per round, caches flushed before each), so that clock or thermal
+    drift during the run moves every op's figures alike. Returns
+    {name: time_cold-style stats}."""
+    for _ in range(warmup):
+        for fn in fns.values():
+            fn()
+    torch.cuda.synchronize()
+    events = {name: [] for name in fns}
+    for _ in range(iters):
+        for name, fn in fns.items():
+            s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            flush_caches()
+            s.record()
+            fn()
+            e.record()
+            events[name].append((s, e))
+    torch.cuda.synchronize()
+    out = {}
+    for name, lst in events.items():
+        us = sorted(s.elapsed_time(e) * 1e3 for s, e in lst)
+        out[name] = {"median_us": round(statistics.median(us), 2), "p10_us": round(us[int(0.1 * (iters - 1))], 2),
+                     "p90_us": round(us[int(0.9 * (iters - 1))], 2), "mean_us": round(statistics.fmean(us), 2)}
+    return out
+
+
 # ---------------------------------------------------------------------------
 # Correctness before timing: every timed op is first compared with the oracle
 # ---------------------------------------------------------------------------
@@ -282,8 +310,8 @@ def extras_gemm() -> dict:
     torch.backends.cuda.preferred_blas_library("cublaslt")  # hipBLASLt on ROCm
     res = {}
     g = torch.Generator(device="cuda").manual_seed(30)
-    for name, n, k, ms in (("qkv", 6144, 4096, (1, 8, 32, 64, 256, 4096)), ("o", 4096, 4096, (1, 8, 32, 64, 256, 4096)),
-                           ("gate_up", 28672, 4096, (1, 8, 32, 64, 256, 4096)), ("down", 4096, 14336, (64, 256, 4096))):
+    ms = (1, 8, 32, 64, 256, 4096)
+    for name, n, k in (("qkv", 6144, 4096), ("o", 4096, 4096), ("gate_up", 28672, 4096), ("down", 4096, 14336)):
         w = torch.randn(n, k, generator=g, device="cuda", dtype=torch.bfloat16) * 0.02
         for m in ms:
             a = torch.randn(m, k, generator=g, device="cuda", dtype=torch.bfloat16) * 0.02
@@ -294,8 +322,9 @@ def extras_gemm() -> dict:
             if err > 2e-2:
                 raise AssertionError(f"gemm {name} M={m}: max abs err {err:.3e} vs hipBLASLt before timing")
             iters = 10 if m == 4096 else 30
-            t_dk = time_cold(lambda: torch.ops.decode_kernels.gemm_tn(out, a, w, None), iters=iters)
-            t_bl = time_cold(lambda: F.linear(a, w), iters=iters)
+            t = time_cold_interleaved({"dk": lambda: torch.ops.decode_kernels.gemm_tn(out, a, w, None),
+                                       "hipblaslt": lambda: F.linear(a, w)}, iters=iters)
+            t_dk, t_bl = t["dk"], t["hipblaslt"]
             flops = 2.0 * m * n * k
             nbytes = (m * k + n * k + m * n) * 2
             res[f"{name}_M{m}"] = {
