@@ -20,6 +20,11 @@ restated in ``oracle/reference.py``) timed on this host's cores over a bounded
 sample of the same workload; the GPU output is checked against it on that
 sample before anything is reported.
 
+Each extra also carries ``cpu_path``: the reference's CPU path for that op
+(the oracle, torch on all host cores) timed in the same run on the same inputs
+(attention: the sequences checked before timing; GEMM: one to three calls;
+norms: eleven), with the thread count -- skipped with ``--no-cpu``.
+
 ``extras``: the other BASELINE configs -- 128K-token split-K decode (fp16,
 batch 1 and 4, HND cache, 1% outlier rows), the head-dim-256 / group-8 stress
 batch, gemm_tn at the decode-layer shapes next to hipBLASLt (``F.linear``; the
@@ -217,10 +222,46 @@ def time_cold_interleaved(fns: dict, iters: int = 30, warmup: int = 3) -> dict:
 # ---------------------------------------------------------------------------
 # Correctness before timing: every timed op is first compared with the oracle
 # ---------------------------------------------------------------------------
-def check_attention(c, what: str, sample: int = 4) -> float:
+# Whether the extras also time the reference's CPU path (off with --no-cpu).
+CPU_PATH = True
+
+
+def cpu_threads() -> int:
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    return cores
+
+
+def cpu_entry(seconds: float, calls: int, what: str, nbytes: float = 0.0, flops: float = 0.0) -> dict:
+    """The reference's CPU path (the oracle, torch on the host's cores) on the
+    same op: microseconds per call and the matching rate."""
+    us = seconds / calls * 1e6
+    out = {"us_per_call": round(us, 1), "threads": torch.get_num_threads(), "sample": what}
+    if nbytes:
+        out["GB/s"] = round(nbytes / (us * 1e-6) / 1e9, 2)
+    if flops:
+        out["TFLOP/s"] = round(flops / (us * 1e-6) / 1e12, 3)
+    return out
+
+
+def time_cpu(fn, calls: int, warmup: int = 1) -> float:
+    """Median seconds of `calls` host calls after `warmup` untimed ones."""
+    for _ in range(warmup):
+        fn()
+    ts = []
+    for _ in range(calls):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return statistics.median(ts)
+
+
+def check_attention(c, what: str, sample: int = 4, cpu: dict | None = None) -> float:
     """Runs the case once and compares up to `sample` sequences (the longest
     first) with the CPU oracle at the parity bar (2e-2 bf16 / 5e-3 fp16, or
-    half an ulp where that is larger). Returns the max abs error."""
+    half an ulp where that is larger). Returns the max abs error. With `cpu` a
+    dict, the oracle calls are timed there too (the reference's CPU path on
+    those sequences: seconds, algorithmic bytes, sequences)."""
     from oracle.reference import paged_attention_reference
 
     c["run"]()
@@ -239,7 +280,14 @@ def check_attention(c, what: str, sample: int = 4) -> float:
         blocks = c["bt"][s, : -(-c["seq_lens"][s] // k.shape[1])].long()
         ks, vs = gather(k, blocks, c["k_scale"]), gather(v, blocks, c["v_scale"])
         bt = torch.arange(blocks.numel(), dtype=torch.int32)[None]
-        ref = paged_attention_reference(c["q"][s : s + 1].float().cpu(), ks, vs, bt, lens[s : s + 1])[0]
+        qs = c["q"][s : s + 1].float().cpu()
+        t0 = time.perf_counter()
+        ref = paged_attention_reference(qs, ks, vs, bt, lens[s : s + 1])[0]
+        if cpu is not None:
+            cpu["s"] = cpu.get("s", 0.0) + time.perf_counter() - t0
+            cpu["bytes"] = cpu.get("bytes", 0) + (int(lens[s]) * 2 * k.shape[2] * k.shape[3] * k.element_size()
+                                                  + 2 * c["q"].shape[1] * c["q"].shape[2] * c["q"].element_size())
+            cpu["seqs"] = cpu.get("seqs", 0) + 1
         got = c["out"][s].float().cpu()
         err = (got - ref).abs()
         bar = half_ulp_bar(ref, c["dtype"])
@@ -268,26 +316,44 @@ def ulps(a: torch.Tensor, b: torch.Tensor) -> int:
 # ---------------------------------------------------------------------------
 # Extras
 # ---------------------------------------------------------------------------
+def attention_cpu_path(cpu: dict, num_seqs: int, fp8: bool = False) -> dict:
+    """The `cpu_path` entry of an attention extra from check_attention's timing."""
+    if not cpu:
+        return {}
+    what = (f"oracle.reference.paged_attention_reference (torch CPU, fp32) on the {cpu['seqs']} longest of "
+            f"{num_seqs} sequences, one call each ({cpu['bytes'] / 1e6:.0f} MB of "
+            f"{'fp8' if fp8 else '16-bit'} KV; the reference has no fp8 path, so its input is the dequantised "
+            "cache)" if fp8 else f"oracle.reference.paged_attention_reference (torch CPU, fp32) on the {cpu['seqs']} "
+            f"longest of {num_seqs} sequences, one call each ({cpu['bytes'] / 1e6:.0f} MB of KV)")
+    entry = cpu_entry(cpu["s"], cpu["seqs"], what, nbytes=cpu["bytes"] / cpu["seqs"])
+    entry["us_per_sequence"] = entry.pop("us_per_call")
+    return {"cpu_path": entry}
+
+
 def extras_attention() -> dict:
     res = {}
     for b in (1, 4):
         c = attention_case(b, 32, 8, 128, 16, [131072] * b, torch.float16, "hnd", seed=10 + b, outlier_frac=0.01)
-        err = check_attention(c, f"128K batch {b}", sample=1)
+        cpu = {}
+        err = check_attention(c, f"128K batch {b}", sample=1, cpu=cpu if CPU_PATH else None)
         t = time_cold(c["run"], iters=20)
         gbs = c["bytes"] / (t["median_us"] * 1e-6) / 1e9
         res[f"split_k_128k_b{b}_fp16"] = {**t, "GB/s": round(gbs, 1), "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 1),
-                                           "MB": round(c["bytes"] / 1e6, 1), "checked_max_abs_err": err}
+                                           "MB": round(c["bytes"] / 1e6, 1), "checked_max_abs_err": err,
+                                           **attention_cpu_path(cpu, len(c["seq_lens"]))}
         progress(f"128K batch {b}: {t['median_us']} us (checked, max abs err {err:.2e})")
         del c
     lens = c5_seq_lens()
     for dtype, tag in ((torch.float16, "fp16"), (torch.bfloat16, "bf16")):
         c = attention_case(256, 16, 2, 256, 32, lens, dtype, "nhd", seed=20, nhd_pad=64)
-        err = check_attention(c, f"D=256 stress {tag}")
+        cpu = {}
+        err = check_attention(c, f"D=256 stress {tag}", cpu=cpu if CPU_PATH else None)
         t = time_cold(c["run"], iters=20)
         gbs = c["bytes"] / (t["median_us"] * 1e-6) / 1e9
         res[f"d256_g8_stress_{tag}"] = {**t, "GB/s": round(gbs, 1), "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 1),
                                         "MB": round(c["bytes"] / 1e6, 1), "checked_max_abs_err": err,
-                                        "kv_layout": "strided NHD [blocks, 32, 2, 256 + 64][..., :256]"}
+                                        "kv_layout": "strided NHD [blocks, 32, 2, 256 + 64][..., :256]",
+                                        **attention_cpu_path(cpu, len(c["seq_lens"]))}
         progress(f"D=256 stress {tag}: {t['median_us']} us (checked, max abs err {err:.2e})")
         del c
     # fp8 (e4m3fn) KV cache, bf16 queries: the headline batch and 128K batch 1
@@ -296,23 +362,28 @@ def extras_attention() -> dict:
     for name, args in (("fp8_kv_llama3_8b_b64", (64, 32, 8, 128, 16, llama_lens, torch.bfloat16, "vllm")),
                        ("fp8_kv_128k_b1", (1, 32, 8, 128, 16, [131072], torch.bfloat16, "hnd"))):
         c = attention_case(*args, seed=60, q_scale=128**-0.5, kv_dtype=torch.float8_e4m3fn, k_scale=0.5, v_scale=0.5)
-        err = check_attention(c, name, sample=1 if len(args[5]) == 1 else 4)
+        cpu = {}
+        err = check_attention(c, name, sample=1 if len(args[5]) == 1 else 4, cpu=cpu if CPU_PATH else None)
         t = time_cold(c["run"], iters=20)
         gbs = c["bytes"] / (t["median_us"] * 1e-6) / 1e9
         res[name] = {**t, "GB/s": round(gbs, 1), "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 1),
-                     "MB": round(c["bytes"] / 1e6, 1), "checked_max_abs_err": err}
+                     "MB": round(c["bytes"] / 1e6, 1), "checked_max_abs_err": err,
+                     **attention_cpu_path(cpu, len(c["seq_lens"]), fp8=True)}
         progress(f"{name}: {t['median_us']} us (checked, max abs err {err:.2e})")
         del c
     return res
 
 
 def extras_gemm() -> dict:
+    from oracle.reference import gemm_reference
+
     torch.backends.cuda.preferred_blas_library("cublaslt")  # hipBLASLt on ROCm
     res = {}
     g = torch.Generator(device="cuda").manual_seed(30)
     ms = (1, 8, 32, 64, 256, 4096)
     for name, n, k in (("qkv", 6144, 4096), ("o", 4096, 4096), ("gate_up", 28672, 4096), ("down", 4096, 14336)):
         w = torch.randn(n, k, generator=g, device="cuda", dtype=torch.bfloat16) * 0.02
+        w_c = w.cpu() if CPU_PATH else None
         for m in ms:
             a = torch.randn(m, k, generator=g, device="cuda", dtype=torch.bfloat16) * 0.02
             out = torch.empty(m, n, device="cuda", dtype=torch.bfloat16)
@@ -333,10 +404,17 @@ def extras_gemm() -> dict:
                 "TFLOP/s": round(flops / (t_dk["median_us"] * 1e-6) / 1e12, 1),
                 "GB/s": round(nbytes / (t_dk["median_us"] * 1e-6) / 1e9, 1),
             }
+            if CPU_PATH:
+                a_c = a.cpu()
+                calls = 1 if m == 4096 else 3
+                sec = time_cpu(lambda: gemm_reference(a_c, w_c), calls, warmup=0 if m == 4096 else 1)
+                res[f"{name}_M{m}"]["cpu_path"] = cpu_entry(
+                    sec, 1, f"oracle.reference.gemm_reference (torch CPU, fp32 F.linear on the bf16 inputs), median "
+                    f"of {calls} call{'s' if calls > 1 else ''}", nbytes=nbytes, flops=flops)
             if m == 4096:
                 res[f"{name}_M{m}"]["pct_mfma_peak"] = round(100 * res[f"{name}_M{m}"]["TFLOP/s"] / BF16_PEAK_TFLOPS, 1)
         progress(f"gemm {name}: " + ", ".join(f"M={m} {res[f'{name}_M{m}']['dk_over_hipblaslt']}x" for m in ms))
-        del w
+        del w, w_c
     return res
 
 
@@ -373,6 +451,17 @@ def extras_norms() -> dict:
     ):
         tm = time_cold(fn, iters=50)
         res[name] = {**tm, "GB/s": round(nbytes / (tm["median_us"] * 1e-6) / 1e9, 1), "checked_max_ulp": checked[name]}
+    if CPU_PATH:
+        x_c, r_c, w_c, xs_c = x.cpu(), r.cpu(), w.cpu(), xs.cpu()
+        for name, fn, nbytes, ref in (
+            ("rms_norm_64x4096", lambda: rms_norm_reference(x_c, w_c, 1e-5), 2 * t * h * 2, "rms_norm_reference"),
+            ("fused_add_rms_norm_64x4096", lambda: fused_add_rms_norm_reference(x_c, r_c, w_c, 1e-5), 4 * t * h * 2,
+             "fused_add_rms_norm_reference"),
+            ("silu_and_mul_64x2x14336", lambda: silu_and_mul_reference(xs_c), 3 * t * d * 2, "silu_and_mul_reference"),
+        ):
+            sec = time_cpu(fn, 11, warmup=2)
+            res[name]["cpu_path"] = cpu_entry(sec, 1, f"oracle.reference.{ref} (torch CPU, fp32), median of 11 calls",
+                                              nbytes=nbytes)
     return res
 
 
@@ -703,6 +792,10 @@ def main() -> int:
         pmc_workload()
         return 0
 
+    global CPU_PATH
+    CPU_PATH = not args.no_cpu
+    if CPU_PATH:
+        cpu_threads()
     case = llama3_8b_decode_case()
     headline_err = check_attention(case, "headline (Llama-3-8B batch 64)", sample=8)
     # K timed steps, each from cold caches (a 1 GiB read before every call,
