@@ -551,17 +551,20 @@ inline SkinnyPlan skinny_plan_unsplit(int M, int N, int K) {
 //     bytes) of activations, or failing that the fewest activation bytes;
 //  3. else the unsplit grid of 1, or for N > 32768 (no grid of one workgroup
 //     per CU) the wide plan.
-// Picks (waves along N x along K, splits; us cold, vs hipBLASLt): qkv (N 6144,
-// K 4096) M <= 32: 2 x 4, unsplit (15.2 at M = 1, 18.2 at M = 32; 0.90 /
-// 1.01x), M = 48/64: 6 x 2, 4 splits (20.0 / 21.0; 0.98 / 1.02x); o (N 4096)
-// M <= 32: 1 x 8, unsplit (12.3 ... 15.0; 0.68 ... 0.94x), M = 48/64: 4 x 2,
-// 4 splits (16.5 / 16.8; 0.97 / 0.94x); down (N 4096, K 14336) M <= 8: 1 x 8
-// (24.8 / 25.0; 0.94x), M = 16/32: 2 x 4 / 4 x 2 with 2 / 4 splits (27.6 /
-// 29.6; 1.02 / 0.91x), M = 48/64: 8 x 1, 8 splits (32.0 / 33.1; 0.84 /
-// 0.66x); gate_up (N 28672): 7 x 2, unsplit. Each pick was the fastest
-// candidate of its shape and M except gate_up at M <= 32, where 4 x 2 (448
-// workgroups) was 6-8% faster on one of four machines and 7 x 2 7% faster on
-// two. A 257th workgroup puts two on one CU and doubles that CU's time.
+// Picks (waves along N x along K, splits), with the unsplit K-walk rotation;
+// us cold, interleaved with hipBLASLt, ratio to it:
+//   qkv (N 6144, K 4096): M <= 32 2 x 4 unsplit, 14.4 (M=1, 0.86x) ... 18.7
+//     (M=32, 1.05x); M = 48/64 6 x 2 with 4 splits, 21.3 (M=64, 1.00x);
+//   o (N 4096): M <= 32 1 x 8 unsplit, 11.3 ... 14.6 (0.62 ... 0.93x);
+//     M = 48/64 4 x 2 with 4 splits, 16.6 (M=64, 0.93x);
+//   gate_up (N 28672): 7 x 2 unsplit, 43.9 (M=1, 0.71x) ... 51.4 (M=64, 0.92x);
+//   down (N 4096, K 14336): M <= 8 1 x 8, 24.4 (0.88x); M = 16 / 32 2 x 4 / 4 x 2
+//     with 2 / 4 splits, 29.3 (M=32, 0.86x); M = 48/64 8 x 1 with 8 splits,
+//     33.0 (M=64, 0.65x).
+// Each pick was the fastest candidate of its shape and M, except gate_up at
+// M <= 32 before the rotation: there 4 x 2 (448 workgroups) was 6-8% faster on
+// one of four machines and 7 x 2 7% faster on two. A 257th workgroup puts two
+// on one CU and doubles that CU's time.
 inline SkinnyPlan skinny_plan(int M, int N, int K, bool split_ok) {
   constexpr int64_t kKiB = 1024;
   SkinnyPlan u = skinny_plan_unsplit(M, N, K);
