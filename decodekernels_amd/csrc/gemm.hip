@@ -315,7 +315,8 @@ __global__ __launch_bounds__(WM * WN * kWave) void gemm_dma_kernel(const uint16_
                                                                    const uint16_t* __restrict__ B,
                                                                    const uint16_t* __restrict__ bias,
                                                                    uint16_t* __restrict__ C, int M, int N, int K,
-                                                                   int lda, int ldb, int ldc, int vec_store) {
+                                                                   int lda, int ldb, int ldc, int vec_store,
+                                                                   float* __restrict__ part, int k_split) {
   constexpr int NW = WM * WN;
   constexpr int TM = BM / WM / 16;  // 16-row fragments per wave
   constexpr int TN = BN / WN / 16;
@@ -333,6 +334,11 @@ __global__ __launch_bounds__(WM * WN * kWave) void gemm_dma_kernel(const uint16_
   const int l16 = lane % 16;
   const int lg = lane / 16;
 
+  // Split-K (part != nullptr): workgroup row blockIdx.y covers K columns
+  // [kb, ke) (k_split a multiple of kDmaBK) and writes its fp32 partial tile to
+  // part[blockIdx.y][M][N], without the bias; gemm_splitk_reduce_kernel sums them.
+  const int kb = part != nullptr ? static_cast<int>(blockIdx.y) * k_split : 0;
+  const int ke = part != nullptr ? min(K, kb + k_split) : K;
   const int tiles_m = (M + BM - 1) / BM;
   const int tiles_n = (N + BN - 1) / BN;
   int tm, tn;
@@ -349,7 +355,7 @@ __global__ __launch_bounds__(WM * WN * kWave) void gemm_dma_kernel(const uint16_
 
   // DMA lane roles: load j of this wave fills tile rows 8 g .. 8 g + 7 (g = wave + j NW);
   // lane l writes position l % 8 of row 8 g + l / 8, i.e. chunk (l % 8) ^ swz(row).
-  int offa[LA], ka[LA], offb[LB], kb[LB];
+  int offa[LA], ka[LA], offb[LB], kbc[LB];
 #pragma unroll
   for (int j = 0; j < LA; ++j) {
     const int r = 8 * (wave + j * NW) + lane / 8;
@@ -361,23 +367,23 @@ __global__ __launch_bounds__(WM * WN * kWave) void gemm_dma_kernel(const uint16_
   for (int j = 0; j < LB; ++j) {
     const int r = 8 * (wave + j * NW) + lane / 8;
     const int c = (lane % 8) ^ swz(r);
-    kb[j] = 8 * c;
+    kbc[j] = 8 * c;
     offb[j] = r < rows_b ? r * ldb * 2 + 16 * c : kOutOfRange;
   }
   // Issued for every slice index, also past the last one (those lanes are out
   // of range and move no data), so each wave always has the same count in flight.
   auto issue = [&](int t, int buf) {
-    const int k0 = t * kDmaBK;
+    const int k0 = kb + t * kDmaBK;
     u32x4* base = lds + buf * kSlice;
 #pragma unroll
     for (int j = 0; j < LA; ++j) {
-      const int off = (offa[j] != kOutOfRange && k0 + ka[j] < K) ? offa[j] + 2 * k0 : kOutOfRange;
+      const int off = (offa[j] != kOutOfRange && k0 + ka[j] < ke) ? offa[j] + 2 * k0 : kOutOfRange;
       __builtin_amdgcn_raw_ptr_buffer_load_lds(
           ra, (__attribute__((address_space(3))) void*)(base + (wave + j * NW) * 64), 16, off, 0, 0, 0);
     }
 #pragma unroll
     for (int j = 0; j < LB; ++j) {
-      const int off = (offb[j] != kOutOfRange && k0 + kb[j] < K) ? offb[j] + 2 * k0 : kOutOfRange;
+      const int off = (offb[j] != kOutOfRange && k0 + kbc[j] < ke) ? offb[j] + 2 * k0 : kOutOfRange;
       __builtin_amdgcn_raw_ptr_buffer_load_lds(
           rb, (__attribute__((address_space(3))) void*)(base + BM * 8 + (wave + j * NW) * 64), 16, off, 0, 0, 0);
     }
@@ -404,7 +410,7 @@ __global__ __launch_bounds__(WM * WN * kWave) void gemm_dma_kernel(const uint16_
 #pragma unroll
     for (int j = 0; j < TN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  const int ktiles = (K + kDmaBK - 1) / kDmaBK;
+  const int ktiles = (ke - kb + kDmaBK - 1) / kDmaBK;
 #pragma unroll
   for (int s = 0; s < STAGES - 1; ++s) issue(s, s);
 
@@ -459,6 +465,17 @@ __global__ __launch_bounds__(WM * WN * kWave) void gemm_dma_kernel(const uint16_
 #pragma unroll
     for (int j = 0; j < TN; ++j) {
       const int n = n0 + wn * (BN / WN) + 16 * j + 4 * lg;
+      if (part != nullptr) {
+        float* prow = part + (static_cast<int64_t>(blockIdx.y) * M + m) * N;
+        if (N % 4 == 0 && n + 3 < N) {
+          *reinterpret_cast<f32x4*>(prow + n) = acc[i][j];
+        } else {
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            if (n + r < N) prow[n + r] = acc[i][j][r];
+        }
+        continue;
+      }
       float v[4];
 #pragma unroll
       for (int r = 0; r < 4; ++r)
@@ -476,12 +493,34 @@ __global__ __launch_bounds__(WM * WN * kWave) void gemm_dma_kernel(const uint16_
 
 template <typename E, int BM, int BN, int WM, int WN, int STAGES>
 hipError_t launch_dma(const uint16_t* A, const uint16_t* B, const uint16_t* bias, uint16_t* C, int M, int N, int K,
-                      int lda, int ldb, int ldc, hipStream_t s) {
+                      int lda, int ldb, int ldc, hipStream_t s, float* part = nullptr, int splits = 1,
+                      int k_split = 0) {
   const int64_t tiles = ceil_div64(M, BM) * ceil_div64(N, BN);
   const int vec = (ldc % 4 == 0 && aligned_to(C, 8)) ? 1 : 0;
-  hipLaunchKernelGGL((gemm_dma_kernel<E, BM, BN, WM, WN, STAGES>), dim3(static_cast<unsigned>(tiles)),
-                     dim3(WM * WN * kWave), 0, s, A, B, bias, C, M, N, K, lda, ldb, ldc, vec);
+  hipLaunchKernelGGL((gemm_dma_kernel<E, BM, BN, WM, WN, STAGES>),
+                     dim3(static_cast<unsigned>(tiles), static_cast<unsigned>(part != nullptr ? splits : 1)),
+                     dim3(WM * WN * kWave), 0, s, A, B, bias, C, M, N, K, lda, ldb, ldc, vec, part,
+                     part != nullptr ? k_split : K);
+  if (part == nullptr) return hipGetLastError();
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  const int64_t threads = static_cast<int64_t>(M) * ((N + 3) / 4);
+  hipLaunchKernelGGL((gemm_splitk_reduce_kernel<E>), dim3(static_cast<unsigned>((threads + 255) / 256)), dim3(256), 0,
+                     s, part, splits, M, N, bias, C, ldc);
   return hipGetLastError();
+}
+
+using DmaLauncher = hipError_t (*)(const uint16_t*, const uint16_t*, const uint16_t*, uint16_t*, int, int, int, int,
+                                   int, int, hipStream_t, float*, int, int);
+
+// Launchers of kDmaShapes' tile shapes, in the same order.
+template <typename E>
+const DmaLauncher* dma_launchers() {
+  static const DmaLauncher fns[] = {
+      launch_dma<E, 256, 256, 4, 2, 2>, launch_dma<E, 256, 128, 4, 2, 3>, launch_dma<E, 128, 128, 4, 2, 3>,
+      launch_dma<E, 128, 64, 2, 2, 4>, launch_dma<E, 64, 64, 2, 2, 4>,
+  };
+  return fns;
 }
 
 #ifndef DK_SKINNY_DEPTH
@@ -627,6 +666,67 @@ inline int64_t skinny_workspace_bytes(const SkinnyPlan& p, int M, int N) {
   return p.splits > 1 ? static_cast<int64_t>(p.splits) * M * N * static_cast<int64_t>(sizeof(float)) : 0;
 }
 
+// Plan of the LDS-DMA kernel (M > 64): tile shape and, with a workspace, K
+// split over workgroup rows. Time model fitted to interleaved cold timings of
+// every shape x {1, 2, 4, 8} splits on the Llama-3-8B projections at M = 128,
+// 256 and 512 (mean 1.5% from the fastest, picks identical to the previous
+// unsplit model at M >= 1000):
+//   rounds(tiles x splits over 256 CUs) x tile flops per split / rate(shape)
+//   + [splits > 1] (1.84 us + splits x M x N x 8 B / 4.68 TB/s),
+// the last term the fp32 partials written and read back plus the reduce
+// launch. Splits are considered only when the unsplit grid leaves CUs idle
+// (< 256 tiles). Measured (us, cold): down (N 4096, K 14336) M = 128 73.2 ->
+// 36.6 (128 x 128, 8 splits; hipBLASLt 83.6), M = 256 73.3 -> 50.9 (256 x 128,
+// 8; 69.0), M = 512 105.3 -> 75.8 (256 x 128, 4; 100.4); o M = 128 24.6 ->
+// 19.3 (64 x 64, 2); qkv M = 256 35.8 -> 33.5 (128 x 128, 2).
+struct DmaPlan {
+  int shape, splits, k_split;
+};
+
+// Largest split-K workspace the plan asks for (bytes); larger splits are not considered.
+constexpr int64_t kDmaMaxWorkspace = int64_t{64} << 20;
+
+struct DmaShape {
+  int bm, bn;
+  double rate;  // TFLOP/s per CU
+};
+constexpr DmaShape kDmaShapes[] = {
+    {256, 256, 5.355}, {256, 128, 4.776}, {128, 128, 3.48}, {128, 64, 2.398}, {64, 64, 2.007},
+};
+
+inline DmaPlan dma_plan(int M, int N, int K, bool split_ok) {
+  DmaPlan best{0, 1, K};
+  double best_t = -1.0;
+  for (int i = 0; i < static_cast<int>(sizeof(kDmaShapes) / sizeof(kDmaShapes[0])); ++i) {
+    const DmaShape& sh = kDmaShapes[i];
+    const int64_t tiles = ceil_div64(M, sh.bm) * ceil_div64(N, sh.bn);
+    for (int s = 1; s <= 8; s *= 2) {
+      int ks = K, sp = 1;
+      if (s > 1) {
+        if (!split_ok || tiles >= kSkinnyCus || K / s < 512) break;
+        const int per = (K + s - 1) / s;
+        ks = (per + kDmaBK - 1) / kDmaBK * kDmaBK;
+        sp = (K + ks - 1) / ks;
+        if (sp < 2) continue;
+        if (static_cast<int64_t>(sp) * M * N * static_cast<int64_t>(sizeof(float)) > kDmaMaxWorkspace) break;
+      }
+      const double rounds = static_cast<double>(ceil_div64(tiles * sp, kSkinnyCus));
+      double t = rounds * sh.bm * sh.bn * 2.0 * ks / 1e6 / sh.rate;
+      if (sp > 1) t += 1.84 + static_cast<double>(sp) * M * N * 8 / 4.68e6;
+      if (best_t < 0 || t < best_t) {
+        best = DmaPlan{i, sp, ks};
+        best_t = t;
+      }
+    }
+  }
+  return best;
+}
+
+inline int64_t dma_workspace_bytes(const DmaPlan& d, int M, int N) {
+  return d.splits > 1 ? static_cast<int64_t>(d.splits) * M * N * static_cast<int64_t>(sizeof(float)) : 0;
+}
+
+
 template <typename E>
 hipError_t launch(const uint16_t* A, const uint16_t* B, const uint16_t* bias, uint16_t* C, int M, int N, int K,
                   int lda, int ldb, int ldc, void* workspace, int64_t workspace_bytes, hipStream_t s) {
@@ -661,34 +761,11 @@ hipError_t launch(const uint16_t* A, const uint16_t* B, const uint16_t* bias, ui
     }
     return hipGetLastError();
   }
-  // Tile shape by a throughput model fitted to measured bf16 runs at K = 4096
-  // and 14336: time ~ ceil(tiles / 256 CUs) x tile flops / per-CU rate of the
-  // shape (TFLOP/s). Large tiles move fewer bytes per flop through L2 and LDS;
-  // small ones keep all 256 CUs busy when M is a few hundred rows.
-  struct Shape {
-    int bm, bn;
-    double rate;
-    hipError_t (*fn)(const uint16_t*, const uint16_t*, const uint16_t*, uint16_t*, int, int, int, int, int, int,
-                     hipStream_t);
-  };
-  static const Shape shapes[] = {
-      {256, 256, 4.7, launch_dma<E, 256, 256, 4, 2, 2>},
-      {256, 128, 4.2, launch_dma<E, 256, 128, 4, 2, 3>},
-      {128, 128, 3.2, launch_dma<E, 128, 128, 4, 2, 3>},
-      {128, 64, 2.2, launch_dma<E, 128, 64, 2, 2, 4>},
-      {64, 64, 1.4, launch_dma<E, 64, 64, 2, 2, 4>},
-  };
-  const Shape* best = nullptr;
-  double best_t = 0.0;
-  for (const Shape& sh : shapes) {
-    const double rounds = static_cast<double>(ceil_div64(ceil_div64(M, sh.bm) * ceil_div64(N, sh.bn), 256));
-    const double t = rounds * sh.bm * sh.bn / sh.rate;
-    if (best == nullptr || t < best_t) {
-      best = &sh;
-      best_t = t;
-    }
-  }
-  return best->fn(A, B, bias, C, M, N, K, lda, ldb, ldc, s);
+  const DmaPlan d = dma_plan(M, N, K, workspace != nullptr);
+  const bool split = d.splits > 1 && dma_workspace_bytes(d, M, N) <= workspace_bytes;
+  const DmaPlan u = split ? d : dma_plan(M, N, K, false);
+  return dma_launchers<E>()[u.shape](A, B, bias, C, M, N, K, lda, ldb, ldc, s,
+                                     split ? static_cast<float*>(workspace) : nullptr, u.splits, u.k_split);
 }
 
 }  // namespace gemm
@@ -735,7 +812,8 @@ extern "C" int dk_gemm_tn(int dtype, const void* A, const void* B, const void* b
 }
 
 extern "C" int64_t dk_gemm_tn_workspace_bytes(int M, int N, int K) {
-  if (M <= 0 || N <= 0 || K <= 0 || M > 64) return 0;
+  if (M <= 0 || N <= 0 || K <= 0) return 0;
+  if (M > 64) return dk::gemm::dma_workspace_bytes(dk::gemm::dma_plan(M, N, K, true), M, N);
   const dk::gemm::SkinnyPlan p = dk::gemm::skinny_plan(M, N, K, true);
   return dk::gemm::skinny_workspace_bytes(p, M, N);
 }
@@ -745,7 +823,11 @@ extern "C" int dk_gemm_tn_plan(int M, int N, int K, int with_workspace, int* pla
   if (plan == nullptr) return dk::fail("gemm_tn_plan: plan must not be NULL");
   if (M <= 0 || N <= 0 || K < 0) return dk::fail("gemm_tn_plan: M and N must be positive, K non-negative");
   if (M > 64) {
-    for (int i = 0; i < 4; ++i) plan[i] = 0;
+    const dk::gemm::DmaPlan d = dk::gemm::dma_plan(M, N, K, with_workspace != 0);
+    plan[0] = dk::gemm::kDmaShapes[d.shape].bm;
+    plan[1] = dk::gemm::kDmaShapes[d.shape].bn;
+    plan[2] = d.splits;
+    plan[3] = d.k_split;
     return hipSuccess;
   }
   const dk::gemm::SkinnyPlan p = dk::gemm::skinny_plan(M, N, K, with_workspace != 0);

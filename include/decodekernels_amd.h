@@ -140,24 +140,26 @@ int64_t dk_gemm_tn_workspace_bytes(int M, int N, int K);
 
 /*
  * Launch plan of dk_gemm_tn_ws (with_workspace != 0, workspace large enough)
- * or dk_gemm_tn for M <= 64: plan[0..3] = waves along N per workgroup (16
- * columns each), waves along K, K splits, columns per split; all 0 for
- * M > 64 (tiled kernel). For tests and tuning; launches nothing.
+ * or dk_gemm_tn. For M <= 64 (skinny kernel) plan[0..3] = waves along N per
+ * workgroup (16 columns each), waves along K, K splits, columns per split;
+ * for M > 64 (tiled kernel) = tile rows, tile columns, K splits, columns per
+ * split. For tests and tuning; launches nothing.
  * No counterpart in DecodeKernels.
  */
 int dk_gemm_tn_plan(int M, int N, int K, int with_workspace, int* plan);
 
 /*
  * dk_gemm_tn with a caller-provided workspace (16-byte aligned). Decode
- * shapes (9 <= M <= 64) run one workgroup per CU with wide column tiles,
- * which cuts the activation rows each workgroup re-reads; where that leaves
- * too few column tiles (the MLP down projection, the attention output and qkv
- * projections), the K reduction is split over workgroups that write fp32
- * partial tiles to the workspace, and a second kernel sums them in a fixed
- * order, adds the bias in fp32 and rounds once: deterministic, and equal to
- * the unsplit result up to the order of the fp32 additions. A NULL workspace,
- * or one smaller than dk_gemm_tn_workspace_bytes(M, N, K), runs exactly
- * dk_gemm_tn.
+ * shapes (M <= 64) run one workgroup per CU with wide column tiles, which
+ * cuts the activation rows each workgroup re-reads; where that leaves too few
+ * column tiles (the MLP down projection, the attention output and qkv
+ * projections), and for tiled shapes (M > 64) whose tiles leave CUs idle
+ * (batched decode, M of a few hundred), the K reduction is split over
+ * workgroups that write fp32 partial tiles to the workspace (at most 64 MiB),
+ * and a second kernel sums them in a fixed order, adds the bias in fp32 and
+ * rounds once: deterministic, and equal to the unsplit result up to the
+ * order of the fp32 additions. A NULL workspace, or one smaller than
+ * dk_gemm_tn_workspace_bytes(M, N, K), runs exactly dk_gemm_tn.
  * No counterpart in DecodeKernels, whose dk::launch_gemm_tn<T>
  * (csrc/gemm_wmma.cuh:209-219) takes no workspace; the torch op gemm_tn
  * (csrc/ops.cu:149-182 there) calls this with a workspace from PyTorch's

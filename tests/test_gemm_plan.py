@@ -71,6 +71,42 @@ def replica_plan(M, N, K, with_workspace=True, mistake=None):
     return u if u is not None else _wide(M, N, K)
 
 
+DMA_SHAPES = [(256, 256, 5.355), (256, 128, 4.776), (128, 128, 3.48), (128, 64, 2.398), (64, 64, 2.007)]
+DMA_MAX_WORKSPACE = 64 << 20
+
+
+def replica_dma_plan(M, N, K, with_workspace=True):
+    """(tile rows, tile columns, splits, k_split) as dma_plan computes it (M > 64):
+    the shape and split count minimising rounds x tile flops per split / rate
+    + (1.84 us + splits M N 8 B / 4.68 TB/s when split); splits only for grids
+    of < 256 tiles, >= 512 columns each and <= 64 MiB of partials."""
+    best, best_t = None, -1.0
+    for bm, bn, rate in DMA_SHAPES:
+        tiles = -(-M // bm) * -(-N // bn)
+        s = 1
+        while s <= 8:
+            ks, sp = K, 1
+            if s > 1:
+                if not with_workspace or tiles >= 256 or K // s < 512:
+                    break
+                per = -(-K // s)
+                ks = -(-per // 64) * 64
+                sp = -(-K // ks)
+                if sp < 2:
+                    s *= 2
+                    continue
+                if sp * M * N * 4 > DMA_MAX_WORKSPACE:
+                    break
+            rounds = float(-(-(tiles * sp) // 256))
+            t = rounds * bm * bn * 2.0 * ks / 1e6 / rate
+            if sp > 1:
+                t += 1.84 + float(sp) * M * N * 8 / 4.68e6
+            if best_t < 0 or t < best_t:
+                best, best_t = (bm, bn, sp, ks), t
+            s *= 2
+    return best
+
+
 def _random_shapes(n, seed):
     rng = random.Random(seed)
     for _ in range(n):
@@ -84,6 +120,38 @@ def test_library_plans_like_the_replica():
     for M, N, K in _random_shapes(20000, 3):
         for ws in (True, False):
             assert capi.gemm_plan(M, N, K, ws) == replica_plan(M, N, K, ws), (M, N, K, ws)
+
+
+def test_tiled_plans_like_the_replica():
+    """M > 64: the tile shape and split of the LDS-DMA kernel, and the
+    workspace it asks for."""
+    L = capi.lib()
+    rng = random.Random(8)
+    for _ in range(20000):
+        M = rng.choice([rng.randint(65, 600), rng.randint(65, 5000)])
+        N = rng.choice([rng.randint(1, 2000), rng.randint(1, 30000)])
+        K = 8 * rng.randint(1, 3000)
+        for ws in (True, False):
+            plan = capi.gemm_plan(M, N, K, ws)
+            assert plan == replica_dma_plan(M, N, K, ws), (M, N, K, ws)
+        bm, bn, sp, ks = capi.gemm_plan(M, N, K)
+        assert L.dk_gemm_tn_workspace_bytes(M, N, K) == (sp * M * N * 4 if sp > 1 else 0)
+        if sp > 1:
+            assert (sp - 1) * ks < K <= sp * ks and ks % 64 == 0 and -(-M // bm) * -(-N // bn) < 256
+            assert sp * M * N * 4 <= DMA_MAX_WORKSPACE
+
+
+# (M, N, K) -> (tile rows, tile columns, splits) measured fastest at batched decode.
+TILED_PICKS = {
+    (128, 4096, 14336): (128, 128, 8), (256, 4096, 14336): (256, 128, 8), (512, 4096, 14336): (256, 128, 4),
+    (256, 6144, 4096): (128, 128, 2), (256, 28672, 4096): (256, 128, 1), (512, 6144, 4096): (128, 128, 1),
+    (4096, 4096, 4096): (256, 256, 1), (4096, 28672, 4096): (256, 256, 1),
+}
+
+
+@pytest.mark.parametrize("shape", sorted(TILED_PICKS))
+def test_batched_decode_projections_get_the_measured_tiles(shape):
+    assert capi.gemm_plan(*shape)[:3] == TILED_PICKS[shape]
 
 
 def test_plan_invariants_and_workspace_size():
@@ -101,8 +169,6 @@ def test_plan_invariants_and_workspace_size():
         assert nbytes == s * M * N * 4
         # without a workspace the same shape is planned unsplit
         assert capi.gemm_plan(M, N, K, False)[2] == 1
-    assert capi.gemm_plan(65, 4096, 4096) == (0, 0, 0, 0)
-    assert L.dk_gemm_tn_workspace_bytes(65, 4096, 14336) == 0
 
 
 # (M, N, K) -> (waves along N, waves along K, splits): the measured-fastest

@@ -98,6 +98,48 @@ def test_split_k_parity_and_determinism(dtype, M, N, K):
     assert_max_abs(c2, gemm_f32(a, b), dtype, f"gemm split-K {M}x{N}x{K} no bias")
 
 
+# Tiled (M > 64) shapes whose grid leaves CUs idle: K split over workgroup rows.
+TILED_SPLIT_SHAPES = [
+    (128, 4096, 14336),  # 128 x 128 tiles, 8 splits
+    (256, 4096, 14336),  # 256 x 128, 8 splits
+    (512, 4096, 14336),  # 256 x 128, 4 splits
+    (128, 4096, 4096),  # 64 x 64, 2 splits
+    (256, 6144, 4096),  # 128 x 128, 2 splits
+    (300, 4101, 4104),  # ragged M and N, N not a multiple of 4 (scalar partial stores and reduce)
+    (100, 1000, 8200),  # ragged K: the last split shorter
+    (65, 4096, 14336),
+]
+
+
+@pytest.mark.parametrize("M,N,K", TILED_SPLIT_SHAPES)
+def test_tiled_split_k(M, N, K):
+    L = capi.lib()
+    plan = capi.gemm_plan(M, N, K)
+    print(f"gemm tiled plan {M}x{N}x{K}: {plan}", flush=True)
+    assert plan[2] > 1
+    nbytes = L.dk_gemm_tn_workspace_bytes(M, N, K)
+    dtype = torch.bfloat16 if M % 2 == 0 else torch.float16
+    a, b, bias = _operands(M, N, K, dtype, M + 7 * N)
+    ws = torch.full((nbytes // 4,), float("nan"), device="cuda")
+    c1 = torch.empty(M, N, device="cuda", dtype=dtype)
+    _ws_call(a, b, bias, c1, ws, nbytes)
+    c2 = torch.empty_like(c1)
+    ws.fill_(float("nan"))
+    _ws_call(a, b, bias, c2, ws, nbytes)
+    torch.cuda.synchronize()
+    assert torch.equal(c1, c2), "split-K result is not deterministic"
+    ref = gemm_f32(a, b, bias)
+    assert_max_abs(c1, ref, dtype, f"gemm tiled split-K {M}x{N}x{K} plan {plan}")
+    assert torch.equal(dk.gemm(a, b, bias), c1)
+    unsplit = torch.empty_like(c1)
+    _call(L.dk_gemm_tn, a, b, bias, unsplit)
+    assert_max_abs(unsplit, ref, dtype, f"gemm tiled unsplit {M}x{N}x{K}")
+    small = torch.empty_like(c1)
+    _ws_call(a, b, bias, small, ws, nbytes - 4)
+    torch.cuda.synchronize()
+    assert torch.equal(small, unsplit), "a workspace too small runs the unsplit kernel"
+
+
 @pytest.mark.parametrize("M,N,K", SPLIT_SHAPES[:4])
 def test_missing_or_small_workspace_runs_the_unsplit_kernel(M, N, K):
     L = capi.lib()
@@ -118,7 +160,8 @@ def test_unsplit_shapes_ignore_the_workspace():
     """Shapes planned unsplit (any workspace) run dk_gemm_tn's kernel."""
     L = capi.lib()
     ws = torch.empty(1 << 20, device="cuda")
-    for M, N, K in [(8, 4096, 14336), (32, 6144, 4096), (64, 28672, 4096), (40, 33000, 1032), (128, 4096, 4096)]:
+    for M, N, K in [(8, 4096, 14336), (32, 6144, 4096), (64, 28672, 4096), (40, 33000, 1032), (512, 6144, 4096),
+                    (4096, 4096, 1032)]:
         assert L.dk_gemm_tn_workspace_bytes(M, N, K) == 0
         a, b, bias = _operands(M, N, K, torch.bfloat16, M + N)
         want = torch.empty(M, N, device="cuda", dtype=torch.bfloat16)

@@ -22,6 +22,7 @@ from parity import (
     attention_f32,
     fused_add_rms_norm_reference,
     gemm_f32,
+    gemm_f32_gpu,
     rms_norm_reference,
     silu_and_mul_reference,
 )
@@ -483,9 +484,8 @@ def test_gemm_decode_layer_shapes(M, N):
 
 
 def _gemm_f32_gpu(a, b):
-    """Plain torch fp32 GEMM on the GPU (a 2-D mm of contiguous fp32 operands),
-    for shapes where the CPU oracle would take minutes."""
-    return torch.mm(a.float(), b.float().t().contiguous())
+    """Plain torch fp32 GEMM on the GPU, for shapes where the CPU oracle would take minutes."""
+    return gemm_f32_gpu(a, b)
 
 
 @pytest.mark.parametrize("M", [1, 16, 32, 48, 64, 4096])

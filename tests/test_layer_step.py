@@ -29,6 +29,7 @@ from parity import (
     attention_f32,
     fused_add_rms_norm_reference,
     gemm_f32,
+    gemm_f32_gpu,
     silu_and_mul_reference,
 )
 
@@ -126,7 +127,7 @@ SEQ_LENS = [0, 1, 600, 1500, 33, 2049, 512, 513]
 
 def _gemm_f32_gpu(a, b):
     """fp32 GEMM on the GPU (the reference for GEMMs too large for the CPU oracle in a test)."""
-    return a.float() @ b.float().t()
+    return gemm_f32_gpu(a, b)
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
