@@ -722,6 +722,34 @@ def pmc_workload_attention_cold(calls: int = 3) -> None:
         torch.cuda.empty_cache()
 
 
+def pmc_workload_norm(calls: int = 3) -> None:
+    """What the norm / activation counter runs profile: rms_norm and
+    fused_add_rms_norm at hidden 4096 and silu_and_mul at 2 x 14336, for 64
+    tokens (decode) and 16384 tokens (a prefill batch), each call from cold
+    caches, then copies of CALIBRATION_BYTES to scale the counters."""
+    g = torch.Generator(device="cuda").manual_seed(40)
+    w = (1 + 0.1 * torch.randn(4096, generator=g, device="cuda")).to(torch.bfloat16)
+    for tokens in (64, 16384):
+        x = torch.randn(tokens, 4096, generator=g, device="cuda", dtype=torch.bfloat16)
+        r = torch.randn(tokens, 4096, generator=g, device="cuda", dtype=torch.bfloat16)
+        out = torch.empty_like(x)
+        gu = torch.randn(tokens, 2 * 14336, generator=g, device="cuda", dtype=torch.bfloat16)
+        act = torch.empty(tokens, 14336, device="cuda", dtype=torch.bfloat16)
+        for _ in range(calls):
+            for fn in (lambda: dk.rms_norm(x, w, 1e-5, out=out), lambda: dk.fused_add_rms_norm(x, r, w, 1e-5),
+                       lambda: dk.silu_and_mul(gu, out=act)):
+                flush_caches()
+                fn()
+        torch.cuda.synchronize()
+        del x, r, out, gu, act
+    src = torch.ones(CALIBRATION_BYTES // 4, dtype=torch.int32, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(calls):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(f"pmc norm workload done: {calls} cold calls of each op at 64 and 16384 tokens", flush=True)
+
+
 def pmc_workload(calls: int = 5) -> None:
     """What the counter runs profile: the headline op `calls` times, then a
     copy of CALIBRATION_BYTES (read once, written once) to scale the counters."""
@@ -767,7 +795,7 @@ def main() -> int:
     ap.add_argument("--no-extras", action="store_true", help="skip the secondary configs")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline (and its correctness check)")
     ap.add_argument("--pmc-workload", nargs="?", const="attention",
-                    choices=["attention", "attention_cold", "attention_fp8", "gemm", "gemm_skinny"],
+                    choices=["attention", "attention_cold", "attention_fp8", "gemm", "gemm_skinny", "norm"],
                     help="run only what the rocprofv3 --pmc passes profile (default: attention)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -787,6 +815,9 @@ def main() -> int:
         return 0
     if args.pmc_workload == "gemm":
         pmc_workload_gemm()
+        return 0
+    if args.pmc_workload == "norm":
+        pmc_workload_norm()
         return 0
     if args.pmc_workload:
         pmc_workload()
