@@ -29,6 +29,13 @@ namespace normact {
 
 constexpr int kVec = 8;  // 16-bit elements per 16-byte vector
 
+#ifndef DK_SILU_NT_LOADS
+// silu_and_mul's gate / up loads with the non-temporal bit: 12-14% faster at
+// 16384 tokens, 4% at 4096, the same at decode sizes. The norms' row loads
+// measured 3-5% slower with it at 4096-16384 rows and keep the default policy.
+#define DK_SILU_NT_LOADS 1
+#endif
+
 __device__ __forceinline__ float inv_rms(float ss, int H, float eps) {
   return 1.0f / __fsqrt_rn(ss / static_cast<float>(H) + eps);
 }
@@ -171,8 +178,10 @@ __global__ __launch_bounds__(kSiluThreads) void silu_and_mul_vec_kernel(uint16_t
   const int i = blockIdx.y * kSiluThreads + threadIdx.x;  // vector index in the row
   if (i >= d / kVec) return;
   const uint16_t* row = in + blockIdx.x * in_stride;
-  const u32x4 g = reinterpret_cast<const u32x4*>(row)[i];
-  const u32x4 u = reinterpret_cast<const u32x4*>(row + d)[i];
+  const u32x4* gp = reinterpret_cast<const u32x4*>(row) + i;
+  const u32x4* up = reinterpret_cast<const u32x4*>(row + d) + i;
+  const u32x4 g = DK_SILU_NT_LOADS ? __builtin_nontemporal_load(gp) : *gp;
+  const u32x4 u = DK_SILU_NT_LOADS ? __builtin_nontemporal_load(up) : *up;
   u32x4 o;
 #pragma unroll
   for (int e = 0; e < 4; ++e) o[e] = pack2<E>(silu(E::lo(g[e])) * E::lo(u[e]), silu(E::hi(g[e])) * E::hi(u[e]));
