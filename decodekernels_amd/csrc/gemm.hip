@@ -457,14 +457,19 @@ __global__ __launch_bounds__(WM * WN * kWave) void gemm_dma_kernel(const uint16_
   __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));
 
   // acc[i][j] lane l, reg r = C[m0 + wm BM/WM + 16 i + l % 16][n0 + wn BN/WN + 16 j + 4 (l / 16) + r].
+  // Column blocks outermost: a lane's 4 bias values of block j are loaded once
+  // for its TM rows (element by element they were waited for one at a time).
 #pragma unroll
-  for (int i = 0; i < TM; ++i) {
-    const int m = m0 + wm * (BM / WM) + 16 * i + l16;
-    if (m >= M) continue;
-    uint16_t* crow = C + static_cast<int64_t>(m) * ldc;
+  for (int j = 0; j < TN; ++j) {
+    const int n = n0 + wn * (BN / WN) + 16 * j + 4 * lg;
+    float bj[4];
 #pragma unroll
-    for (int j = 0; j < TN; ++j) {
-      const int n = n0 + wn * (BN / WN) + 16 * j + 4 * lg;
+    for (int r = 0; r < 4; ++r)
+      bj[r] = (bias != nullptr && part == nullptr && n + r < N) ? E::to_float(bias[n + r]) : 0.0f;
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      const int m = m0 + wm * (BM / WM) + 16 * i + l16;
+      if (m >= M) continue;
       if (part != nullptr) {
         float* prow = part + (static_cast<int64_t>(blockIdx.y) * M + m) * N;
         if (N % 4 == 0 && n + 3 < N) {
@@ -476,10 +481,10 @@ __global__ __launch_bounds__(WM * WN * kWave) void gemm_dma_kernel(const uint16_
         }
         continue;
       }
+      uint16_t* crow = C + static_cast<int64_t>(m) * ldc;
       float v[4];
 #pragma unroll
-      for (int r = 0; r < 4; ++r)
-        v[r] = acc[i][j][r] + (bias != nullptr && n + r < N ? E::to_float(bias[n + r]) : 0.0f);
+      for (int r = 0; r < 4; ++r) v[r] = acc[i][j][r] + bj[r];
       if (vec_store && n + 3 < N) {
         *reinterpret_cast<u32x2*>(crow + n) = u32x2{pack2<E>(v[0], v[1]), pack2<E>(v[2], v[3])};
       } else {
