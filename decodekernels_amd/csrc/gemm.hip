@@ -21,7 +21,7 @@
 //   in flight across the per-step barrier.
 // * LDS-DMA (M > 64, batched decode and prefill): A and B tiles go from HBM
 //   straight into LDS (buffer_load ... lds), bank-conflict-free XOR-swizzled,
-//   through a multi-stage ring; five tile shapes from 256x256 down to 64x64,
+//   through a multi-stage ring; six tile shapes from 256x256 down to 64x64,
 //   picked per call by a throughput model so that batches of a few hundred
 //   rows still fill all 256 CUs.
 #include <algorithm>
@@ -522,8 +522,8 @@ using DmaLauncher = hipError_t (*)(const uint16_t*, const uint16_t*, const uint1
 template <typename E>
 const DmaLauncher* dma_launchers() {
   static const DmaLauncher fns[] = {
-      launch_dma<E, 256, 256, 4, 2, 2>, launch_dma<E, 256, 128, 4, 2, 3>, launch_dma<E, 128, 128, 4, 2, 3>,
-      launch_dma<E, 128, 64, 2, 2, 4>, launch_dma<E, 64, 64, 2, 2, 4>,
+      launch_dma<E, 256, 256, 4, 2, 2>, launch_dma<E, 256, 192, 4, 2, 2>, launch_dma<E, 256, 128, 4, 2, 3>,
+      launch_dma<E, 128, 128, 4, 2, 3>, launch_dma<E, 128, 64, 2, 2, 4>,  launch_dma<E, 64, 64, 2, 2, 4>,
   };
   return fns;
 }
@@ -683,7 +683,12 @@ inline int64_t skinny_workspace_bytes(const SkinnyPlan& p, int M, int N) {
 // (< 256 tiles). Measured (us, cold): down (N 4096, K 14336) M = 128 73.2 ->
 // 36.6 (128 x 128, 8 splits; hipBLASLt 83.6), M = 256 73.3 -> 50.9 (256 x 128,
 // 8; 69.0), M = 512 105.3 -> 75.8 (256 x 128, 4; 100.4); o M = 128 24.6 ->
-// 19.3 (64 x 64, 2); qkv M = 256 35.8 -> 33.5 (128 x 128, 2).
+// 19.3 (64 x 64, 2); qkv M = 256 35.8 -> 33.5 (128 x 128, 2). The 256 x 192
+// tile (rate placed between its neighbours from the qkv M = 4096 timing) fills
+// whole rounds where 256 x 256 leaves the last one part-empty: qkv (N 6144)
+// M = 1536 / 3072 / 4096 / 6000 103.9 / 188.3 / 194.1 / 298.7 -> 93.5 / 175.7
+// / 182.2 / 258.1, N 3072 and 5120 at M = 4096 105.2 / 185.9 -> 98.3 / 175.3
+// (each pick the fastest of the three 256-row tiles).
 struct DmaPlan {
   int shape, splits, k_split;
 };
@@ -696,7 +701,7 @@ struct DmaShape {
   double rate;  // TFLOP/s per CU
 };
 constexpr DmaShape kDmaShapes[] = {
-    {256, 256, 5.355}, {256, 128, 4.776}, {128, 128, 3.48}, {128, 64, 2.398}, {64, 64, 2.007},
+    {256, 256, 5.355}, {256, 192, 5.15}, {256, 128, 4.776}, {128, 128, 3.48}, {128, 64, 2.398}, {64, 64, 2.007},
 };
 
 inline DmaPlan dma_plan(int M, int N, int K, bool split_ok) {

@@ -108,6 +108,7 @@ TILED_SPLIT_SHAPES = [
     (300, 4101, 4104),  # ragged M and N, N not a multiple of 4 (scalar partial stores and reduce)
     (100, 1000, 8200),  # ragged K: the last split shorter
     (65, 4096, 14336),
+    (961, 6113, 5704),  # 256 x 192 tiles, 2 splits, ragged M and N (scalar partial stores and reduce)
 ]
 
 

@@ -454,9 +454,11 @@ GEMM_SHAPES = [
     (512, 4096, 1032),  # 128x64 tiles
     (512, 6144, 1032),  # 128x128 tiles
     (512, 11008, 4096),
+    (902, 10465, 560),  # 256x192 tiles, ragged M and N, N odd (scalar stores)
     (1000, 1000, 136),
     (274, 10917, 520),  # 256x128 tiles, partial in M and N
-    (2000, 6000, 264),  # 256x256 tiles, partial in M and N
+    (2000, 6000, 264),  # 256x192 tiles, partial in M and N
+    (2000, 7000, 264),  # 256x256 tiles, partial in M and N
 ]
 
 
