@@ -662,7 +662,8 @@ CALIBRATION_BYTES = 256 << 20
 def pmc_workload_gemm(calls: int = 3) -> None:
     """What the GEMM counter runs profile: gemm_tn at a prefill shape (M=4096,
     N=K=4096: 256x256 tiles) and a batched-decode shape (M=256, N=6144,
-    K=4096: 128x64 tiles), `calls` times each."""
+    K=4096: 128x128 tiles, K in 2 splits), `calls` times each, then hipBLASLt
+    (torch's F.linear) at the prefill shape for comparison."""
     g = torch.Generator(device="cuda").manual_seed(30)
     for m, n in ((4096, 4096), (256, 6144)):
         a = torch.randn(m, 4096, generator=g, device="cuda", dtype=torch.bfloat16) * 0.02
@@ -670,8 +671,12 @@ def pmc_workload_gemm(calls: int = 3) -> None:
         c = torch.empty(m, n, device="cuda", dtype=torch.bfloat16)
         for _ in range(calls):
             torch.ops.decode_kernels.gemm_tn(c, a, w, None)
+        if m == 4096:
+            for _ in range(calls):
+                torch.nn.functional.linear(a, w)
     torch.cuda.synchronize()
-    print(f"pmc gemm workload done: {calls} calls each at M=4096 N=4096 and M=256 N=6144 (K=4096)", flush=True)
+    print(f"pmc gemm workload done: {calls} calls each at M=4096 N=4096 and M=256 N=6144 (K=4096), "
+          f"{calls} hipBLASLt calls at M=4096", flush=True)
 
 
 def pmc_workload_gemm_skinny(calls: int = 3) -> None:
