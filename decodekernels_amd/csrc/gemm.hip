@@ -325,7 +325,10 @@ __global__ __launch_bounds__(WM * WN * kWave) void gemm_dma_kernel(const uint16_
   constexpr int kSlice = (BM + BN) * 8;  // u32x4 per slice
   static_assert(BM % (8 * NW) == 0 && BN % (8 * NW) == 0 && TM >= 1 && TN >= 1, "tile shape");
   static_assert(STAGES >= 2 && (STAGES - 2) * (LA + LB) < 64, "vmcnt range");
-  __shared__ u32x4 lds[STAGES * kSlice];
+  constexpr int kStagePitch = BN / WN * 2 + 16;         // bytes per staged output row
+  constexpr int kStageWave = BM / WM * kStagePitch;     // bytes of one wave's staged tile
+  static_assert((BM / WM) * (BN / WN / 8) % kWave == 0, "staged tile: whole 64-lane passes");
+  __shared__ u32x4 lds[STAGES * kSlice > NW * kStageWave / 16 ? STAGES * kSlice : NW * kStageWave / 16];
 
   const int lane = threadIdx.x % kWave;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
@@ -457,20 +460,14 @@ __global__ __launch_bounds__(WM * WN * kWave) void gemm_dma_kernel(const uint16_
   __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));
 
   // acc[i][j] lane l, reg r = C[m0 + wm BM/WM + 16 i + l % 16][n0 + wn BN/WN + 16 j + 4 (l / 16) + r].
-  // Column blocks outermost: a lane's 4 bias values of block j are loaded once
-  // for its TM rows (element by element they were waited for one at a time).
+  if (part != nullptr) {  // fp32 partial tile, no bias
 #pragma unroll
-  for (int j = 0; j < TN; ++j) {
-    const int n = n0 + wn * (BN / WN) + 16 * j + 4 * lg;
-    float bj[4];
+    for (int j = 0; j < TN; ++j) {
+      const int n = n0 + wn * (BN / WN) + 16 * j + 4 * lg;
 #pragma unroll
-    for (int r = 0; r < 4; ++r)
-      bj[r] = (bias != nullptr && part == nullptr && n + r < N) ? E::to_float(bias[n + r]) : 0.0f;
-#pragma unroll
-    for (int i = 0; i < TM; ++i) {
-      const int m = m0 + wm * (BM / WM) + 16 * i + l16;
-      if (m >= M) continue;
-      if (part != nullptr) {
+      for (int i = 0; i < TM; ++i) {
+        const int m = m0 + wm * (BM / WM) + 16 * i + l16;
+        if (m >= M) continue;
         float* prow = part + (static_cast<int64_t>(blockIdx.y) * M + m) * N;
         if (N % 4 == 0 && n + 3 < N) {
           *reinterpret_cast<f32x4*>(prow + n) = acc[i][j];
@@ -479,19 +476,71 @@ __global__ __launch_bounds__(WM * WN * kWave) void gemm_dma_kernel(const uint16_
           for (int r = 0; r < 4; ++r)
             if (n + r < N) prow[n + r] = acc[i][j][r];
         }
-        continue;
       }
-      uint16_t* crow = C + static_cast<int64_t>(m) * ldc;
+    }
+    return;
+  }
+
+  // Every bias value this lane adds, loaded before any store, with clamped
+  // addresses and no branch per element so that the loads issue together.
+  // (Loaded one at a time under a bounds branch, each was waited for behind
+  // the stores before it: up to 6 us at M = N = 4096.) Columns past N are
+  // never stored, so their clamped values do not matter.
+  float bj[TN][4];
+  if (bias != nullptr) {
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const int n = n0 + wn * (BN / WN) + 16 * j + 4 * lg;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) bj[j][r] = E::to_float(bias[min(n + r, N - 1)]);
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) bj[j][r] = 0.0f;
+  }
+
+  // The output goes through LDS: each wave writes its (BM/WM) x (BN/WN) tile
+  // into its own part of the ring in the MFMA layout (8 bytes per lane), then
+  // reads it back row by row, 16 bytes per lane, so a store writes whole row
+  // segments instead of 32-byte pieces of 16 rows. Rows are padded by 16 bytes.
+  constexpr int kNc = BN / WN / 8;  // 16-byte chunks per tile row
+  char* stg = reinterpret_cast<char*>(lds) + wave * kStageWave;
+  __syncthreads();  // every wave is done with the ring
+#pragma unroll
+  for (int j = 0; j < TN; ++j) {
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      const int row = 16 * i + l16;
+      const int c = 2 * j + lg / 2;
       float v[4];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) v[r] = acc[i][j][r] + bj[r];
-      if (vec_store && n + 3 < N) {
-        *reinterpret_cast<u32x2*>(crow + n) = u32x2{pack2<E>(v[0], v[1]), pack2<E>(v[2], v[3])};
-      } else {
+      for (int r = 0; r < 4; ++r) v[r] = acc[i][j][r] + bj[j][r];
+      *reinterpret_cast<u32x2*>(stg + row * kStagePitch + c * 16 + (lg % 2) * 8) =
+          u32x2{pack2<E>(v[0], v[1]), pack2<E>(v[2], v[3])};
+    }
+  }
+  __syncthreads();  // the tile's rows come from the other lanes of the wave
 #pragma unroll
-        for (int r = 0; r < 4; ++r)
-          if (n + r < N) crow[n + r] = E::from_float(v[r]);
-      }
+  for (int it = 0; it < (BM / WM) * kNc / kWave; ++it) {
+    const int idx = it * kWave + lane;
+    const int row = idx / kNc;
+    const int c = idx % kNc;
+    const u32x4 val = *reinterpret_cast<const u32x4*>(stg + row * kStagePitch + c * 16);
+    const int m = m0 + wm * (BM / WM) + row;
+    const int n = n0 + wn * (BN / WN) + 8 * c;
+    if (m >= M) continue;
+    uint16_t* crow = C + static_cast<int64_t>(m) * ldc;
+    if (vec_store == 2 && n + 7 < N) {
+      *reinterpret_cast<u32x4*>(crow + n) = val;
+    } else if (vec_store == 1 && n + 7 < N) {
+      *reinterpret_cast<u32x2*>(crow + n) = u32x2{val[0], val[1]};
+      *reinterpret_cast<u32x2*>(crow + n + 4) = u32x2{val[2], val[3]};
+    } else {
+#pragma unroll
+      for (int r = 0; r < 8; ++r)
+        if (n + r < N) crow[n + r] = static_cast<uint16_t>(val[r / 2] >> (16 * (r % 2)));
     }
   }
 }
@@ -501,7 +550,8 @@ hipError_t launch_dma(const uint16_t* A, const uint16_t* B, const uint16_t* bias
                       int lda, int ldb, int ldc, hipStream_t s, float* part = nullptr, int splits = 1,
                       int k_split = 0) {
   const int64_t tiles = ceil_div64(M, BM) * ceil_div64(N, BN);
-  const int vec = (ldc % 4 == 0 && aligned_to(C, 8)) ? 1 : 0;
+  // Output stores of 16 bytes, or 8 where C's rows allow only that.
+  const int vec = (ldc % 8 == 0 && aligned_to(C, 16)) ? 2 : (ldc % 4 == 0 && aligned_to(C, 8)) ? 1 : 0;
   hipLaunchKernelGGL((gemm_dma_kernel<E, BM, BN, WM, WN, STAGES>),
                      dim3(static_cast<unsigned>(tiles), static_cast<unsigned>(part != nullptr ? splits : 1)),
                      dim3(WM * WN * kWave), 0, s, A, B, bias, C, M, N, K, lda, ldb, ldc, vec, part,
