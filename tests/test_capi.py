@@ -71,3 +71,35 @@ def test_capi_gemm_and_norms():
     rc = L.dk_silu_and_mul(code, ys.data_ptr(), xs.data_ptr(), 64, 14336, 2 * 14336, 14336, _stream())
     assert rc == 0, capi.last_error()
     assert_ulp(ys, silu_and_mul_reference(xs.cpu()))
+
+
+@pytest.mark.parametrize("offset,ldc_pad", [(0, 0), (0, 4), (4, 8), (1, 7)])
+def test_capi_gemm_strided_output(offset, ldc_pad):
+    """Tiled gemm_tn (M > 64) into a C that is a window of a larger buffer:
+    row stride N + ldc_pad and a start offset of `offset` elements select the
+    16-byte (aligned, ldc % 8 == 0), 8-byte and element-wise store paths. Each
+    must give the contiguous result's bits and leave every element outside the
+    window untouched."""
+    dtype = torch.bfloat16
+    code = capi.dtype_code(dtype)
+    L = capi.lib()
+    M, N, K = 300, 520, 264
+    g = torch.Generator(device="cuda").manual_seed(24)
+    a = torch.randn(M, K, generator=g, device="cuda", dtype=dtype)
+    b = torch.randn(N, K, generator=g, device="cuda", dtype=dtype) / K**0.5
+    bias = torch.randn(N, generator=g, device="cuda", dtype=dtype)
+    want = torch.empty(M, N, device="cuda", dtype=dtype)
+    rc = L.dk_gemm_tn(code, a.data_ptr(), b.data_ptr(), bias.data_ptr(), want.data_ptr(), M, N, K, K, K, N, _stream())
+    assert rc == 0, capi.last_error()
+    ldc = N + ldc_pad
+    buf = torch.full((offset + M * ldc + 64,), -7.0, device="cuda", dtype=dtype)
+    c_ptr = buf.data_ptr() + offset * buf.element_size()
+    rc = L.dk_gemm_tn(code, a.data_ptr(), b.data_ptr(), bias.data_ptr(), c_ptr, M, N, K, K, K, ldc, _stream())
+    assert rc == 0, capi.last_error()
+    torch.cuda.synchronize()
+    window = buf[offset:offset + M * ldc].view(M, ldc)
+    assert torch.equal(window[:, :N], want)
+    outside = torch.ones_like(buf, dtype=torch.bool)
+    outside[offset:offset + M * ldc].view(M, ldc)[:, :N] = False
+    assert bool((buf[outside] == -7.0).all())
+    assert_max_abs(want, gemm_f32(a, b, bias), dtype)
