@@ -23,7 +23,8 @@
 //   straight into LDS (buffer_load ... lds), bank-conflict-free XOR-swizzled,
 //   through a multi-stage ring; six tile shapes from 256x256 down to 64x64,
 //   picked per call by a throughput model so that batches of a few hundred
-//   rows still fill all 256 CUs.
+//   rows still fill all 256 CUs. The output tile leaves through the freed
+//   ring, read back row by row for 16-byte stores.
 #include <algorithm>
 
 #include "../../include/decodekernels_amd.h"
