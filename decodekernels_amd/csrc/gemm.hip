@@ -329,7 +329,9 @@ __global__ __launch_bounds__(WM * WN * kWave) void gemm_dma_kernel(const uint16_
   constexpr int kStagePitch = BN / WN * 2 + 16;         // bytes per staged output row
   constexpr int kStageWave = BM / WM * kStagePitch;     // bytes of one wave's staged tile
   static_assert((BM / WM) * (BN / WN / 8) % kWave == 0, "staged tile: whole 64-lane passes");
-  __shared__ u32x4 lds[STAGES * kSlice > NW * kStageWave / 16 ? STAGES * kSlice : NW * kStageWave / 16];
+  constexpr int kLdsU4 = STAGES * kSlice > NW * kStageWave / 16 ? STAGES * kSlice : NW * kStageWave / 16;
+  static_assert(kLdsU4 * 16 <= 160 * 1024, "LDS of one workgroup (gfx950: 160 KB)");
+  __shared__ u32x4 lds[kLdsU4];
 
   const int lane = threadIdx.x % kWave;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
