@@ -232,14 +232,17 @@ __global__ __launch_bounds__(WN * WK * kWave) void gemm_skinny_lds_kernel(const 
   }
 }
 
-// Sums the split-K partial tiles of the skinny kernel in split order, adds
-// the bias in fp32 and rounds once: C[m][n] = round(sum_s part[s][m][n] + bias[n]).
+// Sums the split-K partial tiles (of either kernel) in split order, adds the
+// bias in fp32 and rounds once: C[m][n] = round(sum_s part[s][m][n] + bias[n]).
 // One thread per 4 consecutive columns of a row; 16-byte loads when N % 4 == 0
-// (every partial row then starts 16-byte aligned).
-template <typename E>
+// (every partial row then starts 16-byte aligned). With S > 0 (= splits) the
+// S partial loads and the bias load are issued together before the in-order
+// sum: loaded one split at a time, each waited for in turn, the reduce took
+// S round trips. S = 0 is the general runtime-count loop.
+template <typename E, int S>
 __global__ __launch_bounds__(256) void gemm_splitk_reduce_kernel(const float* __restrict__ part, int splits, int M,
                                                                  int N, const uint16_t* __restrict__ bias,
-                                                                 uint16_t* __restrict__ C, int ldc) {
+                                                                 uint16_t* __restrict__ C, int ldc, int vec_store) {
   const int n4 = (N + 3) / 4;
   const int64_t idx = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
   if (idx >= static_cast<int64_t>(M) * n4) return;
@@ -247,26 +250,77 @@ __global__ __launch_bounds__(256) void gemm_splitk_reduce_kernel(const float* __
   const int n = static_cast<int>(idx % n4) * 4;
   const int64_t plane = static_cast<int64_t>(M) * N;
   const float* p = part + static_cast<int64_t>(m) * N + n;
+  auto load_bias = [&](float (&b)[4]) {  // columns past N are not stored: clamped addresses
+    if (bias != nullptr) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) b[r] = E::to_float(bias[min(n + r, N - 1)]);
+    } else {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) b[r] = 0.0f;
+    }
+  };
   float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-  if (N % 4 == 0) {
+  float b[4];
+  if (S > 0 && N % 4 == 0) {
+    f32x4 x[S > 0 ? S : 1];
+#pragma unroll
+    for (int sp = 0; sp < S; ++sp) x[sp] = *reinterpret_cast<const f32x4*>(p + sp * plane);
+    load_bias(b);
+#pragma unroll
+    for (int sp = 0; sp < S; ++sp)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) v[r] += x[sp][r];
+  } else if (N % 4 == 0) {
     for (int sp = 0; sp < splits; ++sp) {
       const f32x4 x = *reinterpret_cast<const f32x4*>(p + sp * plane);
 #pragma unroll
       for (int r = 0; r < 4; ++r) v[r] += x[r];
     }
+    load_bias(b);
   } else {
     for (int sp = 0; sp < splits; ++sp) {
 #pragma unroll
       for (int r = 0; r < 4; ++r)
         if (n + r < N) v[r] += p[sp * plane + r];
     }
+    load_bias(b);
   }
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    if (n + r >= N) break;
-    if (bias != nullptr) v[r] += E::to_float(bias[n + r]);
-    C[static_cast<int64_t>(m) * ldc + n + r] = E::from_float(v[r]);
+  for (int r = 0; r < 4; ++r) v[r] += b[r];
+  uint16_t* c = C + static_cast<int64_t>(m) * ldc + n;
+  if (vec_store && n + 3 < N) {
+    *reinterpret_cast<u32x2*>(c) = u32x2{pack2<E>(v[0], v[1]), pack2<E>(v[2], v[3])};
+  } else {
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      if (n + r < N) c[r] = E::from_float(v[r]);
   }
+}
+
+template <typename E>
+void launch_splitk_reduce(const float* part, int splits, int M, int N, const uint16_t* bias, uint16_t* C, int ldc,
+                          hipStream_t s) {
+  const int64_t threads = static_cast<int64_t>(M) * ((N + 3) / 4);
+  const dim3 grid(static_cast<unsigned>((threads + 255) / 256));
+  const int vec = (ldc % 4 == 0 && aligned_to(C, 8)) ? 1 : 0;
+#define DK_REDUCE_CASE(S_)                                                                                 \
+  case S_:                                                                                                 \
+    hipLaunchKernelGGL((gemm_splitk_reduce_kernel<E, S_>), grid, dim3(256), 0, s, part, splits, M, N, bias, C, \
+                       ldc, vec);                                                                          \
+    return;
+  switch (splits) {
+    DK_REDUCE_CASE(2)
+    DK_REDUCE_CASE(3)
+    DK_REDUCE_CASE(4)
+    DK_REDUCE_CASE(5)
+    DK_REDUCE_CASE(6)
+    DK_REDUCE_CASE(7)
+    DK_REDUCE_CASE(8)
+    default:
+      hipLaunchKernelGGL((gemm_splitk_reduce_kernel<E, 0>), grid, dim3(256), 0, s, part, splits, M, N, bias, C, ldc,
+                         vec);
+  }
+#undef DK_REDUCE_CASE
 }
 
 // ---------------------------------------------------------------------------
@@ -562,9 +616,7 @@ hipError_t launch_dma(const uint16_t* A, const uint16_t* B, const uint16_t* bias
   if (part == nullptr) return hipGetLastError();
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  const int64_t threads = static_cast<int64_t>(M) * ((N + 3) / 4);
-  hipLaunchKernelGGL((gemm_splitk_reduce_kernel<E>), dim3(static_cast<unsigned>((threads + 255) / 256)), dim3(256), 0,
-                     s, part, splits, M, N, bias, C, ldc);
+  launch_splitk_reduce<E>(part, splits, M, N, bias, C, ldc, s);
   return hipGetLastError();
 }
 
@@ -818,9 +870,7 @@ hipError_t launch(const uint16_t* A, const uint16_t* B, const uint16_t* bias, ui
     if (part != nullptr) {
       const hipError_t e = hipGetLastError();
       if (e != hipSuccess) return e;
-      const int64_t threads = static_cast<int64_t>(M) * ((N + 3) / 4);
-      hipLaunchKernelGGL((gemm_splitk_reduce_kernel<E>), dim3(static_cast<unsigned>((threads + 255) / 256)), dim3(256),
-                         0, s, part, p.splits, M, N, bias, C, ldc);
+      launch_splitk_reduce<E>(part, p.splits, M, N, bias, C, ldc, s);
     }
     return hipGetLastError();
   }
