@@ -38,6 +38,9 @@ SPLIT_SHAPES = [
     (17, 1000, 8200),  # ragged N and K, the last split shorter
     (33, 4101, 4104),  # N not a multiple of 4 (scalar reduce)
     (64, 8, 1024),  # one N tile
+    (1, 1536, 3072),  # 5 splits
+    (16, 1280, 14336),  # 6 splits
+    (1, 2304, 4096),  # 7 splits
 ]
 
 
