@@ -46,4 +46,4 @@ __all__ = [
     "rotary_embedding_and_cache",
     "silu_and_mul",
 ]
-__version__ = "0.1.0"
+__version__ = "0.2.0"  # pyproject.toml's [project] version (checked by tests/test_packaging.py)

@@ -14,6 +14,12 @@ package has none of, so the commands are issued directly.
 
     python -m decodekernels_amd._build            # build both libraries
     python -m decodekernels_amd._build --resource-usage   # plus per-kernel VGPR/LDS/spill report
+
+Every build keeps the compiler's per-kernel resource report (registers, spills,
+scratch, LDS, occupancy; ``-Rpass-analysis=kernel-resource-usage``) of each
+source in ``_build/<source>.resources.txt``; ``resource_table()`` parses it
+(``tests/test_resource_usage.py`` gates on it, as the reference's
+``tools/compile_check.sh`` reports registers and spills per kernel).
 """
 
 from __future__ import annotations
@@ -56,25 +62,82 @@ def _hipcc() -> str:
     return os.path.join(ROCM, "bin", "hipcc")
 
 
-def _run(cmd: list[str]) -> None:
+RESOURCE_REMARK = "-Rpass-analysis=kernel-resource-usage"
+
+
+def _run(cmd: list[str], quiet_remarks: bool = False) -> str:
     proc = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
     out = "\n".join(
         line for line in proc.stdout.splitlines() if "packed-fp32-ops' is not a recognized feature" not in line
     )
     if proc.returncode != 0:
         raise RuntimeError(f"command failed ({proc.returncode}): {' '.join(cmd)}\n{out}")
-    if out.strip():
-        print(out)
+    shown = out
+    if quiet_remarks:  # drop each resource remark and the source excerpt under it
+        kept, skip = [], False
+        for line in out.splitlines():
+            if RESOURCE_REMARK in line:
+                skip = True
+            elif skip and "|" in line[:12]:
+                pass
+            else:
+                skip = False
+                kept.append(line)
+        shown = "\n".join(kept)
+    if shown.strip():
+        print(shown)
+    return out
+
+
+def resource_report_path(src: str) -> Path:
+    return BUILD / (Path(src).stem + ".resources.txt")
 
 
 def _compile_hip(src: str, resource_usage: bool) -> Path:
     BUILD.mkdir(exist_ok=True)
     obj = BUILD / (Path(src).stem + ".o")
-    cmd = [_hipcc(), *HIP_FLAGS, "-c", str(CSRC / src), "-o", str(obj)]
-    if resource_usage:
-        cmd.insert(1, "-Rpass-analysis=kernel-resource-usage")
-    _run(cmd)
+    cmd = [_hipcc(), RESOURCE_REMARK, *HIP_FLAGS, "-c", str(CSRC / src), "-o", str(obj)]
+    out = _run(cmd, quiet_remarks=not resource_usage)
+    resource_report_path(src).write_text(out)
     return obj
+
+
+def parse_resource_report(text: str) -> list[dict]:
+    """Per-kernel records of a ``-Rpass-analysis=kernel-resource-usage`` log:
+    {"symbol", "name" (demangled), "SGPRs", "VGPRs", "AGPRs", "ScratchSize",
+    "Occupancy", "SGPRs Spill", "VGPRs Spill", "LDS"} (integers)."""
+    import re
+
+    keys = {"TotalSGPRs": "SGPRs", "VGPRs": "VGPRs", "AGPRs": "AGPRs", "ScratchSize [bytes/lane]": "ScratchSize",
+            "Occupancy [waves/SIMD]": "Occupancy", "SGPRs Spill": "SGPRs Spill", "VGPRs Spill": "VGPRs Spill",
+            "LDS Size [bytes/block]": "LDS"}
+    recs: list[dict] = []
+    for line in text.splitlines():
+        if RESOURCE_REMARK not in line:
+            continue
+        m = re.search(r"remark: Function Name: (\S+)", line)
+        if m:
+            recs.append({"symbol": m.group(1)})
+            continue
+        m = re.search(r"remark:\s+([^:]+): (\S+) \[", line)
+        if m and recs and m.group(1).strip() in keys:
+            recs[-1][keys[m.group(1).strip()]] = int(m.group(2))
+    names = subprocess.run(["c++filt"], input="\n".join(r["symbol"] for r in recs), capture_output=True,
+                           text=True).stdout.splitlines()
+    for r, n in zip(recs, names):
+        r["name"] = n
+    return recs
+
+
+def resource_table(sources: list[str] | None = None) -> list[dict]:
+    """Resource records of every kernel of the sources, from the last build's
+    reports; each record also names its "source"."""
+    recs = []
+    for src in sources or HIP_SOURCES:
+        for r in parse_resource_report(resource_report_path(src).read_text()):
+            r["source"] = src
+            recs.append(r)
+    return recs
 
 
 def build_lib(resource_usage: bool = False, jobs: int = 4) -> Path:

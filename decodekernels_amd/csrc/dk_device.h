@@ -115,6 +115,15 @@ __device__ __forceinline__ u32x2 load4(const uint16_t* p) {
   }
 }
 
+// A per-lane value the compiler must treat as produced here (an empty volatile
+// asm on a VGPR): comparisons against it are made where they are written
+// instead of being hoisted out of a loop, whose 64-bit lane masks would
+// otherwise stay live in scalar registers across it. Costs nothing.
+__device__ __forceinline__ int fresh_vgpr(int v) {
+  __asm__ volatile("" : "+v"(v));
+  return v;
+}
+
 // ---------------------------------------------------------------------------
 // Wave and block reductions (64 lanes).
 // ---------------------------------------------------------------------------

@@ -40,7 +40,10 @@
 //   columns per lane group, V row-contiguous (whole 128-byte lines, as the
 //   16-bit row loads), both converted exactly to the model dtype when a tile
 //   is consumed; k_scale folds into the logit scale, v_scale into the output.
+#include <algorithm>
 #include <atomic>
+#include <climits>
+#include <cstdint>
 #include <cstdlib>
 #include <cstring>
 #include <type_traits>
@@ -120,9 +123,13 @@ struct KParams {
   float* tmp_out;
   float* max_logits;
   float* exp_sums;
-  int64_t q_ss, q_sh, o_ss, o_sh;
-  int64_t k_sb, k_st, k_sh, v_sb, v_st, v_sh;
-  int64_t bt_stride;
+  // Element strides, each below 2^31 (checked by the host); every address
+  // computed from them is formed in 64 bits. As 32-bit kernel arguments they
+  // take half the scalar registers, which the balanced kernel's schedule state
+  // needs (with 64-bit strides it spilled scalar registers to VGPR lanes).
+  int32_t q_ss, q_sh, o_ss, o_sh;
+  int32_t k_sb, k_st, k_sh, v_sb, v_st, v_sh;
+  int32_t bt_stride;
   int num_q_heads, group, block_size, max_partitions;
   int num_seqs, num_kv_heads;
   int num_units;  // split-K grid: unit positions per sequence, ceil(max_partitions / 2)
@@ -363,7 +370,7 @@ struct UnitEngine {
     if constexpr (BS16) {
       const int lb0 = u.start / p.block_size;
       const int lb_last = (u.end - 1) / p.block_size;
-      if (lb0 + lane <= lb_last) v = p.block_tables[u.seq * p.bt_stride + lb0 + lane];
+      if (lb0 + lane <= lb_last) v = p.block_tables[static_cast<int64_t>(u.seq) * p.bt_stride + lb0 + lane];
     }
     return v;
   }
@@ -375,8 +382,10 @@ struct UnitEngine {
     return KV8 && !ROW ? 64 * (c / 2) + 16 * lg + 8 * (c % 2) : 32 * c + 8 * lg;
   }
 
-  __device__ __forceinline__ void load_q(const Unit& u) {
-    const uint16_t* qrow = p.q + u.seq * p.q_ss + (u.kv_head * p.group + l16) * p.q_sh;
+  __device__ __forceinline__ void load_q(const Unit& u) { load_q(u, p.q_ss, p.q_sh); }
+  __device__ __forceinline__ void load_q(const Unit& u, int32_t q_ss, int32_t q_sh) {
+    const uint16_t* qrow =
+        p.q + static_cast<int64_t>(u.seq) * q_ss + static_cast<int64_t>(u.kv_head * p.group + l16) * q_sh;
 #pragma unroll
     for (int c = 0; c < CH; ++c) {
       u32x4 w = {0u, 0u, 0u, 0u};
@@ -404,8 +413,8 @@ struct UnitEngine {
     // Element pointers of the K / V cache (bytes for fp8, 16-bit otherwise).
     using KvT = typename std::conditional<KV8, uint8_t, uint16_t>::type;
     constexpr int kElt = sizeof(KvT);
-    const KvT* kbase = reinterpret_cast<const KvT*>(p.k) + u.kv_head * p.k_sh;
-    const KvT* vbase = reinterpret_cast<const KvT*>(p.v) + u.kv_head * p.v_sh;
+    const KvT* kbase = reinterpret_cast<const KvT*>(p.k) + static_cast<int64_t>(u.kv_head) * p.k_sh;
+    const KvT* vbase = reinterpret_cast<const KvT*>(p.v) + static_cast<int64_t>(u.kv_head) * p.v_sh;
     if constexpr (BS16) {
       const int lb = t0 / p.block_size;
       const int phys = __builtin_amdgcn_readlane(bt_lane, lb - u.start / p.block_size);
@@ -421,8 +430,8 @@ struct UnitEngine {
         // every instruction reads whole lines of consecutive rows. Rows past
         // the sequence end re-read its last row.
         const int last = u.end - 1 - t0;
-        const int kst = kElt * static_cast<int>(p.k_st);
-        const int vst = kElt * static_cast<int>(p.v_st);
+        const int kst = kElt * p.k_st;  // 16 rows of either fit 2^31 bytes (host)
+        const int vst = kElt * p.v_st;
 #pragma unroll
         for (int j = 0; j < NI; ++j) {
           const int o = 1024 * j + 16 * lane;
@@ -438,20 +447,20 @@ struct UnitEngine {
           else r.v[j] = bload8<ALIGN, DK_ATTN_ROW_AUX>(rv, rr * vst + o % RB);
         }
       } else if constexpr (KV8) {
-        const int koff = row * static_cast<int>(p.k_st) + 16 * lg;
+        const int koff = row * p.k_st + 16 * lg;
 #pragma unroll
         for (int j = 0; j < CH / 2; ++j) r.k[j] = bload16b<ALIGN, DK_ATTN_FP8_K_AUX>(rk, koff + 64 * j);
         // V row-contiguous; rows past the sequence end re-read its last row.
         const int last = u.end - 1 - t0;
-        const int vst = static_cast<int>(p.v_st);
+        const int vst = p.v_st;
 #pragma unroll
         for (int j = 0; j < CH / 2; ++j) {
           const int o = 1024 * j + 16 * lane;
           r.v[j] = bload16b<ALIGN, DK_ATTN_ROW_AUX>(rv, min(o / RB, last) * vst + o % RB);
         }
       } else {
-        const int koff = kElt * (row * static_cast<int>(p.k_st) + 8 * lg);
-        const int voff = kElt * (row * static_cast<int>(p.v_st) + 8 * lg);
+        const int koff = kElt * (row * p.k_st + 8 * lg);
+        const int voff = kElt * (row * p.v_st + 8 * lg);
 #pragma unroll
         for (int c = 0; c < CH; ++c) r.k[c] = bload8<ALIGN>(rk, koff + 64 * c);
 #pragma unroll
@@ -460,7 +469,7 @@ struct UnitEngine {
     } else {
       const int t = t0 + row;
       const int lb = t / p.block_size;
-      const int64_t phys = p.block_tables[u.seq * p.bt_stride + lb];
+      const int64_t phys = p.block_tables[static_cast<int64_t>(u.seq) * p.bt_stride + lb];
       const int64_t off = t - lb * p.block_size;
       if constexpr (KV8) {
         const KvT* kp = kbase + phys * p.k_sb + off * p.k_st + 16 * lg;
@@ -652,13 +661,18 @@ struct UnitEngine {
     const int group = p.group;
     // Exp-sum of head l16 over all four lane groups.
     const float l_tot = rows_sum(l_run);
-    if (lane < 16) {
+    // The lane test is made here, per merge: hoisted out of the balanced
+    // kernel's piece loop, its 64-bit mask (like the one below) stayed live in
+    // scalar registers for the whole loop and was spilled.
+    if (fresh_vgpr(lane) < 16) {
       sm.m[wave][lane] = m_ref;
       sm.t[wave][lane] = m_true;
       sm.l[wave][lane] = l_tot;
     }
-    // Heads in passes of kMergeHeads (one pass up to 8, two up to 16).
-    for (int h0 = 0; h0 < group; h0 += kMergeHeads) {
+    // Heads in passes of kMergeHeads (one pass up to 8, two up to 16); the
+    // group has at least one head (host), so the first pass needs no test.
+    int h0 = 0;
+    do {
       const int hn = min(kMergeHeads, group - h0);
       // acc[n] lane l: O[head 4*lg + i][column 16n + l16].
 #pragma unroll
@@ -672,7 +686,8 @@ struct UnitEngine {
       lds_barrier();
       merge_pass(u, h0, hn);
       lds_barrier();
-    }
+      h0 += kMergeHeads;
+    } while (h0 < group);
   }
 
   // Combines the waves' partial outputs of heads h0 .. h0 + hn - 1 (in LDS)
@@ -712,7 +727,7 @@ struct UnitEngine {
           }
         }
       } else {
-        p.out[u.seq * p.o_ss + q_head * p.o_sh + d] = E::from_float(res);
+        p.out[static_cast<int64_t>(u.seq) * p.o_ss + static_cast<int64_t>(q_head) * p.o_sh + d] = E::from_float(res);
       }
     }
   }
@@ -755,7 +770,7 @@ void paged_attention_kernel(const KParams p) {
       for (int idx = threadIdx.x; idx < p.group * D; idx += NW * kWave) {
         const int h = idx / D;
         const int d = idx - h * D;
-        p.out[seq * p.o_ss + (kv_head * p.group + h) * p.o_sh + d] = 0;
+        p.out[static_cast<int64_t>(seq) * p.o_ss + static_cast<int64_t>(kv_head * p.group + h) * p.o_sh + d] = 0;
       }
     }
     return;
@@ -815,6 +830,9 @@ void paged_attention_balanced_kernel(const KParams p) {
   __shared__ UnitSmem<D, NW, row_load<BS16, KV8>()> sm;
   __shared__ int pre[kMaxBalancedSeqs + 1];  // cost per KV head of sequences 0 .. s-1
   __shared__ int len[kMaxBalancedSeqs];      // lengths, clamped to the workspace
+  // The query strides, read from here once per stream: kept in scalar
+  // registers across the piece loop, they were what spilled at head_dim 96.
+  __shared__ int32_t q_str[2];
   // Wave totals of the set-up scan, in wave 0's region (no tile is processed before the set-up's last barrier).
   static_assert(sizeof(sm.w[0]) >= NW * sizeof(int), "scan space");
   int* scan = reinterpret_cast<int*>(&sm.w[0]);
@@ -855,6 +873,10 @@ void paged_attention_balanced_kernel(const KParams p) {
     run += cost_of_len(len[s]);
   }
   if (tid == NT - 1) pre[S] = incl;
+  if (tid == 0) {
+    q_str[0] = p.q_ss;
+    q_str[1] = p.q_sh;
+  }
   __syncthreads();
 
   const int hkv = p.num_kv_heads;
@@ -869,17 +891,18 @@ void paged_attention_balanced_kernel(const KParams p) {
     share_b = max(kMinShareTiles, static_cast<int>((static_cast<int64_t>(total) * 100 + denom - 1) / denom));
     share_a = max(kMinShareTiles, static_cast<int>((static_cast<int64_t>(share_b) * r + 99) / 100));
   }
-  const int64_t split_at = static_cast<int64_t>(H) * share_a;
-  auto first_pos = [&](int wg) -> int64_t {
-    return wg < H ? static_cast<int64_t>(wg) * share_a : split_at + static_cast<int64_t>(wg - H) * share_b;
-  };
+  // Share boundaries stay below 2^31: total < 2^30 + 2^17 (the host bounds
+  // the tiles by 2^30) and the rounding of the shares adds at most a few
+  // positions per workgroup.
+  const int split_at = H * share_a;
+  auto first_pos = [&](int wg) -> int { return wg < H ? wg * share_a : split_at + (wg - H) * share_b; };
   auto owner = [&](int x) -> int {  // workgroup whose share holds cost position x
-    return x < split_at ? static_cast<int>(x / share_a) : H + static_cast<int>((x - split_at) / share_b);
+    return x < split_at ? x / share_a : H + (x - split_at) / share_b;
   };
   const int w = blockIdx.x;
   if (first_pos(w) >= total) return;
-  const int a = static_cast<int>(first_pos(w));
-  const int b = static_cast<int>(min(first_pos(w + 1), static_cast<int64_t>(total)));
+  const int a = first_pos(w);
+  const int b = min(first_pos(w + 1), total);
   auto cost_of = [&](int s) { return pre[s + 1] - pre[s]; };
 
   // Stream holding cost position a: the last sequence whose first position
@@ -895,6 +918,14 @@ void paged_attention_balanced_kernel(const KParams p) {
     seq = lo;
   }
   int kv = (a - pre[seq] * hkv) / cost_of(seq);
+  // Row of this share's piece of that stream: the number of shares before
+  // this one that hold its tiles. Every later stream starts inside this share
+  // (its first tile lies at or past a), so its row is 0; the share layout
+  // (and its scalar registers) is not needed past this point.
+  const int first_row = [&]() {
+    const int first = pre[seq] * hkv + kv * cost_of(seq) + kStreamCost;
+    return first < a ? w - owner(first) : 0;
+  }();
 
   // Walk the streams that meet [a, b): each contributes the tiles
   // [lo, hi) of its own (local) numbering that lie inside the share.
@@ -917,7 +948,7 @@ void paged_attention_balanced_kernel(const KParams p) {
       hi = min(b, first + n) - first;
       if (lo < hi) {
         u = lo;
-        row = w - owner(first);
+        row = first < a ? first_row : 0;
         last_tile_here = hi == n;
         return true;
       }
@@ -945,7 +976,7 @@ void paged_attention_balanced_kernel(const KParams p) {
   UnitEngine<E, D, true, BS16, ALIGN, NW, KV8> eng(p, sm);
   Sub cur = make_sub();
   int cur_bt = eng.load_bt(cur.unit);
-  eng.load_q(cur.unit);
+  eng.load_q(cur.unit, q_str[0], q_str[1]);
   eng.prologue(cur.unit, cur_bt);
   for (;;) {
     u += cur.tiles;
@@ -963,14 +994,14 @@ void paged_attention_balanced_kernel(const KParams p) {
     }
     eng.run_tiles(cur.unit, cur_bt);
     if (more) {
-      if (new_stream) eng.load_q(nxt.unit);
+      if (new_stream) eng.load_q(nxt.unit, q_str[0], q_str[1]);
       eng.prologue(nxt.unit, nxt_bt);
     }
     if (cur.piece_end) {
       eng.merge(cur.unit);
       eng.reset();
       const int next_row = cur.unit.slot + 1;
-      if (cur.stream_end && next_row < P && tid < p.group) {
+      if (cur.stream_end && next_row < P && fresh_vgpr(tid) < p.group) {
         const int64_t r =
             (static_cast<int64_t>(cur.unit.seq) * p.num_q_heads + cur.unit.kv_head * p.group + tid) * P + next_row;
         p.max_logits[r] = -__builtin_huge_valf();
@@ -1015,7 +1046,8 @@ __global__ __launch_bounds__(reduce_waves<WPH>() * kWave) void paged_attention_r
   __shared__ float red[WPH > 1 ? kReduceWaves : 1][D + 1];
   const bool active = q_head < p.num_q_heads;
   const bool cols = C * lane < D;  // this lane owns output columns
-  uint16_t* out = p.out + seq * p.o_ss + (active ? q_head : 0) * p.o_sh + (cols ? C * lane : 0);
+  uint16_t* out = p.out + static_cast<int64_t>(seq) * p.o_ss + static_cast<int64_t>(active ? q_head : 0) * p.o_sh +
+                  (cols ? C * lane : 0);
   const int64_t row0 = (static_cast<int64_t>(seq) * p.num_q_heads + (active ? q_head : 0)) * p.max_partitions;
   const float* ml = p.max_logits + row0;
   const float* es = p.exp_sums + row0;
@@ -1364,6 +1396,18 @@ int paged_attention_entry(const dk_paged_attn_params* a, int dtype, int head_dim
   }
   if (a->num_seqs > 65535 || a->num_kv_heads > 65535 || a->num_q_heads > 65535)
     return fail("paged_attention_decode: num_seqs and head counts must be at most 65535");
+  {
+    // The kernels take element strides as 32-bit arguments and form every
+    // address from them in 64 bits, so any cache size works; only a single
+    // stride of 2^31 elements or more (or a negative one) is refused.
+    const int64_t st[11] = {a->q_stride_seq,   a->q_stride_head,  a->out_stride_seq, a->out_stride_head,
+                            a->k_stride_block, a->k_stride_token, a->k_stride_head,  a->v_stride_block,
+                            a->v_stride_token, a->v_stride_head,  a->bt_stride};
+    for (int64_t v : st)
+      if (v < 0 || v > INT32_MAX)
+        return fail("paged_attention_decode: strides must be in [0, 2^31) elements, got %lld",
+                    static_cast<long long>(v));
+  }
 
   const bool split = max_seq_len > kPart;
   if (split) {
@@ -1412,7 +1456,13 @@ int paged_attention_entry(const dk_paged_attn_params* a, int dtype, int head_dim
   kp.num_seqs = a->num_seqs;
   kp.num_kv_heads = a->num_kv_heads;
 
-  const bool bs16 = a->block_size % kTile == 0;
+  // Whole-tile loads address a tile's 16 rows with 32-bit buffer offsets from
+  // the tile's first row; a token stride too large for that takes the per-row
+  // path, whose addresses are 64-bit.
+  const int64_t elt = kv8 ? 1 : 2;
+  const bool rows_fit = static_cast<int64_t>(kTile) * std::max(a->k_stride_token, a->v_stride_token) * elt +
+                            2 * head_dim * elt <= INT32_MAX;
+  const bool bs16 = a->block_size % kTile == 0 && rows_fit;
   hipStream_t s = static_cast<hipStream_t>(stream);
   hipError_t e;
   if (dtype == DK_BFLOAT16) {

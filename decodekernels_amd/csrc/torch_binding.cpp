@@ -7,8 +7,14 @@
 // rotary_embedding and reshape_and_cache, cover the steps around attention
 // that the reference leaves to vLLM, with vLLM's schemas. Each impl checks tensor
 // metadata, fills the C-ABI arguments and enqueues the HIP kernels on the
-// current stream of the input's device; nothing here allocates memory, so the
-// ops can be captured in a graph.
+// current stream of the input's device. One op allocates, unlike the
+// reference's (csrc/ops.cu:149-182, which allocates nothing): gemm_tn takes
+// its split-K workspace (splits * M * N fp32, at most 8.4 MB at the
+// Llama-3-8B decode projections) from PyTorch's caching allocator on the shapes
+// whose plan splits K. That allocation is stream-ordered and served from the
+// graph's private pool under capture, so every op can be captured in a graph;
+// callers that must not allocate at all use the C ABI's dk_gemm_tn_ws with a
+// workspace of their own (or dk_gemm_tn, which runs those shapes unsplit).
 //
 // Importing the Python module `decodekernels_amd._C` (this library) runs the
 // static op registration.

@@ -2,10 +2,14 @@
 
 Mirrors DecodeKernels' ``decode_kernels/ops.py`` (same names, arguments,
 defaults and errors) over this package's HIP kernels. The raw ops
-``torch.ops.decode_kernels.*`` mutate their ``Tensor!`` arguments and allocate
-nothing, so they can run on preallocated buffers inside a HIP graph; these
-wrappers allocate outputs (and the split-K workspace) when the caller does not
-pass them.
+``torch.ops.decode_kernels.*`` mutate their ``Tensor!`` arguments and can run
+on preallocated buffers inside a HIP graph; these wrappers allocate outputs
+(and the attention split-K workspace) when the caller does not pass them. All
+raw ops but one allocate nothing. ``gemm_tn``, unlike the reference's op, takes
+the fp32 workspace of the decode shapes whose plan splits K (splits * M * N * 4
+bytes) from PyTorch's caching allocator, stream-ordered, so it still captures
+in a graph (private pool). The C ABI's ``dk_gemm_tn_ws`` with a caller
+workspace is the allocation-free route.
 """
 
 from __future__ import annotations

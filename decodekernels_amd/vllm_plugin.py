@@ -6,8 +6,9 @@ DECODE_KERNELS_VLLM=1, so installing the package never changes vLLM by itself.
     DECODE_KERNELS_VLLM=1                                 enable
     DECODE_KERNELS_OPS=attention,rms_norm,silu_and_mul   ops to swap (default: all)
 
-Register it with the entry point
-``[project.entry-points."vllm.general_plugins"] decodekernels_amd = "decodekernels_amd.vllm_plugin:register"``.
+The package registers it under the reference's entry-point name (pyproject.toml):
+``[project.entry-points."vllm.general_plugins"] decode_kernels = "decode_kernels.vllm_plugin:register"``
+(``decode_kernels.vllm_plugin`` is this module under the reference's import name).
 """
 
 import os

@@ -43,11 +43,13 @@ def pytest_terminal_summary(terminalreporter, exitstatus, config):
             for rec in ERRORS:
                 f.write(json.dumps(rec) + "\n")
     tr = terminalreporter
-    tr.section("parity: achieved max abs error (bar: max(2e-2 bf16 / 5e-3 fp16, half an ulp))")
+    tr.section("parity: achieved max abs error (bar: max(2e-2 bf16 / 5e-3 fp16, half an ulp + fp32 slack))")
     full = [r for r in ERRORS if "test_full_size" in r["test"]]
     for r in full:
+        plain = r.get("worst_err_over_bar_without_slack")
         tr.write_line(f"  {r['what']:<48} {r['dtype']:<9} max err {r['max_abs_err']:.3e}  "
-                      f"worst err/bar {r['worst_err_over_bar']:.3f}")
+                      f"worst err/bar {r['worst_err_over_bar']:.3f}"
+                      + ("" if plain is None else f" (without the slack {plain:.3f})"))
     tr.write_line(f"  {len(ERRORS)} checks; closest to the bar:")
     for r in sorted(ERRORS, key=lambda r: -r["worst_err_over_bar"])[:8]:
         tr.write_line(f"  {r['worst_err_over_bar']:.3f}  {r['max_abs_err']:.3e} {r['dtype']:<9} {r['what']}  [{r['test']}]")

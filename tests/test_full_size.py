@@ -12,9 +12,9 @@
 * C5 -- the head-dim-256 / group-8 stress batch: 256 sequences with
   log-uniform lengths in [1, 32768] and 8 empty ones, 16 query / 2 KV heads,
   block 32, bf16 and fp16; every sequence against the CPU oracle. The NHD
-  cache is contiguous in two cases and, as BASELINE.json's C5 states, a
-  strided view in the third: [blocks, 32, 2, 256 + 64][..., :256] (token and
-  block strides padded by 64 elements per head row).
+  cache is contiguous in one case per dtype and, as BASELINE.json's C5
+  states, a strided view in the other: [blocks, 32, 2, 256 + 64][..., :256]
+  (token and block strides padded by 64 elements per head row).
 
 The oracle bar is the same as the small-size tests (``tests/parity.py``).
 Two properties that hold exactly at any size are checked on top: permuting
@@ -112,6 +112,8 @@ CONFIGS = {
                                    layout="nhd", q_scale=1.0, outlier=0.0, pad=64),
     "c5_stress_fp16": dict(lens=_stress_lens, hq=16, hkv=2, d=256, bs=32, dtype=torch.float16, layout="nhd",
                            q_scale=1.0, outlier=0.0),
+    "c5_stress_fp16_strided": dict(lens=_stress_lens, hq=16, hkv=2, d=256, bs=32, dtype=torch.float16,
+                                   layout="nhd", q_scale=1.0, outlier=0.0, pad=64),
 }
 
 

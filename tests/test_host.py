@@ -99,6 +99,18 @@ def test_capi_attention_workspace_too_small_and_misaligned():
     assert rc == capi.HIP_ERROR_INVALID_VALUE and "aligned" in capi.last_error()
 
 
+@pytest.mark.parametrize("field,value", [("k_stride_token", 2**31), ("q_stride_seq", -128), ("bt_stride", 2**40),
+                                         ("out_stride_head", 2**31 + 128), ("v_stride_block", -(2**33))])
+def test_capi_attention_rejects_strides_outside_int32(field, value):
+    """The kernels take element strides as 32-bit arguments (addresses formed
+    in 64 bits), so a stride of 2^31 elements or more, or a negative one, is
+    refused before any launch."""
+    p = _attn_params()
+    setattr(p, field, value)
+    rc = capi.lib().dk_paged_attention_decode(ctypes.byref(p), capi.DK_FLOAT16, 128, 10, None)
+    assert rc == capi.HIP_ERROR_INVALID_VALUE and "strides must be in [0, 2^31)" in capi.last_error()
+
+
 def test_capi_attention_fp8_validation():
     L = capi.lib()
     p = _attn_params()

@@ -189,6 +189,53 @@ def test_paged_attention_strided_layouts(layout, seq_lens):
     _check_attention(_q(len(seq_lens), 8, 128, torch.float16), kv, torch.float16)
 
 
+@pytest.mark.parametrize("schedule", ["grid", "balanced"])
+def test_paged_attention_token_stride_beyond_tile_offsets(schedule, monkeypatch):
+    """A token stride of 2^26 elements (a [block_size, blocks, heads, D] cache
+    viewed as [blocks, block_size, heads, D], 2 GiB per K/V): 16 rows of a tile
+    span 2^31 bytes, more than the whole-tile loads' 32-bit buffer offsets
+    reach, so the host routes the call to the per-row loads (64-bit
+    addresses). Blocks are spread over the whole cache, up to the last one.
+    Checked against the oracle on the gathered blocks and, under the grid
+    schedule, bit for bit against the same call on a compact copy (whole-tile
+    loads). The balanced schedule cuts the streams by the resident workgroup
+    count, which differs between the two kernels (the per-row one needs less
+    LDS and fits three workgroups per CU, not two), so its pieces, and the
+    last bits, differ there."""
+    monkeypatch.setenv("DK_ATTN_SCHEDULE", schedule)
+    hkv, d, bs, nb = 2, 128, 16, 2**18
+    seq_lens = [37, 700, 1300]
+    need = [-(-n // bs) for n in seq_lens]
+    g = torch.Generator(device="cuda").manual_seed(11)
+    ids = torch.randperm(nb, generator=g, device="cuda")[: sum(need)]
+    ids[-1] = nb - 1
+    big_k = torch.empty(bs, nb, hkv, d, device="cuda", dtype=torch.bfloat16)
+    big_v = torch.empty_like(big_k)
+    k_cache, v_cache = big_k.permute(1, 0, 2, 3), big_v.permute(1, 0, 2, 3)
+    assert k_cache.stride(1) == 2**26
+    kc = torch.randn(len(ids), bs, hkv, d, generator=g, device="cuda", dtype=torch.bfloat16)
+    vc = torch.randn(len(ids), bs, hkv, d, generator=g, device="cuda", dtype=torch.bfloat16)
+    k_cache[ids], v_cache[ids] = kc, vc
+    bt = torch.zeros(len(seq_lens), max(need), dtype=torch.int32, device="cuda")
+    bt_c = torch.zeros_like(bt)
+    pos = 0
+    for s, n in enumerate(need):
+        bt[s, :n] = ids[pos : pos + n].to(torch.int32)
+        bt_c[s, :n] = torch.arange(pos, pos + n, dtype=torch.int32, device="cuda")
+        pos += n
+    lens = torch.tensor(seq_lens, dtype=torch.int32, device="cuda")
+    q = _q(len(seq_lens), 8, d, torch.bfloat16, seed=12)
+    out = dk.paged_attention_decode(q, k_cache, v_cache, bt, lens)
+    compact = dk.paged_attention_decode(q, kc, vc, bt_c, lens)
+    torch.cuda.synchronize()
+    del big_k, big_v, k_cache, v_cache
+    ref = attention_f32(q, kc, vc, bt_c, lens)
+    assert_max_abs(out, ref, torch.bfloat16, "token stride 2^26")
+    assert_max_abs(compact, ref, torch.bfloat16, "compact copy")
+    if schedule == "grid":
+        assert torch.equal(out, compact)
+
+
 @pytest.mark.parametrize("max_seq_len", [100, 2000])
 def test_paged_attention_empty_sequences(max_seq_len):
     seq_lens = [0, 50, 0, max_seq_len]

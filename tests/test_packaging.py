@@ -61,3 +61,9 @@ def test_vllm_entry_point_from_package_metadata(tmp_path):
     assert eps[0].load() is decodekernels_amd.vllm_plugin.register
     top = (Path(dists[0]._path) / "top_level.txt").read_text().split()
     assert set(top) == {"decode_kernels", "decodekernels_amd"}
+    assert dists[0].metadata["Version"] == decodekernels_amd.__version__
+
+
+def test_plugin_docstring_names_the_registered_entry_point():
+    text = decodekernels_amd.vllm_plugin.__doc__
+    assert 'decode_kernels = "decode_kernels.vllm_plugin:register"' in text

@@ -8,7 +8,11 @@ half of the grid ``pair_ratio / 100`` times the share of the second half. Each
 piece (one stream's tiles inside one share) writes workspace row
 ``w - owner(first tile)`` of its stream, and the workgroup holding a stream's
 last tile marks the row after its own empty when there is one. The reduce
-merges the rows before the first empty one.
+merges the rows before the first empty one. The kernel evaluates ``owner``
+once, for the stream that holds the share's first position: every later
+stream it enters starts inside the share, so its row is 0 (checked here
+against ``w - owner(first tile)`` for every piece). Share boundaries are kept
+in 32-bit integers (checked below 2^31).
 
 This file restates that arithmetic line for line and checks, over the
 benchmark configurations and random shapes (lengths, heads, partitions, grid
@@ -36,7 +40,7 @@ PART = 512
 MIN_SHARE = 64
 
 
-def balanced_schedule(lens, hkv, P, G, pair_ratio, stream_cost, mistake=None):
+def balanced_schedule(lens, hkv, P, G, pair_ratio, stream_cost, mistake=None, with_subs=True):
     """Pieces {(seq, kv): [(wg, row, tile_lo, tile_hi, sub_units)]} and marks
     {(seq, kv): row} as the kernel computes them. ``mistake`` plants an error
     (tests show the checks catch it): "row" numbers rows from the owner of the
@@ -66,6 +70,8 @@ def balanced_schedule(lens, hkv, P, G, pair_ratio, stream_cost, mistake=None):
     def cost_of(s):
         return pre[s + 1] - pre[s]
 
+    assert max(split_at, first_pos(G)) < 2**31, "share boundaries must fit 32-bit integers"
+
     pieces, marks = {}, {}
     for w in range(G):
         if first_pos(w) >= total:
@@ -82,6 +88,9 @@ def balanced_schedule(lens, hkv, P, G, pair_ratio, stream_cost, mistake=None):
         st = {"seq": lo}
         assert cost_of(lo) > 0
         st["kv"] = (a - pre[lo] * hkv) // cost_of(lo)
+        first0 = pre[lo] * hkv + st["kv"] * cost_of(lo) + stream_cost
+        anchor0 = first0 - stream_cost if mistake == "row" else first0
+        first_row = w - owner(anchor0) if first0 < a else 0
 
         def advance():
             st["kv"] += 1
@@ -105,8 +114,10 @@ def balanced_schedule(lens, hkv, P, G, pair_ratio, stream_cost, mistake=None):
                 t_lo = max(a, first) - first
                 st["hi"] = min(b, first + n) - first - (1 if mistake == "end" else 0)
                 if t_lo < st["hi"]:
-                    row_anchor = first - stream_cost if mistake == "row" else first
-                    st["u"], st["row"], st["last"] = t_lo, w - owner(row_anchor), st["hi"] == n
+                    row = first_row if first < a else 0
+                    if mistake is None:
+                        assert row == w - owner(first)
+                    st["u"], st["row"], st["last"] = t_lo, row, st["hi"] == n
                     return True
                 if not advance():
                     return False
@@ -117,7 +128,7 @@ def balanced_schedule(lens, hkv, P, G, pair_ratio, stream_cost, mistake=None):
             seq, kv, u, hi, row = st["seq"], st["kv"], st["u"], st["hi"], st["row"]
             subs = []
             t = u
-            while t < hi:
+            while with_subs and t < hi:
                 m = min(MIN_SHARE, hi - t)
                 subs.append((t * TILE, min((t + m) * TILE, ln[seq])))
                 t += m
@@ -215,3 +226,15 @@ def test_planted_mistake_is_caught(mistake):
     check(lens, 8, 8, 512)
     with pytest.raises(AssertionError):
         check(lens, 8, 8, 512, mistake=mistake)
+
+
+@pytest.mark.parametrize("G", [512, 768])
+def test_largest_balanced_launch_keeps_32_bit_boundaries(G):
+    """The host takes the balanced schedule while sequences x KV heads x
+    partitions x 32 tiles < 2^30: at 2048 sequences of the longest length the
+    cost line is just below that, and every share boundary still fits."""
+    P = (2**30 // (2048 * 8 * 32)) - 1
+    lens = [P * PART] * 2048
+    assert 2048 * 8 * P * (PART // TILE) < 2**30
+    pieces, _, _, tiles_of = balanced_schedule(lens, 8, P, G, 200 if G == 512 else 100, 12, with_subs=False)
+    assert sum(hi - lo for ps in pieces.values() for _, _, lo, hi, _ in ps) == 8 * sum(tiles_of)
