@@ -80,9 +80,9 @@ def _pick(table, *parts):
 # (name fragments, waves per SIMD the design needs). Attention: the headline
 # balanced kernel and its grid form hold two 4-wave workgroups per CU at
 # head_dim 128 (16-bit cache), three with an fp8 cache, four at head_dim 64;
-# the split-K reduce and norms are small. GEMM: two 8-wave LDS-DMA workgroups
-# of the 256-row tiles per CU (one per SIMD pair), and the skinny M <= 64 tiles
-# at least 6 waves per SIMD at M = 1.
+# the split-K reduce and norms are small. GEMM: one 8-wave LDS-DMA workgroup of
+# the 256-row tiles per CU (two waves per SIMD), and the skinny M <= 64 tiles at
+# least 6 waves per SIMD at M = 1.
 OCCUPANCY = [
     (("paged_attention_balanced_kernel<dk::Bf16, 128, true, 16, 4, false>",), 2),
     (("paged_attention_balanced_kernel<dk::F16, 128, true, 16, 4, false>",), 2),
