@@ -531,6 +531,46 @@ def layer_step(num_seqs, hq, hkv, d, bs, seq_lens, dtype, layout, seed, hidden=4
         "rotary_embedding": lambda: dko.rotary_embedding(positions, qkv[:, : hq * d], k_new, d, rope, True),
         "cache_write": lambda: dko.reshape_and_cache(k_new, v_new, case["k"], case["v"], slots),
     }
+    # The same layer with each decode GEMM fused into the op that consumes its
+    # output (the split-K sum done by the consumer): qkv -> RoPE + cache write,
+    # o -> post-attention norm, down -> the next layer's input norm. The step
+    # starts from the normalised input (x) and leaves the next layer's in x,
+    # so it runs the same ops per layer as the unfused step: 4 GEMMs, 2 norms,
+    # RoPE + cache, attention, SiLU.
+    fused = {
+        "qkv_gemm_rotary_embedding_and_cache": lambda: dko.gemm_tn_rotary_embedding_and_cache(
+            qkv, x, w_qkv, None, positions, qkv[:, : hq * d], k_new, v_new, d, rope, True, case["k"], case["v"], slots),
+        "attention": ops["attention"],
+        "o_gemm_add_rms_norm": lambda: dko.gemm_tn_add_rms_norm(o, attn.view(num_seqs, hq * d), w_o, None, resid, ln2,
+                                                                1e-5),
+        "gate_up_gemm": ops["gate_up_gemm"],
+        "silu_and_mul": ops["silu_and_mul"],
+        "down_gemm_add_rms_norm": lambda: dko.gemm_tn_add_rms_norm(x, act, w_down, None, resid, ln1, 1e-5),
+    }
+
+    def check_fused() -> dict:
+        """One fused step against the unfused ops from the same state, bit for
+        bit: norm1 -> the unfused layer -> norm1 of its down output (the next
+        layer's first op) against norm1 (setup) -> the fused layer."""
+        x0, r0 = x.clone(), resid.clone()
+        kc0, vc0 = case["k"].clone(), case["v"].clone()
+        for fn in ops.values():
+            fn()
+        dko.fused_add_rms_norm(down, resid, ln1, 1e-5)
+        want = [t.clone() for t in (qkv, case["k"], case["v"], attn, o, gu, act, down, resid)]
+        x.copy_(x0), resid.copy_(r0), case["k"].copy_(kc0), case["v"].copy_(vc0)
+        for t in (qkv, attn, o, gu, act, down):
+            t.fill_(float("nan"))
+        ops["fused_add_rms_norm"]()
+        for fn in fused.values():
+            fn()
+        got = [qkv, case["k"], case["v"], attn, o, gu, act, x, resid]
+        torch.cuda.synchronize()
+        names = ("qkv", "k_cache", "v_cache", "attention", "o_normed", "gate_up", "act", "next_layer_input", "residual")
+        for name, a, b in zip(names, want, got):
+            if not torch.equal(a, b):
+                raise AssertionError(f"fused layer step: {name} differs from the unfused ops")
+        return {"bit_identical_to_unfused": list(names)}
 
     def check() -> dict:
         """After one step: the stages whose inputs the rest of the step leaves
@@ -553,7 +593,7 @@ def layer_step(num_seqs, hq, hkv, d, bs, seq_lens, dtype, layout, seed, hidden=4
         errs["silu_and_mul_ulp"] = u
         return errs
 
-    return ops, unfused, nbytes, check
+    return ops, unfused, fused, nbytes, check, check_fused
 
 
 def extras_layer_step() -> dict:
@@ -570,19 +610,13 @@ def extras_layer_step() -> dict:
         ("llama3_8b_b64_bf16", (64, 32, 8, 128, 16, torch.randint(512, 4097, (64,), generator=torch.Generator().manual_seed(0)).tolist(),
                                 torch.bfloat16, "vllm")),
     )
-    for name, args in cases:
-        ops, unfused, nbytes, check = layer_step(*args, seed=50)
-
+    def timed(fns: dict) -> tuple[float, float]:
+        """Eager (back to back) and HIP-graph replay time of one step."""
         def step():
-            for fn in ops.values():
+            for fn in fns.values():
                 fn()
 
-        step()
-        torch.cuda.synchronize()
-        checked = check()
-        per_op = {k: time_cold(fn, iters=20)["median_us"] for k, fn in ops.items()}
-        unfused_us = {k: time_cold(fn, iters=20)["median_us"] for k, fn in unfused.items()}
-        eager_us = time_back_to_back(step, 20, 3) * 1e3
+        eager = time_back_to_back(step, 20, 3) * 1e3
         side = torch.cuda.Stream()
         side.wait_stream(torch.cuda.current_stream())
         with torch.cuda.stream(side):
@@ -591,17 +625,41 @@ def extras_layer_step() -> dict:
         graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(graph):
             step()
-        graph_us = time_back_to_back(graph.replay, 20, 3) * 1e3
+        replay = time_back_to_back(graph.replay, 20, 3) * 1e3
+        del graph
+        return eager, replay
+
+    for name, args in cases:
+        ops, unfused, fused, nbytes, check, check_fused = layer_step(*args, seed=50)
+        for fn in ops.values():
+            fn()
+        torch.cuda.synchronize()
+        checked = check()
+        checked.update(check_fused())
+        per_op = {k: time_cold(fn, iters=20)["median_us"] for k, fn in ops.items()}
+        fused_per_op = {k: time_cold(fn, iters=20)["median_us"] for k, fn in fused.items()
+                        if k not in ("attention", "gate_up_gemm", "silu_and_mul")}
+        unfused_us = {k: time_cold(fn, iters=20)["median_us"] for k, fn in unfused.items()}
+        eager_us, graph_us = timed(fused)
+        u_eager_us, u_graph_us = timed(ops)
         res[name] = {
             "eager_us": round(eager_us, 1), "graph_us": round(graph_us, 1),
+            "step": "fused decode GEMMs: qkv -> rotary_embedding_and_cache, o -> post-attention norm, "
+                    "down -> next layer's input norm (the split-K sums done by the consumers)",
+            "unfused": {"eager_us": round(u_eager_us, 1), "graph_us": round(u_graph_us, 1),
+                        "step": "norm -> qkv -> rotary_embedding_and_cache -> attention -> o -> norm -> gate_up "
+                                "-> silu_and_mul -> down, one op per launch"},
             "sum_of_cold_ops_us": round(sum(per_op.values()), 1), "ops_cold_us": per_op,
+            "fused_ops_cold_us": fused_per_op,
             "unfused_rope_and_cache_cold_us": unfused_us,
             "weights_plus_kv_MB": round(nbytes / 1e6, 1),
+            "eager_GB/s": round(nbytes / (eager_us * 1e-6) / 1e9, 1),
             "graph_GB/s": round(nbytes / (graph_us * 1e-6) / 1e9, 1),
             "checked_before_timing": checked,
         }
-        progress(f"layer step {name}: eager {eager_us:.1f} us, graph {graph_us:.1f} us")
-        del ops, graph
+        progress(f"layer step {name}: fused eager {eager_us:.1f} us, graph {graph_us:.1f} us; "
+                 f"unfused eager {u_eager_us:.1f} us, graph {u_graph_us:.1f} us")
+        del ops, fused
         torch.cuda.empty_cache()
     return res
 

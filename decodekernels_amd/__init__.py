@@ -8,7 +8,8 @@ Same public API as DecodeKernels' ``decode_kernels`` package
 ``torch.ops.decode_kernels.*`` names. ``rotary_embedding`` and
 ``reshape_and_cache`` add the two steps around attention that the reference
 leaves to vLLM (vLLM's signatures); ``rotary_embedding_and_cache`` runs both
-in one launch.
+in one launch. ``gemm_add_rms_norm`` and ``gemm_rotary_embedding_and_cache``
+fuse a decode GEMM with the op that consumes its output.
 """
 
 from .ops import (
@@ -19,6 +20,8 @@ from .ops import (
     alloc_workspace,
     fused_add_rms_norm,
     gemm,
+    gemm_add_rms_norm,
+    gemm_rotary_embedding_and_cache,
     is_available,
     num_partitions,
     paged_attention_decode,
@@ -37,6 +40,8 @@ __all__ = [
     "alloc_workspace",
     "fused_add_rms_norm",
     "gemm",
+    "gemm_add_rms_norm",
+    "gemm_rotary_embedding_and_cache",
     "is_available",
     "num_partitions",
     "paged_attention_decode",

@@ -178,6 +178,23 @@ _SIGNATURES = {
         [ctypes.POINTER(RotaryParams), ctypes.POINTER(CacheWriteParams), ctypes.c_int, ctypes.c_float, ctypes.c_float]
         + [ctypes.c_void_p],
     ),
+    "dk_gemm_tn_add_rms_norm": (
+        ctypes.c_int,
+        [ctypes.c_int] + [ctypes.c_void_p] * 6 + [ctypes.c_float] + [ctypes.c_int] * 7
+        + [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p],
+    ),
+    "dk_gemm_tn_rotary_embedding_and_cache": (
+        ctypes.c_int,
+        [ctypes.c_int] + [ctypes.c_void_p] * 4 + [ctypes.c_int] * 6
+        + [ctypes.POINTER(RotaryParams), ctypes.POINTER(CacheWriteParams), ctypes.c_void_p, ctypes.c_int64,
+           ctypes.c_void_p],
+    ),
+    "dk_gemm_tn_rotary_embedding_and_cache_fp8": (
+        ctypes.c_int,
+        [ctypes.c_int] + [ctypes.c_void_p] * 4 + [ctypes.c_int] * 6
+        + [ctypes.POINTER(RotaryParams), ctypes.POINTER(CacheWriteParams), ctypes.c_float, ctypes.c_float,
+           ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p],
+    ),
     "dk_last_error": (ctypes.c_char_p, []),
     "dk_error_string": (ctypes.c_char_p, [ctypes.c_int]),
     "dk_version": (ctypes.c_char_p, []),

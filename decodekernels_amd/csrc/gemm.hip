@@ -602,10 +602,11 @@ __global__ __launch_bounds__(WM * WN * kWave) void gemm_dma_kernel(const uint16_
   }
 }
 
+// With part != nullptr the K splits write fp32 partial tiles; `reduce` then
+// launches gemm_splitk_reduce_kernel, otherwise the caller consumes them.
 template <typename E, int BM, int BN, int WM, int WN, int STAGES>
 hipError_t launch_dma(const uint16_t* A, const uint16_t* B, const uint16_t* bias, uint16_t* C, int M, int N, int K,
-                      int lda, int ldb, int ldc, hipStream_t s, float* part = nullptr, int splits = 1,
-                      int k_split = 0) {
+                      int lda, int ldb, int ldc, hipStream_t s, float* part, int splits, int k_split, bool reduce) {
   const int64_t tiles = ceil_div64(M, BM) * ceil_div64(N, BN);
   // Output stores of 16 bytes, or 8 where C's rows allow only that.
   const int vec = (ldc % 8 == 0 && aligned_to(C, 16)) ? 2 : (ldc % 4 == 0 && aligned_to(C, 8)) ? 1 : 0;
@@ -613,7 +614,7 @@ hipError_t launch_dma(const uint16_t* A, const uint16_t* B, const uint16_t* bias
                      dim3(static_cast<unsigned>(tiles), static_cast<unsigned>(part != nullptr ? splits : 1)),
                      dim3(WM * WN * kWave), 0, s, A, B, bias, C, M, N, K, lda, ldb, ldc, vec, part,
                      part != nullptr ? k_split : K);
-  if (part == nullptr) return hipGetLastError();
+  if (part == nullptr || !reduce) return hipGetLastError();
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   launch_splitk_reduce<E>(part, splits, M, N, bias, C, ldc, s);
@@ -621,7 +622,7 @@ hipError_t launch_dma(const uint16_t* A, const uint16_t* B, const uint16_t* bias
 }
 
 using DmaLauncher = hipError_t (*)(const uint16_t*, const uint16_t*, const uint16_t*, uint16_t*, int, int, int, int,
-                                   int, int, hipStream_t, float*, int, int);
+                                   int, int, hipStream_t, float*, int, int, bool);
 
 // Launchers of kDmaShapes' tile shapes, in the same order.
 template <typename E>
@@ -842,14 +843,21 @@ inline int64_t dma_workspace_bytes(const DmaPlan& d, int M, int N) {
 }
 
 
+// Launches C = A B^T (+ bias) with the plan for (M, N, K) and the workspace
+// given. With deferred_splits != nullptr, a plan that splits K stops after the
+// main kernel, leaving splits x M x N fp32 partial tiles (no bias) in the
+// workspace for the caller to sum in split order, and reports the split count
+// there (1: C was written directly).
 template <typename E>
 hipError_t launch(const uint16_t* A, const uint16_t* B, const uint16_t* bias, uint16_t* C, int M, int N, int K,
-                  int lda, int ldb, int ldc, void* workspace, int64_t workspace_bytes, hipStream_t s) {
+                  int lda, int ldb, int ldc, void* workspace, int64_t workspace_bytes, hipStream_t s,
+                  int* deferred_splits = nullptr) {
   if (M <= 64) {
     SkinnyPlan p = skinny_plan(M, N, K, true);
     if (p.splits > 1 && (workspace == nullptr || skinny_workspace_bytes(p, M, N) > workspace_bytes))
       p = skinny_plan(M, N, K, false);
     float* part = p.splits > 1 ? static_cast<float*>(workspace) : nullptr;
+    if (deferred_splits != nullptr) *deferred_splits = p.splits;
     const dim3 g2(static_cast<unsigned>(ceil_div64(N, 16 * p.wn)), static_cast<unsigned>(p.splits));
 #define DK_SKINNY_LDS(MT_, WN_, WK_)                                                                 \
   case MT_ * 100 + WN_ * 10 + WK_:                                                                   \
@@ -867,7 +875,7 @@ hipError_t launch(const uint16_t* A, const uint16_t* B, const uint16_t* bias, ui
     }
 #undef DK_SKINNY_MT
 #undef DK_SKINNY_LDS
-    if (part != nullptr) {
+    if (part != nullptr && deferred_splits == nullptr) {
       const hipError_t e = hipGetLastError();
       if (e != hipSuccess) return e;
       launch_splitk_reduce<E>(part, p.splits, M, N, bias, C, ldc, s);
@@ -877,8 +885,10 @@ hipError_t launch(const uint16_t* A, const uint16_t* B, const uint16_t* bias, ui
   const DmaPlan d = dma_plan(M, N, K, workspace != nullptr);
   const bool split = d.splits > 1 && dma_workspace_bytes(d, M, N) <= workspace_bytes;
   const DmaPlan u = split ? d : dma_plan(M, N, K, false);
+  if (deferred_splits != nullptr) *deferred_splits = u.splits;
   return dma_launchers<E>()[u.shape](A, B, bias, C, M, N, K, lda, ldb, ldc, s,
-                                     split ? static_cast<float*>(workspace) : nullptr, u.splits, u.k_split);
+                                     split ? static_cast<float*>(workspace) : nullptr, u.splits, u.k_split,
+                                     deferred_splits == nullptr);
 }
 
 }  // namespace gemm
@@ -887,7 +897,8 @@ hipError_t launch(const uint16_t* A, const uint16_t* B, const uint16_t* bias, ui
 namespace {
 
 int gemm_tn_checked(int dtype, const void* A, const void* B, const void* bias, void* C, int M, int N, int K, int lda,
-                    int ldb, int ldc, void* workspace, int64_t workspace_bytes, void* stream) {
+                    int ldb, int ldc, void* workspace, int64_t workspace_bytes, void* stream,
+                    int* deferred_splits = nullptr) {
   using namespace dk;
   clear_error();
   if (dtype != DK_FLOAT16 && dtype != DK_BFLOAT16)
@@ -912,8 +923,8 @@ int gemm_tn_checked(int dtype, const void* A, const void* B, const void* bias, v
   auto* c = static_cast<uint16_t*>(C);
   const hipError_t e =
       dtype == DK_BFLOAT16
-          ? gemm::launch<Bf16>(a, b, bi, c, M, N, K, lda, ldb, ldc, workspace, workspace_bytes, s)
-          : gemm::launch<F16>(a, b, bi, c, M, N, K, lda, ldb, ldc, workspace, workspace_bytes, s);
+          ? gemm::launch<Bf16>(a, b, bi, c, M, N, K, lda, ldb, ldc, workspace, workspace_bytes, s, deferred_splits)
+          : gemm::launch<F16>(a, b, bi, c, M, N, K, lda, ldb, ldc, workspace, workspace_bytes, s, deferred_splits);
   return static_cast<int>(e);
 }
 
@@ -954,4 +965,85 @@ extern "C" int dk_gemm_tn_plan(int M, int N, int K, int with_workspace, int* pla
 extern "C" int dk_gemm_tn_ws(int dtype, const void* A, const void* B, const void* bias, void* C, int M, int N, int K,
                              int lda, int ldb, int ldc, void* workspace, int64_t workspace_bytes, void* stream) {
   return gemm_tn_checked(dtype, A, B, bias, C, M, N, K, lda, ldb, ldc, workspace, workspace_bytes, stream);
+}
+
+// gemm_tn followed by fused_add_rms_norm on its output, with the split-K sum
+// of decode-size plans done inside the norm's kernel (one launch fewer, the
+// GEMM output never written before the norm). Results equal dk_gemm_tn_ws into
+// `out` followed by dk_fused_add_rms_norm(out, residual, weight, eps) bit for
+// bit; rows whose norm cannot take its vector path run exactly that pair.
+extern "C" int dk_gemm_tn_add_rms_norm(int dtype, const void* A, const void* B, const void* bias, void* out,
+                                       void* residual, const void* weight, float eps, int M, int N, int K, int lda,
+                                       int ldb, int ld_out, int ld_res, void* workspace, int64_t workspace_bytes,
+                                       void* stream) {
+  using namespace dk;
+  clear_error();
+  if (dtype != DK_FLOAT16 && dtype != DK_BFLOAT16)
+    return fail("gemm_tn_add_rms_norm: expected float16 or bfloat16, got dtype code %d", dtype);
+  if (M < 0 || N < 0 || K < 0) return fail("gemm_tn: M, N and K must be non-negative");
+  if (M == 0 || N == 0) return hipSuccess;
+  if (out == nullptr || residual == nullptr || weight == nullptr)
+    return fail("gemm_tn_add_rms_norm: out, residual and weight must not be NULL");
+  if (ld_out < N || ld_res < N) return fail("gemm_tn_add_rms_norm: row strides of out and residual must be >= N");
+  const bool fused = fused_add_rms_norm_vectorizable(N, ld_out, ld_res, out, residual, weight);
+  int splits = 1;
+  const int rc = gemm_tn_checked(dtype, A, B, bias, out, M, N, K, lda, ldb, ld_out, workspace, workspace_bytes,
+                                 stream, fused ? &splits : nullptr);
+  if (rc != hipSuccess) return rc;
+  if (splits > 1)
+    return launch_splitk_fused_add_rms_norm(dtype, static_cast<const float*>(workspace), splits, bias, out, ld_out,
+                                            residual, ld_res, weight, M, N, eps, static_cast<hipStream_t>(stream));
+  return dk_fused_add_rms_norm(dtype, out, residual, weight, M, N, ld_out, ld_res, eps, stream);
+}
+
+namespace {
+
+int gemm_tn_rope_cache(const char* op, int dtype, const void* A, const void* B, const void* bias, void* C, int M, int N,
+                       int K, int lda, int ldb, int ldc, const dk_rotary_params* r, const dk_cache_write_params* c,
+                       bool fp8, float k_scale, float v_scale, void* workspace, int64_t workspace_bytes,
+                       void* stream) {
+  using namespace dk;
+  clear_error();
+  if (dtype != DK_FLOAT16 && dtype != DK_BFLOAT16) return fail("%s: expected float16 or bfloat16, got dtype code %d", op, dtype);
+  if (M < 0 || N < 0 || K < 0) return fail("gemm_tn: M, N and K must be non-negative");
+  if (M == 0 || N == 0) return hipSuccess;
+  if (C == nullptr) return fail("gemm_tn: pointers must not be NULL");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  // Everything is checked before the GEMM runs, so a bad rotary / cache
+  // argument leaves C untouched.
+  if (const int rc = rotary_and_cache_on_rows(op, r, c, dtype, fp8, k_scale, v_scale, nullptr, 1, bias, C, ldc, M, N,
+                                              true, s))
+    return rc;
+  int splits = 1;
+  const int rc = gemm_tn_checked(dtype, A, B, bias, C, M, N, K, lda, ldb, ldc, workspace, workspace_bytes, stream,
+                                 &splits);
+  if (rc != hipSuccess) return rc;
+  return rotary_and_cache_on_rows(op, r, c, dtype, fp8, k_scale, v_scale,
+                                  splits > 1 ? static_cast<const float*>(workspace) : nullptr, splits, bias, C, ldc, M, N,
+                                  false, s);
+}
+
+}  // namespace
+
+// gemm_tn into C (e.g. a fused q | k | v projection) followed by
+// rotary_embedding_and_cache on q / k / v views of C's rows; a plan that
+// splits K forms each token's row of C from the partial tiles inside the
+// rotary / cache kernel (one launch fewer). Results equal dk_gemm_tn_ws then
+// dk_rotary_embedding_and_cache bit for bit.
+extern "C" int dk_gemm_tn_rotary_embedding_and_cache(int dtype, const void* A, const void* B, const void* bias, void* C,
+                                                     int M, int N, int K, int lda, int ldb, int ldc,
+                                                     const dk_rotary_params* r, const dk_cache_write_params* c,
+                                                     void* workspace, int64_t workspace_bytes, void* stream) {
+  return gemm_tn_rope_cache("gemm_tn_rotary_embedding_and_cache", dtype, A, B, bias, C, M, N, K, lda, ldb, ldc, r, c,
+                            false, 1.0f, 1.0f, workspace, workspace_bytes, stream);
+}
+
+// The same into fp8 (e4m3fn) caches (dk_rotary_embedding_and_cache_fp8).
+extern "C" int dk_gemm_tn_rotary_embedding_and_cache_fp8(int dtype, const void* A, const void* B, const void* bias,
+                                                         void* C, int M, int N, int K, int lda, int ldb, int ldc,
+                                                         const dk_rotary_params* r, const dk_cache_write_params* c,
+                                                         float k_scale, float v_scale, void* workspace,
+                                                         int64_t workspace_bytes, void* stream) {
+  return gemm_tn_rope_cache("gemm_tn_rotary_embedding_and_cache_fp8", dtype, A, B, bias, C, M, N, K, lda, ldb, ldc, r,
+                            c, true, k_scale, v_scale, workspace, workspace_bytes, stream);
 }

@@ -108,16 +108,14 @@ __global__ __launch_bounds__(1024) void rms_norm_scalar_kernel(uint16_t* __restr
 // ---------------------------------------------------------------------------
 // fused_add_rms_norm
 // ---------------------------------------------------------------------------
-template <typename E, int NV>
-__global__ __launch_bounds__(1024) void fused_add_rms_norm_vec_kernel(uint16_t* __restrict__ input,
-                                                                      uint16_t* __restrict__ residual,
-                                                                      const uint16_t* __restrict__ weight, int H,
-                                                                      int64_t in_stride, int64_t res_stride,
-                                                                      float eps) {
-  __shared__ float slots[1024 / kWave];
-  u32x4* x = reinterpret_cast<u32x4*>(input + blockIdx.x * in_stride);
-  u32x4* r = reinterpret_cast<u32x4*>(residual + blockIdx.x * res_stride);
-  const u32x4* w = reinterpret_cast<const u32x4*>(weight);
+// One row of fused_add_rms_norm: x vector i comes from load_x(i), the
+// normalised row goes to y. Thread t takes vectors t, t + blockDim.x, ...; the
+// sum of squares follows that mapping, so every caller with the same block
+// size gets the same bits.
+template <typename E, int NV, typename LoadX>
+__device__ __forceinline__ void add_rms_norm_row(u32x4* __restrict__ y, u32x4* __restrict__ r,
+                                                 const u32x4* __restrict__ w, int H, float eps, float* slots,
+                                                 LoadX load_x) {
   const int nvec = H / kVec;
   u32x4 rv[NV];
   float ss = 0.0f;
@@ -126,7 +124,7 @@ __global__ __launch_bounds__(1024) void fused_add_rms_norm_vec_kernel(uint16_t* 
     const int i = threadIdx.x + j * blockDim.x;
     u32x4 s = {0u, 0u, 0u, 0u};
     if (i < nvec) {
-      const u32x4 a = x[i];
+      const u32x4 a = load_x(i);
       const u32x4 b = r[i];
 #pragma unroll
       for (int e = 0; e < 4; ++e) s[e] = pack2<E>(E::lo(a[e]) + E::lo(b[e]), E::hi(a[e]) + E::hi(b[e]));
@@ -139,8 +137,74 @@ __global__ __launch_bounds__(1024) void fused_add_rms_norm_vec_kernel(uint16_t* 
 #pragma unroll
   for (int j = 0; j < NV; ++j) {
     const int i = threadIdx.x + j * blockDim.x;
-    if (i < nvec) x[i] = scale8<E>(rv[j], w[i], inv);
+    if (i < nvec) y[i] = scale8<E>(rv[j], w[i], inv);
   }
+}
+
+template <typename E, int NV>
+__global__ __launch_bounds__(1024) void fused_add_rms_norm_vec_kernel(uint16_t* __restrict__ input,
+                                                                      uint16_t* __restrict__ residual,
+                                                                      const uint16_t* __restrict__ weight, int H,
+                                                                      int64_t in_stride, int64_t res_stride,
+                                                                      float eps) {
+  __shared__ float slots[1024 / kWave];
+  u32x4* x = reinterpret_cast<u32x4*>(input + blockIdx.x * in_stride);
+  u32x4* r = reinterpret_cast<u32x4*>(residual + blockIdx.x * res_stride);
+  add_rms_norm_row<E, NV>(x, r, reinterpret_cast<const u32x4*>(weight), H, eps, slots,
+                          [&](int i) { return x[i]; });
+}
+
+// fused_add_rms_norm whose input rows are a GEMM's split-K partial tiles:
+// x = round(sum of the `splits` fp32 planes [splits][rows][H] in split order,
+// starting from 0, plus the bias or 0), exactly as gemm_splitk_reduce_kernel
+// rounds them into C, then the residual add and the norm as
+// fused_add_rms_norm_vec_kernel. The result equals gemm_tn (split) followed by
+// fused_add_rms_norm bit for bit; x itself is never stored, only the
+// normalised row (into `out`) and the new residual. S > 0: a compile-time
+// split count (all partial loads issued together); S = 0: `splits` at run time.
+template <typename E, int NV, int S>
+__global__ __launch_bounds__(1024) void splitk_add_rms_norm_kernel(uint16_t* __restrict__ out,
+                                                                   uint16_t* __restrict__ residual,
+                                                                   const uint16_t* __restrict__ weight, int H,
+                                                                   int64_t out_stride, int64_t res_stride, float eps,
+                                                                   const float* __restrict__ part, int splits,
+                                                                   int64_t plane, const uint16_t* __restrict__ bias) {
+  __shared__ float slots[1024 / kWave];
+  u32x4* y = reinterpret_cast<u32x4*>(out + blockIdx.x * out_stride);
+  u32x4* r = reinterpret_cast<u32x4*>(residual + blockIdx.x * res_stride);
+  const float* prow = part + static_cast<int64_t>(blockIdx.x) * H;
+  auto load_x = [&](int i) {
+    const float* p = prow + kVec * i;
+    float v[kVec];
+#pragma unroll
+    for (int e = 0; e < kVec; ++e) v[e] = 0.0f;
+    if constexpr (S > 0) {
+      f32x4 lo[S], hi[S];
+#pragma unroll
+      for (int sp = 0; sp < S; ++sp) {
+        lo[sp] = *reinterpret_cast<const f32x4*>(p + sp * plane);
+        hi[sp] = *reinterpret_cast<const f32x4*>(p + sp * plane + 4);
+      }
+#pragma unroll
+      for (int sp = 0; sp < S; ++sp)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] += lo[sp][e], v[4 + e] += hi[sp][e];
+    } else {
+      for (int sp = 0; sp < splits; ++sp) {
+        const f32x4 lo = *reinterpret_cast<const f32x4*>(p + sp * plane);
+        const f32x4 hi = *reinterpret_cast<const f32x4*>(p + sp * plane + 4);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] += lo[e], v[4 + e] += hi[e];
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < kVec; ++e) v[e] += bias != nullptr ? E::to_float(bias[kVec * i + e]) : 0.0f;
+    u32x4 a;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) a[e] = pack2<E>(v[2 * e], v[2 * e + 1]);
+    return a;
+  };
+  add_rms_norm_row<E, NV>(y, r, reinterpret_cast<const u32x4*>(weight), H, eps, slots, load_x);
 }
 
 template <typename E>
@@ -253,6 +317,41 @@ hipError_t launch_fused_add(uint16_t* x, uint16_t* r, const uint16_t* w, int row
   return hipGetLastError();
 }
 
+template <typename E, int NV>
+void launch_splitk_add_nv(uint16_t* out, uint16_t* r, const uint16_t* w, int rows, int H, int64_t os, int64_t rs_,
+                          float eps, const float* part, int splits, const uint16_t* bias, dim3 block, hipStream_t s) {
+  const int64_t plane = static_cast<int64_t>(rows) * H;
+#define DK_SPLIT_CASE(S_)                                                                                     \
+  case S_:                                                                                                    \
+    hipLaunchKernelGGL((splitk_add_rms_norm_kernel<E, NV, S_>), dim3(rows), block, 0, s, out, r, w, H, os, rs_, \
+                       eps, part, splits, plane, bias);                                                       \
+    return;
+  switch (splits) {
+    DK_SPLIT_CASE(2)
+    DK_SPLIT_CASE(4)
+    DK_SPLIT_CASE(8)
+    default:
+      hipLaunchKernelGGL((splitk_add_rms_norm_kernel<E, NV, 0>), dim3(rows), block, 0, s, out, r, w, H, os, rs_, eps,
+                         part, splits, plane, bias);
+  }
+#undef DK_SPLIT_CASE
+}
+
+template <typename E>
+hipError_t launch_splitk_add(uint16_t* out, uint16_t* r, const uint16_t* w, int rows, int H, int64_t os, int64_t rs_,
+                             float eps, const float* part, int splits, const uint16_t* bias, hipStream_t s) {
+  const RowShape rs = row_shape(H, true);
+  const dim3 block(rs.threads);
+  switch (rs.nv) {
+    case 1: launch_splitk_add_nv<E, 1>(out, r, w, rows, H, os, rs_, eps, part, splits, bias, block, s); break;
+    case 2: launch_splitk_add_nv<E, 2>(out, r, w, rows, H, os, rs_, eps, part, splits, bias, block, s); break;
+    case 4: launch_splitk_add_nv<E, 4>(out, r, w, rows, H, os, rs_, eps, part, splits, bias, block, s); break;
+    case 8: launch_splitk_add_nv<E, 8>(out, r, w, rows, H, os, rs_, eps, part, splits, bias, block, s); break;
+    default: return hipErrorInvalidValue;  // the caller checked the vector path applies
+  }
+  return hipGetLastError();
+}
+
 template <typename E>
 hipError_t launch_silu(uint16_t* out, const uint16_t* in, int rows, int d, int64_t is, int64_t os, bool vec,
                        hipStream_t s) {
@@ -308,6 +407,29 @@ extern "C" int dk_fused_add_rms_norm(int dtype, void* input, void* residual, con
   return static_cast<int>(dtype == DK_BFLOAT16 ? launch_fused_add<Bf16>(x, r, w, rows, H, in_stride, res_stride, eps, vec, s)
                                                : launch_fused_add<F16>(x, r, w, rows, H, in_stride, res_stride, eps, vec, s));
 }
+
+namespace dk {
+
+bool fused_add_rms_norm_vectorizable(int H, int64_t in_stride, int64_t res_stride, const void* input,
+                                     const void* residual, const void* weight) {
+  return H % normact::kVec == 0 && in_stride % normact::kVec == 0 && res_stride % normact::kVec == 0 &&
+         aligned_to(input, 16) && aligned_to(residual, 16) && aligned_to(weight, 16) &&
+         normact::row_shape(H, true).nv > 0;
+}
+
+int launch_splitk_fused_add_rms_norm(int dtype, const float* part, int splits, const void* bias, void* out,
+                                     int64_t out_stride, void* residual, int64_t res_stride, const void* weight,
+                                     int rows, int H, float eps, hipStream_t s) {
+  auto* o = static_cast<uint16_t*>(out);
+  auto* r = static_cast<uint16_t*>(residual);
+  auto* w = static_cast<const uint16_t*>(weight);
+  auto* b = static_cast<const uint16_t*>(bias);
+  return static_cast<int>(dtype == DK_BFLOAT16
+                              ? launch_splitk_add<Bf16>(o, r, w, rows, H, out_stride, res_stride, eps, part, splits, b, s)
+                              : launch_splitk_add<F16>(o, r, w, rows, H, out_stride, res_stride, eps, part, splits, b, s));
+}
+
+}  // namespace dk
 
 extern "C" int dk_silu_and_mul(int dtype, void* out, const void* input, int rows, int d, int64_t in_stride,
                                int64_t out_stride, void* stream) {

@@ -243,7 +243,59 @@ constexpr int kThreads = 256;
 struct KParams {
   rope::KParams r;   // positions, q, k (rotated in place), cos | sin table
   cache::KParams c;  // key (== r.k), value, caches, slots
+  // Split-K input (part != nullptr): q, k and v are views of the rows of a
+  // GEMM output C [num_tokens, N] whose K splits left fp32 partial planes
+  // [splits][num_tokens][N]; each token's row of C is first formed from them.
+  const float* part;
+  const uint16_t* bias;
+  uint16_t* C;
+  int64_t ldc, plane;
+  int N, splits, vec_c;
 };
+
+// Row t of C = round(sum of the partial planes in split order, starting from
+// 0, plus the bias or 0): gemm_splitk_reduce_kernel's arithmetic and store
+// path (8-byte packed stores where it uses them, elementwise otherwise), so C
+// ends bit for bit as the GEMM's own reduce leaves it.
+constexpr int kMaxSplits = 8;  // the GEMM plans split K at most 8 ways (checked by the host)
+
+template <typename E>
+__device__ __forceinline__ void reduce_row(const KParams& p, int t) {
+  const float* prow = p.part + static_cast<int64_t>(t) * p.N;
+  uint16_t* crow = p.C + static_cast<int64_t>(t) * p.ldc;
+  for (int n = 4 * static_cast<int>(threadIdx.x); n < p.N; n += 4 * kThreads) {
+    float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (p.N % 4 == 0) {
+      // Every split's 16 bytes are loaded before the in-order sum, so one
+      // round trip serves them all (a load per split in turn took one each).
+      f32x4 x[kMaxSplits];
+#pragma unroll
+      for (int sp = 0; sp < kMaxSplits; ++sp)
+        if (sp < p.splits) x[sp] = *reinterpret_cast<const f32x4*>(prow + sp * p.plane + n);
+#pragma unroll
+      for (int sp = 0; sp < kMaxSplits; ++sp)
+        if (sp < p.splits) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) v[r] += x[sp][r];
+        }
+    } else {
+      for (int sp = 0; sp < p.splits; ++sp) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          if (n + r < p.N) v[r] += prow[sp * p.plane + n + r];
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) v[r] += p.bias != nullptr ? E::to_float(p.bias[min(n + r, p.N - 1)]) : 0.0f;
+    if (p.vec_c && n + 3 < p.N) {
+      *reinterpret_cast<u32x2*>(crow + n) = u32x2{pack2<E>(v[0], v[1]), pack2<E>(v[2], v[3])};
+    } else {
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        if (n + r < p.N) crow[n + r] = E::from_float(v[r]);
+    }
+  }
+}
 
 // rotary_embedding followed by reshape_and_cache in one launch, one
 // workgroup per token. The thread that rotates a pair of k also writes it to
@@ -262,6 +314,10 @@ __global__ __launch_bounds__(kThreads) void rotary_and_cache_kernel(const KParam
   const int t = blockIdx.x;
   const rope::KParams& r = p.r;
   const cache::KParams& c = p.c;
+  if (p.part != nullptr) {  // the token's q | k | v row from the GEMM's partials, before anything reads it
+    reduce_row<E>(p, t);
+    __syncthreads();
+  }
   const int64_t pos = r.positions[t];
   const bool rot = pos >= 0 && pos < r.max_position;
   const int64_t slot = c.slots[t];
@@ -538,6 +594,7 @@ int check_scales(const char* op, float k_scale, float v_scale) {
 // 16-bit caches, or with fp8 caches when fp8 is set).
 int fused_params(const char* op, const dk_rotary_params* r, const dk_cache_write_params* c, int dtype, bool fp8,
                  rope_cache::KParams& kp, bool& neox, bool& vec, bool& empty) {
+  kp = rope_cache::KParams{};  // no split-K input unless the caller sets one
   bool rvec = false, cvec = false, cempty = false;
   if (const int rc = rotary_params(op, r, dtype, kp.r, neox, rvec, empty)) return rc;
   if (const int rc = cache_params(op, c, dtype, kp.c, cvec, cempty)) return rc;
@@ -555,6 +612,48 @@ int fused_params(const char* op, const dk_rotary_params* r, const dk_cache_write
 }
 
 }  // namespace
+
+// rotary_embedding_and_cache (fp8: into e4m3fn caches) whose q, k and v are
+// views of the rows of C [M, N]: row strides ldc, every head inside the row.
+// With part != nullptr, C's rows are first formed from a GEMM's split-K
+// partial planes (and bias), in the same launch. check_only: validate only.
+int rotary_and_cache_on_rows(const char* op, const dk_rotary_params* r, const dk_cache_write_params* c, int dtype,
+                             bool fp8, float k_scale, float v_scale, const float* part, int splits, const void* bias,
+                             void* C, int64_t ldc, int M, int N, bool check_only, hipStream_t s) {
+  rope_cache::KParams kp;
+  bool neox = false, vec = false, empty = false;
+  if (const int rc = fused_params(op, r, c, dtype, fp8, kp, neox, vec, empty)) return rc;
+  if (fp8) {
+    if (const int rc = check_scales(op, k_scale, v_scale)) return rc;
+  }
+  if (r->num_tokens != M) return fail("%s: one token per GEMM output row expected (%d tokens, %d rows)", op,
+                                      static_cast<int>(r->num_tokens), M);
+  auto inside = [&](const void* v, int64_t st, int64_t sh, int heads) {
+    const auto* b = static_cast<const uint16_t*>(C);
+    const auto* x = static_cast<const uint16_t*>(v);
+    return st == ldc && x >= b && sh >= 0 && (x - b) + (heads - 1) * sh + r->head_size <= N;
+  };
+  if (!inside(r->query, r->q_stride_token, r->q_stride_head, r->num_q_heads) ||
+      !inside(r->key, r->k_stride_token, r->k_stride_head, r->num_kv_heads) ||
+      !inside(c->value, c->v_stride_token, c->v_stride_head, c->num_kv_heads))
+    return fail("%s: query, key and value must be views of the GEMM output's rows", op);
+  if (check_only || empty) return 0;
+  if (part != nullptr && (splits < 1 || splits > rope_cache::kMaxSplits))
+    return fail("%s: %d K splits (at most %d)", op, splits, rope_cache::kMaxSplits);
+  if (part != nullptr) {
+    kp.part = part;
+    kp.bias = static_cast<const uint16_t*>(bias);
+    kp.C = static_cast<uint16_t*>(C);
+    kp.ldc = ldc;
+    kp.plane = static_cast<int64_t>(M) * N;
+    kp.N = N;
+    kp.splits = splits;
+    kp.vec_c = (ldc % 4 == 0 && aligned_to(C, 8)) ? 1 : 0;  // gemm_splitk_reduce_kernel's store choice
+  }
+  return static_cast<int>(fp8 ? rope_cache::launch_any<true>(kp, dtype, r->cache_dtype, neox, vec, k_scale, v_scale, s)
+                              : rope_cache::launch_any<false>(kp, dtype, r->cache_dtype, neox, vec, 1.0f, 1.0f, s));
+}
+
 }  // namespace dk
 
 extern "C" int dk_rotary_embedding(const dk_rotary_params* a, int dtype, void* stream) {

@@ -225,7 +225,19 @@ void paged_attention_decode_fp8(at::Tensor& out, const at::Tensor& q, const at::
 // ---------------------------------------------------------------------------
 // gemm_tn (csrc/ops.cu:149-182)
 // ---------------------------------------------------------------------------
-void gemm_tn(at::Tensor& c, const at::Tensor& a, const at::Tensor& b, const std::optional<at::Tensor>& bias) {
+namespace {
+
+// Checked arguments of a gemm_tn call, with its split-K workspace (decode
+// shapes that split K take it from the caching allocator; freed back to it
+// when the op returns, the stream order keeps it alive for the kernels).
+struct GemmArgs {
+  int dt, M, N, K, lda, ldb, ldc;
+  const void* bias;
+  at::Tensor ws;
+  int64_t ws_bytes;
+};
+
+GemmArgs gemm_args(at::Tensor& c, const at::Tensor& a, const at::Tensor& b, const std::optional<at::Tensor>& bias) {
   TORCH_CHECK(a.is_cuda(), "gemm_tn: tensors must be on CUDA");
   TORCH_CHECK(a.dim() == 2 && b.dim() == 2 && c.dim() == 2, "gemm_tn: a [M,K], b [N,K], c [M,N]");
   check_same(a, b, "a/b");
@@ -247,20 +259,50 @@ void gemm_tn(at::Tensor& c, const at::Tensor& a, const at::Tensor& b, const std:
     TORCH_CHECK(bias->dim() == 1 && bias->size(0) == N && bias->is_contiguous(), "gemm_tn: bias must be [N]");
     bias_ptr = bias->data_ptr();
   }
-  const int dt = dtype_code(a.scalar_type(), "gemm_tn");
+  GemmArgs g{};
+  g.dt = dtype_code(a.scalar_type(), "gemm_tn");
+  g.M = static_cast<int>(M);
+  g.N = static_cast<int>(N);
+  g.K = static_cast<int>(K);
+  g.lda = static_cast<int>(a.stride(0));
+  g.ldb = static_cast<int>(b.stride(0));
+  g.ldc = static_cast<int>(c.stride(0));
+  g.bias = bias_ptr;
+  g.ws_bytes = dk_gemm_tn_workspace_bytes(g.M, g.N, g.K);
+  if (g.ws_bytes > 0) g.ws = at::empty({g.ws_bytes / 4}, a.options().dtype(at::kFloat));
+  return g;
+}
+
+}  // namespace
+
+void gemm_tn(at::Tensor& c, const at::Tensor& a, const at::Tensor& b, const std::optional<at::Tensor>& bias) {
+  GemmArgs g = gemm_args(c, a, b, bias);
   const DeviceGuard guard(a.device());
-  // Decode shapes that split K take an fp32 workspace from the caching
-  // allocator (freed back to it when this call returns; the stream order keeps
-  // it alive for the kernels).
-  const int64_t ws_bytes =
-      dk_gemm_tn_workspace_bytes(static_cast<int>(M), static_cast<int>(N), static_cast<int>(K));
-  at::Tensor ws;
-  if (ws_bytes > 0) ws = at::empty({ws_bytes / 4}, a.options().dtype(at::kFloat));
-  check_status(dk_gemm_tn_ws(dt, a.data_ptr(), b.data_ptr(), bias_ptr, c.data_ptr(), static_cast<int>(M),
-                             static_cast<int>(N), static_cast<int>(K), static_cast<int>(a.stride(0)),
-                             static_cast<int>(b.stride(0)), static_cast<int>(c.stride(0)),
-                             ws_bytes > 0 ? ws.data_ptr() : nullptr, ws_bytes, stream_of(a)),
+  check_status(dk_gemm_tn_ws(g.dt, a.data_ptr(), b.data_ptr(), g.bias, c.data_ptr(), g.M, g.N, g.K, g.lda, g.ldb, g.ldc,
+                             g.ws_bytes > 0 ? g.ws.data_ptr() : nullptr, g.ws_bytes, stream_of(a)),
                "gemm_tn");
+}
+
+// gemm_tn into `out`, then fused_add_rms_norm(out, residual, weight, eps); the
+// split-K sum of decode shapes happens inside the norm's kernel (same bits as
+// the two ops).
+void gemm_tn_add_rms_norm(at::Tensor& out, const at::Tensor& a, const at::Tensor& b,
+                          const std::optional<at::Tensor>& bias, at::Tensor& residual, const at::Tensor& weight,
+                          double eps) {
+  GemmArgs g = gemm_args(out, a, b, bias);
+  const DeviceGuard guard(a.device());
+  check_same(out, residual, "out/residual");
+  check_same(out, weight, "out/weight");
+  TORCH_CHECK(residual.dim() == 2 && residual.size(0) == g.M && residual.size(1) == g.N && residual.stride(1) == 1,
+              "gemm_tn_add_rms_norm: residual must be [M, N] with contiguous rows");
+  TORCH_CHECK(residual.stride(0) < (int64_t{1} << 31), "gemm_tn_add_rms_norm: residual row stride must fit in 32 bits");
+  TORCH_CHECK(weight.dim() == 1 && weight.size(0) == g.N && weight.is_contiguous(),
+              "gemm_tn_add_rms_norm: weight must be [N]");
+  check_status(dk_gemm_tn_add_rms_norm(g.dt, a.data_ptr(), b.data_ptr(), g.bias, out.data_ptr(), residual.data_ptr(),
+                                       weight.data_ptr(), static_cast<float>(eps), g.M, g.N, g.K, g.lda, g.ldb, g.ldc,
+                                       static_cast<int>(residual.stride(0)),
+                                       g.ws_bytes > 0 ? g.ws.data_ptr() : nullptr, g.ws_bytes, stream_of(a)),
+               "gemm_tn_add_rms_norm");
 }
 
 // ---------------------------------------------------------------------------
@@ -496,6 +538,49 @@ void rotary_embedding_and_cache_fp8(const at::Tensor& positions, at::Tensor& que
                "rotary_embedding_and_cache_fp8");
 }
 
+// gemm_tn into qkv, then rotary_embedding_and_cache on the query / key / value
+// views of qkv's rows; the split-K sum of decode shapes happens inside the
+// rotary / cache kernel (same bits as the two ops).
+void gemm_tn_rotary_embedding_and_cache(at::Tensor& qkv, const at::Tensor& a, const at::Tensor& b,
+                                        const std::optional<at::Tensor>& bias, const at::Tensor& positions,
+                                        at::Tensor& query, at::Tensor& key, const at::Tensor& value,
+                                        int64_t head_size, const at::Tensor& cos_sin_cache, bool is_neox,
+                                        at::Tensor& key_cache, at::Tensor& value_cache,
+                                        const at::Tensor& slot_mapping) {
+  GemmArgs g = gemm_args(qkv, a, b, bias);
+  const DeviceGuard guard(a.device());
+  int dt = 0, dt2 = 0;
+  const dk_rotary_params r = rotary_params(positions, query, key, head_size, cos_sin_cache, is_neox, dt);
+  const dk_cache_write_params c = cache_params(key, value, key_cache, value_cache, slot_mapping, dt2);
+  TORCH_CHECK(key_cache.size(3) == head_size, "gemm_tn_rotary_embedding_and_cache: cache head_size must equal head_size");
+  check_status(dk_gemm_tn_rotary_embedding_and_cache(g.dt, a.data_ptr(), b.data_ptr(), g.bias, qkv.data_ptr(), g.M,
+                                                     g.N, g.K, g.lda, g.ldb, g.ldc, &r, &c,
+                                                     g.ws_bytes > 0 ? g.ws.data_ptr() : nullptr, g.ws_bytes,
+                                                     stream_of(a)),
+               "gemm_tn_rotary_embedding_and_cache");
+}
+
+// The same into fp8 (e4m3fn) caches with per-tensor scales.
+void gemm_tn_rotary_embedding_and_cache_fp8(at::Tensor& qkv, const at::Tensor& a, const at::Tensor& b,
+                                            const std::optional<at::Tensor>& bias, const at::Tensor& positions,
+                                            at::Tensor& query, at::Tensor& key, const at::Tensor& value,
+                                            int64_t head_size, const at::Tensor& cos_sin_cache, bool is_neox,
+                                            at::Tensor& key_cache, at::Tensor& value_cache,
+                                            const at::Tensor& slot_mapping, double k_scale, double v_scale) {
+  GemmArgs g = gemm_args(qkv, a, b, bias);
+  const DeviceGuard guard(a.device());
+  int dt = 0, dt2 = 0;
+  const dk_rotary_params r = rotary_params(positions, query, key, head_size, cos_sin_cache, is_neox, dt);
+  const dk_cache_write_params c = cache_params(key, value, key_cache, value_cache, slot_mapping, dt2, true);
+  TORCH_CHECK(key_cache.size(3) == head_size,
+              "gemm_tn_rotary_embedding_and_cache_fp8: cache head_size must equal head_size");
+  check_status(dk_gemm_tn_rotary_embedding_and_cache_fp8(
+                   g.dt, a.data_ptr(), b.data_ptr(), g.bias, qkv.data_ptr(), g.M, g.N, g.K, g.lda, g.ldb, g.ldc, &r,
+                   &c, static_cast<float>(k_scale), static_cast<float>(v_scale),
+                   g.ws_bytes > 0 ? g.ws.data_ptr() : nullptr, g.ws_bytes, stream_of(a)),
+               "gemm_tn_rotary_embedding_and_cache_fp8");
+}
+
 // ---------------------------------------------------------------------------
 // Registration (csrc/ops.cu:270-286)
 // ---------------------------------------------------------------------------
@@ -525,6 +610,17 @@ TORCH_LIBRARY(decode_kernels, m) {
       "rotary_embedding_and_cache_fp8(Tensor positions, Tensor! query, Tensor! key, Tensor value, int head_size, "
       "Tensor cos_sin_cache, bool is_neox, Tensor! key_cache, Tensor! value_cache, Tensor slot_mapping, "
       "float k_scale, float v_scale) -> ()");
+  m.def(
+      "gemm_tn_add_rms_norm(Tensor! out, Tensor a, Tensor b, Tensor? bias, Tensor! residual, Tensor weight, "
+      "float eps) -> ()");
+  m.def(
+      "gemm_tn_rotary_embedding_and_cache(Tensor! qkv, Tensor a, Tensor b, Tensor? bias, Tensor positions, "
+      "Tensor! query, Tensor! key, Tensor value, int head_size, Tensor cos_sin_cache, bool is_neox, "
+      "Tensor! key_cache, Tensor! value_cache, Tensor slot_mapping) -> ()");
+  m.def(
+      "gemm_tn_rotary_embedding_and_cache_fp8(Tensor! qkv, Tensor a, Tensor b, Tensor? bias, Tensor positions, "
+      "Tensor! query, Tensor! key, Tensor value, int head_size, Tensor cos_sin_cache, bool is_neox, "
+      "Tensor! key_cache, Tensor! value_cache, Tensor slot_mapping, float k_scale, float v_scale) -> ()");
 }
 
 TORCH_LIBRARY_IMPL(decode_kernels, CUDA, m) {
@@ -539,6 +635,9 @@ TORCH_LIBRARY_IMPL(decode_kernels, CUDA, m) {
   m.impl("rotary_embedding_and_cache", &rotary_embedding_and_cache);
   m.impl("reshape_and_cache_fp8", &reshape_and_cache_fp8);
   m.impl("rotary_embedding_and_cache_fp8", &rotary_embedding_and_cache_fp8);
+  m.impl("gemm_tn_add_rms_norm", &gemm_tn_add_rms_norm);
+  m.impl("gemm_tn_rotary_embedding_and_cache", &gemm_tn_rotary_embedding_and_cache);
+  m.impl("gemm_tn_rotary_embedding_and_cache_fp8", &gemm_tn_rotary_embedding_and_cache_fp8);
 }
 
 // Python module entry point: an empty module; importing it loads this

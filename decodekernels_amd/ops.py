@@ -116,6 +116,26 @@ if _AVAILABLE:
               k_scale, v_scale):
             return None
 
+    if _has_op("gemm_tn_add_rms_norm"):
+
+        @torch.library.register_fake("decode_kernels::gemm_tn_add_rms_norm")
+        def _(out, a, b, bias, residual, weight, eps):
+            return None
+
+    if _has_op("gemm_tn_rotary_embedding_and_cache"):
+
+        @torch.library.register_fake("decode_kernels::gemm_tn_rotary_embedding_and_cache")
+        def _(qkv, a, b, bias, positions, query, key, value, head_size, cos_sin_cache, is_neox, key_cache,
+              value_cache, slot_mapping):
+            return None
+
+    if _has_op("gemm_tn_rotary_embedding_and_cache_fp8"):
+
+        @torch.library.register_fake("decode_kernels::gemm_tn_rotary_embedding_and_cache_fp8")
+        def _(qkv, a, b, bias, positions, query, key, value, head_size, cos_sin_cache, is_neox, key_cache,
+              value_cache, slot_mapping, k_scale, v_scale):
+            return None
+
 
 # ---------------------------------------------------------------------------
 # Paged attention
@@ -318,3 +338,72 @@ def rotary_embedding_and_cache(
         positions, query, key, value, int(head_size), cos_sin_cache, bool(is_neox), key_cache, value_cache, slot_mapping
     )
     return query, key
+
+
+# ---------------------------------------------------------------------------
+# Decode-layer fusions: a GEMM with the op that consumes its output (no
+# counterpart in DecodeKernels). At decode sizes the GEMM splits K and the
+# consumer's kernel sums the partial tiles itself; the results equal the two
+# calls in sequence bit for bit.
+# ---------------------------------------------------------------------------
+def gemm_add_rms_norm(
+    a: torch.Tensor,
+    b: torch.Tensor,
+    residual: torch.Tensor,
+    weight: torch.Tensor,
+    eps: float = 1e-6,
+    bias: torch.Tensor | None = None,
+    out: torch.Tensor | None = None,
+):
+    """``out = gemm(a, b, bias)`` then ``fused_add_rms_norm(out, residual, weight,
+    eps)`` (residual updated in place): the o projection into the
+    post-attention norm, or the down projection into the next layer's input
+    norm. a: [M, K], b: [N, K], residual: [M, N]. Returns (out, residual)."""
+    _require()
+    if out is None:
+        out = torch.empty(a.shape[0], b.shape[0], dtype=a.dtype, device=a.device)
+    torch.ops.decode_kernels.gemm_tn_add_rms_norm(out, a, b, bias, residual, weight, float(eps))
+    return out, residual
+
+
+def gemm_rotary_embedding_and_cache(
+    a: torch.Tensor,
+    b: torch.Tensor,
+    qkv: torch.Tensor,
+    num_q_heads: int,
+    num_kv_heads: int,
+    positions: torch.Tensor,
+    head_size: int,
+    cos_sin_cache: torch.Tensor,
+    is_neox: bool,
+    key_cache: torch.Tensor,
+    value_cache: torch.Tensor,
+    slot_mapping: torch.Tensor,
+    bias: torch.Tensor | None = None,
+    k_scale: float = 1.0,
+    v_scale: float = 1.0,
+):
+    """``qkv = gemm(a, b, bias)`` (the fused q | k | v projection, [tokens,
+    (num_q_heads + 2 num_kv_heads) head_size] or wider), then
+    ``rotary_embedding_and_cache`` of its q, k and v columns: q and k rotated
+    in place in ``qkv``, the rotated k and v written to the cache slots (also
+    ``torch.float8_e4m3fn`` caches with k_scale / v_scale). Returns (query,
+    key, value) as views of ``qkv``."""
+    _require()
+    hq, hkv, d = int(num_q_heads), int(num_kv_heads), int(head_size)
+    query = qkv[:, : hq * d]
+    key = qkv[:, hq * d : (hq + hkv) * d]
+    value = qkv[:, (hq + hkv) * d : (hq + 2 * hkv) * d]
+    if key_cache.dtype == torch.float8_e4m3fn:
+        torch.ops.decode_kernels.gemm_tn_rotary_embedding_and_cache_fp8(
+            qkv, a, b, bias, positions, query, key, value, d, cos_sin_cache, bool(is_neox), key_cache, value_cache,
+            slot_mapping, float(k_scale), float(v_scale)
+        )
+    else:
+        if k_scale != 1.0 or v_scale != 1.0:
+            raise ValueError("k_scale / v_scale apply to an fp8 (float8_e4m3fn) KV cache only")
+        torch.ops.decode_kernels.gemm_tn_rotary_embedding_and_cache(
+            qkv, a, b, bias, positions, query, key, value, d, cos_sin_cache, bool(is_neox), key_cache, value_cache,
+            slot_mapping
+        )
+    return query, key, value

@@ -280,6 +280,45 @@ int dk_rotary_embedding_and_cache(const dk_rotary_params* r, const dk_cache_writ
 int dk_rotary_embedding_and_cache_fp8(const dk_rotary_params* r, const dk_cache_write_params* c, int dtype,
                                       float k_scale, float v_scale, void* stream);
 
+/*
+ * Decode-layer fusions of a GEMM with the op that consumes its output. The
+ * GEMM's plan splits K at decode sizes (see dk_gemm_tn_ws); the consumer's
+ * kernel then sums the fp32 partial tiles itself, in split order, and rounds
+ * them exactly as the GEMM's own reduce kernel would, so each call equals the
+ * two calls in sequence bit for bit while launching one kernel fewer. Plans
+ * that do not split run the two ops in sequence. workspace / workspace_bytes
+ * as for dk_gemm_tn_ws (dk_gemm_tn_workspace_bytes(M, N, K); NULL: no split).
+ * No counterpart in DecodeKernels, whose decode step runs gemm_tn and the
+ * norm (csrc/ops.cu:149-182, 200-265) as separate launches and leaves the
+ * rotary embedding and cache write to the serving engine.
+ *
+ * dk_gemm_tn_add_rms_norm: out = A B^T (+ bias) as dk_gemm_tn_ws [M, N] (row
+ * stride ld_out), then dk_fused_add_rms_norm(out, residual, weight, eps)
+ * over its M rows of N: residual = round(out + residual), out =
+ * rms_norm(residual) * weight. The o projection into the post-attention
+ * norm, or the down projection into the next layer's input norm.
+ */
+int dk_gemm_tn_add_rms_norm(int dtype, const void* A, const void* B, const void* bias, void* out, void* residual,
+                            const void* weight, float eps, int M, int N, int K, int lda, int ldb, int ld_out,
+                            int ld_res, void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
+ * dk_gemm_tn_rotary_embedding_and_cache: C = A B^T (+ bias) as dk_gemm_tn_ws
+ * (a fused q | k | v projection), then dk_rotary_embedding_and_cache(r, c).
+ * r->query, r->key (== c->key) and c->value must be views of C's rows (token
+ * stride ldc, every head inside the row) and r->num_tokens == M. _fp8: the
+ * caches are e4m3fn, as dk_rotary_embedding_and_cache_fp8.
+ */
+int dk_gemm_tn_rotary_embedding_and_cache(int dtype, const void* A, const void* B, const void* bias, void* C, int M,
+                                          int N, int K, int lda, int ldb, int ldc, const dk_rotary_params* r,
+                                          const dk_cache_write_params* c, void* workspace, int64_t workspace_bytes,
+                                          void* stream);
+int dk_gemm_tn_rotary_embedding_and_cache_fp8(int dtype, const void* A, const void* B, const void* bias, void* C,
+                                              int M, int N, int K, int lda, int ldb, int ldc,
+                                              const dk_rotary_params* r, const dk_cache_write_params* c,
+                                              float k_scale, float v_scale, void* workspace, int64_t workspace_bytes,
+                                              void* stream);
+
 /* Description of the last argument error raised on this thread ("" if none).
  * The reference reports these through TORCH_CHECK messages (csrc/ops.cu). */
 const char* dk_last_error(void);

@@ -41,8 +41,9 @@ EPS = 1e-5
 
 
 class Layer:
-    def __init__(self, seq_lens, dtype, seed=0, fused_rope_cache=False, inter=INTER):
+    def __init__(self, seq_lens, dtype, seed=0, fused_rope_cache=False, inter=INTER, fused_gemm=False):
         self.fused_rope_cache = fused_rope_cache
+        self.fused_gemm = fused_gemm  # qkv gemm + rope / cache and o gemm + norm as the fused ops
         g = torch.Generator(device="cuda").manual_seed(seed)
         kw = dict(device="cuda", dtype=dtype)
         self.dtype = dtype
@@ -91,10 +92,17 @@ class Layer:
         ops.fused_add_rms_norm(self.x, self.resid, self.ln1, EPS)
         if keep:
             self.saved["norm1"] = (self.x.clone(), self.resid.clone())
-        ops.gemm_tn(self.qkv, self.x, self.w_qkv, None)
+        if self.fused_gemm:
+            ops.gemm_tn_rotary_embedding_and_cache(self.qkv, self.x, self.w_qkv, None, self.positions,
+                                                   self.qkv[:, : HQ * D], self.k_new, self.v_new, D, self.rope, True,
+                                                   self.kv.k_cache, self.kv.v_cache, self.slots)
+        else:
+            ops.gemm_tn(self.qkv, self.x, self.w_qkv, None)
         if keep:
             self.saved["qkv"] = self.qkv.clone()
-        if self.fused_rope_cache:
+        if self.fused_gemm:
+            pass
+        elif self.fused_rope_cache:
             if keep:
                 self.saved["k_cache"] = self.kv.k_cache.clone()
                 self.saved["v_cache"] = self.kv.v_cache.clone()
@@ -108,11 +116,14 @@ class Layer:
             ops.reshape_and_cache(self.k_new, self.v_new, self.kv.k_cache, self.kv.v_cache, self.slots)
         dk.paged_attention_decode(self.q, self.kv.k_cache, self.kv.v_cache, self.kv.block_tables, self.kv.seq_lens,
                                   max_seq_len=self.max_len, out=self.attn, workspace=self.ws)
-        ops.gemm_tn(self.o, self.attn.view(self.n, HIDDEN), self.w_o, None)
-        if keep:
-            self.saved["o"] = self.o.clone()
-            self.saved["resid1"] = self.resid.clone()
-        ops.fused_add_rms_norm(self.o, self.resid, self.ln2, EPS)
+        if self.fused_gemm:
+            ops.gemm_tn_add_rms_norm(self.o, self.attn.view(self.n, HIDDEN), self.w_o, None, self.resid, self.ln2, EPS)
+        else:
+            ops.gemm_tn(self.o, self.attn.view(self.n, HIDDEN), self.w_o, None)
+            if keep:
+                self.saved["o"] = self.o.clone()
+                self.saved["resid1"] = self.resid.clone()
+            ops.fused_add_rms_norm(self.o, self.resid, self.ln2, EPS)
         ops.gemm_tn(self.gu, self.o, self.w_gu, None)
         ops.silu_and_mul(self.act, self.gu)
         ops.gemm_tn(self.down, self.act, self.w_down, None)
@@ -207,6 +218,41 @@ def test_layer_step_graph_replays_match_eager(fused):
         names = ("qkv", "k_cache", "v_cache", "attn", "o", "resid", "gate_up", "act", "down")
         for name, a, b in zip(names, got, want):
             assert torch.equal(a, b), f"replay {i}: {name} differs from the eager step"
+
+
+def test_layer_step_fused_gemms_equal_unfused():
+    """64 sequences (decode batch 64, the shapes whose GEMM plans split K): the
+    step with the qkv GEMM fused into rotary_embedding_and_cache and the o GEMM
+    fused into the post-attention norm gives the same bits as the unfused step,
+    and so does a graph replay of it."""
+    from decodekernels_amd import capi
+
+    g = torch.Generator().manual_seed(8)
+    lens = [int(x) for x in torch.randint(1, 3000, (64,), generator=g)]
+    lens[5] = 0
+    assert capi.gemm_plan(64, (HQ + 2 * HKV) * D, HIDDEN)[2] > 1 and capi.gemm_plan(64, HIDDEN, HIDDEN)[2] > 1
+    a = Layer(lens, torch.bfloat16, seed=9)
+    b = Layer(lens, torch.bfloat16, seed=9, fused_gemm=True)
+    a.step()
+    b.step()
+    torch.cuda.synchronize()
+    names = ("qkv", "k_cache", "v_cache", "attn", "o", "resid", "gate_up", "act", "down")
+    want = a.outputs()
+    for name, x, y in zip(names, want, b.outputs()):
+        assert torch.equal(x, y), f"{name} differs between the fused-GEMM and the unfused step"
+    graph = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        b.step()
+    torch.cuda.current_stream().wait_stream(side)
+    with torch.cuda.graph(graph):
+        b.step()
+    for _ in range(3):
+        graph.replay()
+        torch.cuda.synchronize()
+        for name, x, y in zip(names, want, b.outputs()):
+            assert torch.equal(x, y), f"{name} differs in a replay of the fused-GEMM step"
 
 
 def test_layer_step_fused_rope_cache_equals_two_ops():
