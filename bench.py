@@ -610,8 +610,12 @@ def extras_layer_step() -> dict:
         ("llama3_8b_b64_bf16", (64, 32, 8, 128, 16, torch.randint(512, 4097, (64,), generator=torch.Generator().manual_seed(0)).tolist(),
                                 torch.bfloat16, "vllm")),
     )
-    def timed(fns: dict) -> tuple[float, float]:
-        """Eager (back to back) and HIP-graph replay time of one step."""
+    def timed(fns: dict) -> tuple[float, float, float]:
+        """Eager (back to back) and HIP-graph replay time of one step, and the
+        per-step time of a graph of 8 consecutive steps (8 layers): each graph
+        launch starts ~8 us after the previous one ends on the device (a kernel
+        trace shows the kernels inside a replay back to back), which one
+        step per graph pays in full and 8 steps share."""
         def step():
             for fn in fns.values():
                 fn()
@@ -626,8 +630,13 @@ def extras_layer_step() -> dict:
         with torch.cuda.graph(graph):
             step()
         replay = time_back_to_back(graph.replay, 20, 3) * 1e3
-        del graph
-        return eager, replay
+        graph8 = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph8):
+            for _ in range(8):
+                step()
+        replay8 = time_back_to_back(graph8.replay, 5, 2) * 1e3 / 8
+        del graph, graph8
+        return eager, replay, replay8
 
     for name, args in cases:
         ops, unfused, fused, nbytes, check, check_fused = layer_step(*args, seed=50)
@@ -640,13 +649,15 @@ def extras_layer_step() -> dict:
         fused_per_op = {k: time_cold(fn, iters=20)["median_us"] for k, fn in fused.items()
                         if k not in ("attention", "gate_up_gemm", "silu_and_mul")}
         unfused_us = {k: time_cold(fn, iters=20)["median_us"] for k, fn in unfused.items()}
-        eager_us, graph_us = timed(fused)
-        u_eager_us, u_graph_us = timed(ops)
+        eager_us, graph_us, graph8_us = timed(fused)
+        u_eager_us, u_graph_us, u_graph8_us = timed(ops)
         res[name] = {
             "eager_us": round(eager_us, 1), "graph_us": round(graph_us, 1),
+            "graph_8_steps_us_per_step": round(graph8_us, 1),
             "step": "fused decode GEMMs: qkv -> rotary_embedding_and_cache, o -> post-attention norm, "
                     "down -> next layer's input norm (the split-K sums done by the consumers)",
             "unfused": {"eager_us": round(u_eager_us, 1), "graph_us": round(u_graph_us, 1),
+                        "graph_8_steps_us_per_step": round(u_graph8_us, 1),
                         "step": "norm -> qkv -> rotary_embedding_and_cache -> attention -> o -> norm -> gate_up "
                                 "-> silu_and_mul -> down, one op per launch"},
             "sum_of_cold_ops_us": round(sum(per_op.values()), 1), "ops_cold_us": per_op,
@@ -657,8 +668,9 @@ def extras_layer_step() -> dict:
             "graph_GB/s": round(nbytes / (graph_us * 1e-6) / 1e9, 1),
             "checked_before_timing": checked,
         }
-        progress(f"layer step {name}: fused eager {eager_us:.1f} us, graph {graph_us:.1f} us; "
-                 f"unfused eager {u_eager_us:.1f} us, graph {u_graph_us:.1f} us")
+        progress(f"layer step {name}: fused eager {eager_us:.1f} us, graph {graph_us:.1f} us "
+                 f"(8-step graph {graph8_us:.1f} us/step); unfused eager {u_eager_us:.1f} us, graph {u_graph_us:.1f} us "
+                 f"(8-step graph {u_graph8_us:.1f} us/step)")
         del ops, fused
         torch.cuda.empty_cache()
     return res
@@ -813,6 +825,42 @@ def pmc_workload_norm(calls: int = 3) -> None:
     print(f"pmc norm workload done: {calls} cold calls of each op at 64 and 16384 tokens", flush=True)
 
 
+def pmc_workload_layer_graph(steps: int = 20) -> None:
+    """What the graph-against-eager kernel trace records: the Llama-3-8B batch-64
+    decode-layer step, fused and unfused, `steps` eager steps and then `steps`
+    replays of a one-step HIP graph, each phase between two marker kernels (an
+    add on a 1-element tensor before it, on a 3-element one after it)."""
+    seq_lens = torch.randint(512, 4097, (64,), generator=torch.Generator().manual_seed(0)).tolist()
+    ops, _, fused, _, _, _ = layer_step(64, 32, 8, 128, 16, seq_lens, torch.bfloat16, "vllm", seed=50)
+    before, after = torch.zeros(1, device="cuda"), torch.zeros(3, device="cuda")
+    for name, fns in (("fused", fused), ("unfused", ops)):
+        def step():
+            for fn in fns.values():
+                fn()
+
+        for _ in range(5):
+            step()
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            step()
+        torch.cuda.current_stream().wait_stream(side)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            step()
+        torch.cuda.synchronize()
+        for run in (step, graph.replay):
+            before.add_(1.0)
+            torch.cuda.synchronize()
+            for _ in range(steps):
+                run()
+            torch.cuda.synchronize()
+            after.add_(1.0)
+            torch.cuda.synchronize()
+        del graph
+    print(f"layer graph workload done: fused and unfused step, {steps} eager steps then {steps} replays each", flush=True)
+
+
 def pmc_workload(calls: int = 5) -> None:
     """What the counter runs profile: the headline op `calls` times, then a
     copy of CALIBRATION_BYTES (read once, written once) to scale the counters."""
@@ -858,8 +906,9 @@ def main() -> int:
     ap.add_argument("--no-extras", action="store_true", help="skip the secondary configs")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline (and its correctness check)")
     ap.add_argument("--pmc-workload", nargs="?", const="attention",
-                    choices=["attention", "attention_cold", "attention_fp8", "gemm", "gemm_skinny", "norm"],
-                    help="run only what the rocprofv3 --pmc passes profile (default: attention)")
+                    choices=["attention", "attention_cold", "attention_fp8", "gemm", "gemm_skinny", "norm",
+                             "layer_graph"],
+                    help="run only what the rocprofv3 --pmc / --kernel-trace passes profile (default: attention)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: every work unit of this path fits one MI355X and no multi-GPU "
@@ -881,6 +930,9 @@ def main() -> int:
         return 0
     if args.pmc_workload == "norm":
         pmc_workload_norm()
+        return 0
+    if args.pmc_workload == "layer_graph":
+        pmc_workload_layer_graph()
         return 0
     if args.pmc_workload:
         pmc_workload()
