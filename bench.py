@@ -304,6 +304,26 @@ def half_ulp_bar(ref_f32: torch.Tensor, dtype) -> torch.Tensor:
     return half.clamp(min=2e-2 if dtype == torch.bfloat16 else 5e-3)
 
 
+def check_gemm(out: torch.Tensor, a: torch.Tensor, w: torch.Tensor, bias=None, what: str = "gemm") -> float:
+    """gemm_tn's output against an fp32 GEMM of the same inputs (the oracle's
+    formula, on the GPU for speed) at the parity bar of the tests: max(2e-2
+    bf16 / 5e-3 fp16, half an ulp) plus the fp32 accumulation-order slack
+    2^-23 sqrt(K) (|A| |W|^T + |bias|). Returns the max abs error."""
+    af, wf = a.float(), w.float()
+    ref = af @ wf.t()
+    slack = af.abs() @ wf.abs().t()
+    if bias is not None:
+        ref = ref + bias.float()
+        slack = slack + bias.float().abs()
+    err = (out.float() - ref).abs()
+    tol = half_ulp_bar(ref, out.dtype) + slack * (2.0**-23 * a.shape[-1] ** 0.5)
+    if (err > tol).any():
+        raise AssertionError(f"{what}: differs from an fp32 GEMM by {err.max().item():.3e} (over the bar) before timing")
+    worst = err.max().item()
+    del ref, slack, err, tol
+    return worst
+
+
 def ulps(a: torch.Tensor, b: torch.Tensor) -> int:
     """Max distance in units in the last place between two 16-bit float tensors."""
     def key(t):
@@ -388,10 +408,7 @@ def extras_gemm() -> dict:
             a = torch.randn(m, k, generator=g, device="cuda", dtype=torch.bfloat16) * 0.02
             out = torch.empty(m, n, device="cuda", dtype=torch.bfloat16)
             torch.ops.decode_kernels.gemm_tn(out, a, w, None)
-            ref = F.linear(a, w)
-            err = (out.float() - ref.float()).abs().max().item()
-            if err > 2e-2:
-                raise AssertionError(f"gemm {name} M={m}: max abs err {err:.3e} vs hipBLASLt before timing")
+            err = check_gemm(out, a, w, what=f"gemm {name} M={m}")
             iters = 10 if m == 4096 else 30
             t = time_cold_interleaved({"dk": lambda: torch.ops.decode_kernels.gemm_tn(out, a, w, None),
                                        "hipblaslt": lambda: F.linear(a, w)}, iters=iters)
@@ -403,6 +420,7 @@ def extras_gemm() -> dict:
                 "dk_over_hipblaslt": round(t_dk["median_us"] / t_bl["median_us"], 3),
                 "TFLOP/s": round(flops / (t_dk["median_us"] * 1e-6) / 1e12, 1),
                 "GB/s": round(nbytes / (t_dk["median_us"] * 1e-6) / 1e9, 1),
+                "checked_max_abs_err": err,
             }
             if CPU_PATH:
                 a_c = a.cpu()
@@ -582,11 +600,7 @@ def layer_step(num_seqs, hq, hkv, d, bs, seq_lens, dtype, layout, seed, hidden=4
         errs = {"attention": check_attention(dict(case, q=q, out=attn, run=ops["attention"]), "layer-step attention",
                                              sample=2)}
         for name, a, w, c in (("gate_up_gemm", o, w_gu, gu), ("down_gemm", act, w_down, down)):
-            ref = a.float() @ w.float().t()
-            err = (c.float() - ref).abs()
-            if (err > half_ulp_bar(ref, dtype)).any():
-                raise AssertionError(f"layer-step {name} differs from an fp32 GEMM by {err.max().item():.3e}")
-            errs[name] = err.max().item()
+            errs[name] = check_gemm(c, a, w, what=f"layer-step {name}")
         u = ulps(act, silu_and_mul_reference(gu.cpu()))
         if u > 1:
             raise AssertionError(f"layer-step silu_and_mul {u} ulp from the oracle")
@@ -825,6 +839,122 @@ def pmc_workload_norm(calls: int = 3) -> None:
     print(f"pmc norm workload done: {calls} cold calls of each op at 64 and 16384 tokens", flush=True)
 
 
+# ---------------------------------------------------------------------------
+# The reference's benchmark sweep (opt-in: --sweep)
+# ---------------------------------------------------------------------------
+SWEEP_ATTN_MODELS = (("llama3-8b", 32, 8, 128), ("qwen2.5-7b", 28, 4, 128), ("qwen2.5-0.5b", 14, 2, 64))
+SWEEP_GEMM_SHAPES = (("qkv_proj", 6144, 4096), ("o_proj", 4096, 4096), ("gate_up_proj", 28672, 4096),
+                     ("down_proj", 4096, 14336))
+SWEEP_MAX_KV_BYTES = 6 * 1024**3  # the reference skips attention configs whose KV cache exceeds this
+
+
+def sweep(dtype, quick: bool, out_path: str | None) -> int:
+    """The grid of DecodeKernels' own benchmark (benchmarks/bench_kernels.py:37-54,
+    227-230): paged decode attention for 3 models x batch {1, 8, 32, 64} x
+    context {512, 2048, 8192, 32768} (every sequence of the context length,
+    block 16, NHD cache, KV caches above 6 GiB skipped as there); gemm_tn at the
+    4 Llama-3-8B projections x M {1, 8, 32, 64, 128, 512, 2048} next to
+    hipBLASLt (F.linear, timed interleaved); rms_norm and fused_add_rms_norm
+    (H 4096) and silu_and_mul (d 14336) at {1, 32, 256, 2048} tokens. Every row
+    is checked before it is timed -- attention on its 2 longest sequences
+    against the CPU oracle at the parity bar, GEMMs against an fp32 GEMM at the
+    bar, norms and SiLU at 1 ulp of the oracle -- and timed as the median of
+    cold-cache calls, with its roofline fraction (HBM 8 TB/s; GEMM also the
+    bf16 / fp16 MFMA peak). One JSON line per row on stdout (and in out_path)."""
+    from oracle.reference import fused_add_rms_norm_reference, rms_norm_reference, silu_and_mul_reference
+
+    torch.backends.cuda.preferred_blas_library("cublaslt")  # hipBLASLt on ROCm
+    batches = (1, 8) if quick else (1, 8, 32, 64)
+    ctxs = (512, 4096) if quick else (512, 2048, 8192, 32768)
+    ms = (1, 64, 512) if quick else (1, 8, 32, 64, 128, 512, 2048)
+    tokens = (1, 256) if quick else (1, 32, 256, 2048)
+    elt = torch.finfo(dtype).bits // 8
+    tag = "bf16" if dtype == torch.bfloat16 else "fp16"
+    sink = open(out_path, "w") if out_path else None
+
+    def emit(row: dict) -> None:
+        row = {"dtype": tag, **row}
+        line = json.dumps(row)
+        print(line, flush=True)
+        if sink:
+            sink.write(line + "\n")
+            sink.flush()
+
+    def rate(nbytes: float, us: float) -> dict:
+        gbs = nbytes / (us * 1e-6) / 1e9
+        return {"GB/s": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 3)}
+
+    for name, hq, hkv, d in SWEEP_ATTN_MODELS:
+        for b in batches:
+            for ctx in ctxs:
+                cfg = f"{name} bs={b} ctx={ctx}"
+                kv_bytes = 2 * b * ctx * hkv * d * elt
+                if kv_bytes > SWEEP_MAX_KV_BYTES:
+                    emit({"op": "attention", "config": cfg, "skipped": f"KV cache {kv_bytes / 1e9:.1f} GB > 6 GiB"})
+                    continue
+                c = attention_case(b, hq, hkv, d, 16, [ctx] * b, dtype, "nhd", seed=b + ctx)
+                err = check_attention(c, f"sweep attention {cfg}", sample=2)
+                t = time_cold(c["run"], iters=20)
+                emit({"op": "attention", "config": cfg, "us": t["median_us"], "p10_us": t["p10_us"],
+                      "p90_us": t["p90_us"], "MB": round(c["bytes"] / 1e6, 2), **rate(c["bytes"], t["median_us"]),
+                      "checked_max_abs_err": err})
+                progress(f"sweep attention {cfg}: {t['median_us']} us")
+                del c
+                torch.cuda.empty_cache()
+    g = torch.Generator(device="cuda").manual_seed(70)
+    peak = BF16_PEAK_TFLOPS
+    for name, n, k in SWEEP_GEMM_SHAPES:
+        w = torch.randn(n, k, generator=g, device="cuda", dtype=dtype) * k**-0.5
+        for m in ms:
+            a = torch.randn(m, k, generator=g, device="cuda", dtype=dtype)
+            out = torch.empty(m, n, device="cuda", dtype=dtype)
+            torch.ops.decode_kernels.gemm_tn(out, a, w, None)
+            err = check_gemm(out, a, w, what=f"sweep gemm {name} M={m}")
+            t = time_cold_interleaved({"dk": lambda: torch.ops.decode_kernels.gemm_tn(out, a, w, None),
+                                       "hipblaslt": lambda: F.linear(a, w)}, iters=10 if m >= 512 else 20)
+            us, bl = t["dk"]["median_us"], t["hipblaslt"]["median_us"]
+            flops, nbytes = 2.0 * m * n * k, (m * k + n * k + m * n) * elt
+            tf = flops / (us * 1e-6) / 1e12
+            emit({"op": "gemm_tn", "config": f"{name} M={m} N={n} K={k}", "us": us, "hipblaslt_us": bl,
+                  "dk_over_hipblaslt": round(us / bl, 3), "TFLOP/s": round(tf, 1), "mfma_frac": round(tf / peak, 3),
+                  **rate(nbytes, us), "checked_max_abs_err": err})
+            progress(f"sweep gemm {name} M={m}: {us} us ({us / bl:.3f}x hipBLASLt)")
+        del w
+    h, dmlp = 4096, 14336
+    wt = (1 + 0.1 * torch.randn(h, generator=g, device="cuda")).to(dtype)
+    for t_ in tokens:
+        x = torch.randn(t_, h, generator=g, device="cuda", dtype=dtype)
+        r = torch.randn(t_, h, generator=g, device="cuda", dtype=dtype)
+        xs = torch.randn(t_, 2 * dmlp, generator=g, device="cuda", dtype=dtype)
+        out, ys = torch.empty_like(x), torch.empty(t_, dmlp, device="cuda", dtype=dtype)
+        torch.ops.decode_kernels.rms_norm(out, x, wt, 1e-6)
+        u_rms = ulps(out, rms_norm_reference(x.cpu(), wt.cpu(), 1e-6))
+        xc, rc = x.clone(), r.clone()
+        torch.ops.decode_kernels.fused_add_rms_norm(xc, rc, wt, 1e-6)
+        want_x, want_r = fused_add_rms_norm_reference(x.cpu(), r.cpu(), wt.cpu(), 1e-6)
+        if not torch.equal(rc.cpu(), want_r):
+            raise AssertionError(f"sweep fused_add_rms_norm T={t_}: residual differs from the oracle before timing")
+        u_fused = ulps(xc, want_x)
+        torch.ops.decode_kernels.silu_and_mul(ys, xs)
+        u_silu = ulps(ys, silu_and_mul_reference(xs.cpu()))
+        if max(u_rms, u_fused, u_silu) > 1:
+            raise AssertionError(f"sweep norms T={t_}: {u_rms} / {u_fused} / {u_silu} ulp from the oracle before timing")
+        for op, fn, nbytes, u in (
+            ("rms_norm", lambda: torch.ops.decode_kernels.rms_norm(out, x, wt, 1e-6), 2 * t_ * h * elt, u_rms),
+            ("fused_add_rms_norm", lambda: torch.ops.decode_kernels.fused_add_rms_norm(xc, rc, wt, 1e-6),
+             4 * t_ * h * elt, u_fused),
+            ("silu_and_mul", lambda: torch.ops.decode_kernels.silu_and_mul(ys, xs), 3 * t_ * dmlp * elt, u_silu),
+        ):
+            tm = time_cold(fn, iters=30)
+            emit({"op": op, "config": f"T={t_} " + (f"d={dmlp}" if op == "silu_and_mul" else f"H={h}"),
+                  "us": tm["median_us"], "p10_us": tm["p10_us"], "p90_us": tm["p90_us"], **rate(nbytes, tm["median_us"]),
+                  "checked_max_ulp": u})
+        progress(f"sweep norms T={t_} done")
+    if sink:
+        sink.close()
+    return 0
+
+
 def pmc_workload_layer_graph(steps: int = 20) -> None:
     """What the graph-against-eager kernel trace records: the Llama-3-8B batch-64
     decode-layer step, fused and unfused, `steps` eager steps and then `steps`
@@ -905,6 +1035,11 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-extras", action="store_true", help="skip the secondary configs")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline (and its correctness check)")
+    ap.add_argument("--sweep", action="store_true",
+                    help="run DecodeKernels' benchmark grid instead (one JSON line per row; not the bench line)")
+    ap.add_argument("--sweep-dtype", choices=["bf16", "fp16"], default="bf16")
+    ap.add_argument("--sweep-quick", action="store_true", help="the reference's --quick grid")
+    ap.add_argument("--sweep-out", default=None, help="also write the sweep's JSON lines to this file")
     ap.add_argument("--pmc-workload", nargs="?", const="attention",
                     choices=["attention", "attention_cold", "attention_fp8", "gemm", "gemm_skinny", "norm",
                              "layer_graph"],
@@ -916,6 +1051,8 @@ def main() -> int:
         return 2
     if not dk.is_available():
         raise RuntimeError("decodekernels_amd HIP extension not available (build it with __graft_entry__.build())")
+    if args.sweep:
+        return sweep(torch.bfloat16 if args.sweep_dtype == "bf16" else torch.float16, args.sweep_quick, args.sweep_out)
     if args.pmc_workload == "attention_cold":
         pmc_workload_attention_cold()
         return 0
