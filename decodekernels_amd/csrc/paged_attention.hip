@@ -133,6 +133,7 @@ struct KParams {
   int num_q_heads, group, block_size, max_partitions;
   int num_seqs, num_kv_heads;
   int num_units;  // split-K grid: unit positions per sequence, ceil(max_partitions / 2)
+  int unit512;    // split-K grid: one 512-token unit per workspace row instead (small grids)
   int pair_ratio;  // balanced kernel: share of workgroups [0, grid/2) over the others', x100
   float scale_log2;  // softmax scale x log2(e) (x k_scale for an fp8 cache)
   float v_scale;     // multiplies the output (fp8 cache's v_scale; 1 otherwise)
@@ -756,12 +757,16 @@ void paged_attention_kernel(const KParams p) {
   int unit_tokens = kPart;
   int seq_len = p.seq_lens[seq];
   if constexpr (SPLIT) {
-    const int full_planes = p.num_units - 1;  // positions 1 .. num_units - 1, 1024 tokens each
-    if (plane < full_planes) {
-      start = (full_planes - plane) * kUnit;
-      unit_tokens = kUnit;
+    if (p.unit512) {
+      start = (p.max_partitions - 1 - plane) * kPart;  // planes walk the 512-token positions from the last down
     } else {
-      start = plane == full_planes ? kPart : 0;
+      const int full_planes = p.num_units - 1;  // positions 1 .. num_units - 1, 1024 tokens each
+      if (plane < full_planes) {
+        start = (full_planes - plane) * kUnit;
+        unit_tokens = kUnit;
+      } else {
+        start = plane == full_planes ? kPart : 0;
+      }
     }
     seq_len = min(seq_len, p.max_partitions * kPart);  // tokens past the workspace are ignored
   }
@@ -776,7 +781,11 @@ void paged_attention_kernel(const KParams p) {
     return;
   }
   UnitEngine<E, D, SPLIT, BS16, ALIGN, NW, KV8> eng(p, sm);
-  const Unit u = make_unit(kv_head, seq, start, unit_tokens, seq_len, start / kPart);
+  Unit u = make_unit(kv_head, seq, start, unit_tokens, seq_len, start / kPart);
+  // 512-token units: rows 0 .. n-1 hold the sequence's partitions and the
+  // last one marks row n empty (if n < max_partitions) -- the layout the
+  // balanced schedule's reduce reads. (two_slots: "mark the next row empty".)
+  if (SPLIT && p.unit512) u.two_slots = start + kPart >= seq_len;
   const int bt = eng.load_bt(u);
   eng.load_q(u);
   eng.prologue(u, bt);
@@ -1271,14 +1280,17 @@ hipError_t launch_aligned(const KParams& kp, unsigned grid, int align, hipStream
   }
 }
 
-// DK_ATTN_SCHEDULE=grid|balanced forces the split-K schedule (tests and
-// tuning compare the two on one input); unset or anything else: automatic.
-enum class Schedule { kAuto, kGrid, kBalanced };
+// DK_ATTN_SCHEDULE=grid|balanced|partitions forces the split-K schedule
+// (tests and tuning compare them on one input): the grid of 1024-token units,
+// the balanced schedule, or the grid of 512-token units (one per workspace
+// row); unset or anything else: automatic.
+enum class Schedule { kAuto, kGrid, kBalanced, kPartitions };
 inline Schedule forced_schedule() {
   const char* v = std::getenv("DK_ATTN_SCHEDULE");
   if (v == nullptr) return Schedule::kAuto;
   if (std::strcmp(v, "grid") == 0) return Schedule::kGrid;
   if (std::strcmp(v, "balanced") == 0) return Schedule::kBalanced;
+  if (std::strcmp(v, "partitions") == 0) return Schedule::kPartitions;
   return Schedule::kAuto;
 }
 
@@ -1308,26 +1320,42 @@ hipError_t launch_split(KParams kp, int num_kv_heads, int num_seqs, int align, h
   // the grid would be more than one round of resident workgroups.
   const Schedule forced = forced_schedule();
   const int64_t tile_bound = per_plane * kp.max_partitions * (kPart / kTile);
+  // One 512-token unit per workspace row (the reference's partitioning).
+  const int64_t partition_units = per_plane * kp.max_partitions;
   int resident = 0;
   int per_cu = 0;
-  if (num_seqs <= kMaxBalancedSeqs && tile_bound < (int64_t{1} << 30) && forced != Schedule::kGrid) {
+  if (forced != Schedule::kGrid && forced != Schedule::kPartitions &&
+      ((num_seqs <= kMaxBalancedSeqs && tile_bound < (int64_t{1} << 30)) || forced == Schedule::kAuto)) {
     const hipError_t e = launch_aligned<E, D, true, BS16, true, KV8>(kp, 0, align, stream, &resident, &per_cu);
     if (e != hipSuccess) return e;
   }
+  const bool balanced_ok = num_seqs <= kMaxBalancedSeqs && tile_bound < (int64_t{1} << 30);
   // Two workgroups per CU sharing its SIMDs (4 waves each): the one
   // dispatched first (blockIdx < grid / 2; the second round of dispatch fills
   // each CU's second slot) streams faster, so the first half of the grid
   // takes the larger shares. (2-wave workgroups at 1 wave/SIMD do not share.)
   kp.pair_ratio = per_cu == 2 && waves_per_group<D>() == 4 ? DK_ATTN_PAIR_RATIO : 100;
+  // Automatic choice: a grid of 512-token units when it fits in one round of
+  // resident workgroups (a small call: twice the workgroups of 1024-token
+  // units, each with half the tokens, so the call's critical path halves);
+  // else the balanced schedule when the 1024-token grid would exceed a round;
+  // else that grid.
+  const bool partitions = forced == Schedule::kPartitions ||
+                          (forced == Schedule::kAuto && resident > 0 && partition_units <= resident);
+  const bool balanced = !partitions && balanced_ok && resident > 0 &&
+                        (forced == Schedule::kBalanced || (forced == Schedule::kAuto && grid_units > resident));
   hipError_t e;
-  const bool balanced = resident > 0 && (forced == Schedule::kBalanced || grid_units > resident);
-  if (balanced) {
+  if (partitions) {
+    if (partition_units >= (int64_t{1} << 31)) return hipErrorInvalidValue;  // bounded by the host's checks
+    kp.unit512 = 1;
+    e = launch_aligned<E, D, true, BS16, false, KV8>(kp, static_cast<unsigned>(partition_units), align, stream);
+  } else if (balanced) {
     e = launch_aligned<E, D, true, BS16, true, KV8>(kp, static_cast<unsigned>(resident), align, stream);
   } else {
     e = launch_aligned<E, D, true, BS16, false, KV8>(kp, static_cast<unsigned>(grid_units), align, stream);
   }
   if (e != hipSuccess) return e;
-  if (balanced) launch_reduce_sized<E, D, true>(kp, num_seqs, stream);
+  if (balanced || partitions) launch_reduce_sized<E, D, true>(kp, num_seqs, stream);
   else launch_reduce_sized<E, D, false>(kp, num_seqs, stream);
   return hipGetLastError();
 }
@@ -1451,7 +1479,8 @@ int paged_attention_entry(const dk_paged_attn_params* a, int dtype, int head_dim
   kp.num_units = split ? static_cast<int>(ceil_div64(a->max_partitions, 2)) : 1;
   kp.scale_log2 = a->scale * k_scale * kLog2e;
   kp.v_scale = v_scale;
-  if (static_cast<int64_t>(a->num_seqs) * a->num_kv_heads * (kp.num_units + 1) >= (int64_t{1} << 31))
+  if (static_cast<int64_t>(a->num_seqs) * a->num_kv_heads * (std::max(kp.num_units, kp.max_partitions) + 1) >=
+      (int64_t{1} << 31))
     return fail("paged_attention_decode: num_seqs x num_kv_heads x partitions is too large");
   kp.num_seqs = a->num_seqs;
   kp.num_kv_heads = a->num_kv_heads;

@@ -56,7 +56,7 @@ def test_fp8_single_pass_and_split(dtype, head_dim, group, layout):
 
 @pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("head_dim,group", [(192, 4), (192, 8), (128, 16), (64, 16), (256, 16)])
-@pytest.mark.parametrize("schedule", ["grid", "balanced"])
+@pytest.mark.parametrize("schedule", ["grid", "balanced", "partitions"])
 def test_fp8_head_dim_192_and_group_16(dtype, head_dim, group, schedule, monkeypatch):
     """Past the reference's limits with an fp8 cache: head_dim 192 (the D=256
     class) and GQA groups of 16 (the LDS merge in two passes of 8 heads),
@@ -73,7 +73,7 @@ def test_fp8_head_dim_192_and_group_16(dtype, head_dim, group, schedule, monkeyp
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
-@pytest.mark.parametrize("schedule", ["grid", "balanced"])
+@pytest.mark.parametrize("schedule", ["grid", "balanced", "partitions"])
 def test_fp8_long_contexts_both_schedules(dtype, schedule, monkeypatch):
     monkeypatch.setenv("DK_ATTN_SCHEDULE", schedule)
     lens = [16384, 3000, 7777, 1, 600, 9000, 12000, 5]
@@ -81,7 +81,7 @@ def test_fp8_long_contexts_both_schedules(dtype, schedule, monkeypatch):
     _check(_q(len(lens), 32, 128, dtype, seed=3), kv, 0.031, 0.25, dtype)
 
 
-@pytest.mark.parametrize("schedule", ["grid", "balanced"])
+@pytest.mark.parametrize("schedule", ["grid", "balanced", "partitions"])
 def test_fp8_128k_batch_1(schedule, monkeypatch):
     """The long-context split-K shape with an fp8 cache: one 131072-token
     sequence, 32 query / 8 KV heads, head_dim 128, HND cache, 1% of rows
@@ -113,7 +113,7 @@ def test_fp8_128k_batch_1(schedule, monkeypatch):
 
 @pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("hq,hkv,head_dim", [(28, 4, 128), (14, 2, 64), (6, 2, 128), (10, 2, 64), (12, 2, 256)])
-@pytest.mark.parametrize("schedule", ["grid", "balanced"])
+@pytest.mark.parametrize("schedule", ["grid", "balanced", "partitions"])
 def test_fp8_odd_gqa_groups(dtype, hq, hkv, head_dim, schedule, monkeypatch):
     """GQA groups 3, 5, 6 and 7 (Qwen2.5-7B: 28 / 4, Qwen2.5-0.5B: 14 / 2) over an
     fp8 cache, single pass and split-K."""

@@ -22,7 +22,8 @@ the physical cache blocks (and the block table with them) leaves the output
 unchanged bit for bit, and doubling V (exact in bf16 / fp16) doubles it bit
 for bit wherever the output is a normal number (subnormal outputs round on a
 fixed grid, so round(2x) and 2 round(x) may differ there by one spacing).
-Both split-K schedules run on every configuration.
+All three split-K schedules (1024-token grid units, balanced shares, 512-token
+partitions) run on every configuration.
 """
 
 import math
@@ -133,7 +134,7 @@ def case(request):
     torch.cuda.empty_cache()
 
 
-@pytest.mark.parametrize("schedule", ["grid", "balanced"])
+@pytest.mark.parametrize("schedule", ["grid", "balanced", "partitions"])
 def test_full_size_against_oracle(case, schedule, monkeypatch):
     name, c, kv, q, ref = case
     monkeypatch.setenv("DK_ATTN_SCHEDULE", schedule)

@@ -73,7 +73,7 @@ def test_paged_attention_split_k(dtype, head_dim, group):
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
-@pytest.mark.parametrize("schedule", ["auto", "grid", "balanced"])
+@pytest.mark.parametrize("schedule", ["auto", "grid", "balanced", "partitions"])
 def test_paged_attention_c1_shape(dtype, schedule, monkeypatch):
     """BASELINE configs[0] on the HIP path: 4 sequences of {1, 511, 512, 513}
     tokens, 8 query / 2 KV heads, head_dim 128, block 16, NHD cache of 160
@@ -103,13 +103,14 @@ def _workspace_rows(exp_sums: torch.Tensor) -> torch.Tensor:
 
 
 @pytest.mark.parametrize("seq_len,min_rows", [(140000, 64), (270000, 128)])
-@pytest.mark.parametrize("schedule", ["grid", "balanced"])
+@pytest.mark.parametrize("schedule", ["grid", "balanced", "partitions"])
 def test_paged_attention_reduce_many_rows(seq_len, min_rows, schedule, monkeypatch):
     """One KV head of one long sequence: under the balanced schedule the stream
     is cut into one piece per workgroup share, so the reduce merges more than
     64 (140K tokens) and more than 128 (270K tokens) workspace rows per query
     head -- its second and third lane-parallel passes over the exp-sums. The
-    grid schedule merges ceil(L / 1024) + 1 rows. Both against the oracle."""
+    grid schedule merges ceil(L / 1024) + 1 rows, the grid of 512-token units
+    ceil(L / 512). All against the oracle."""
     monkeypatch.setenv("DK_ATTN_SCHEDULE", schedule)
     dtype = torch.bfloat16
     kv = make_paged_kv([seq_len], 1, 128, 16, dtype, "cuda", layout="nhd", seed=seq_len % 1000)
@@ -127,6 +128,8 @@ def test_paged_attention_reduce_many_rows(seq_len, min_rows, schedule, monkeypat
         assert (rows == rows[0, 0]).all(), "every query head of a stream uses the same rows"
         assert int(rows[0, 0]) > min_rows, f"the stream spans {int(rows[0, 0])} rows, expected > {min_rows}"
         assert int(rows[0, 0]) <= ws[2].shape[-1]
+    if schedule == "partitions":  # one row per 512-token partition, as the reference's workspace
+        assert (_workspace_rows(ws[2]) == -(-seq_len // 512)).all()
 
 
 # Qwen2.5-7B (28 query / 4 KV heads, group 7, head_dim 128), Qwen2.5-0.5B
@@ -136,7 +139,7 @@ ODD_GROUP_CASES = [(28, 4, 128), (14, 2, 64), (6, 2, 128), (10, 2, 64), (12, 2, 
 
 @pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("hq,hkv,head_dim", ODD_GROUP_CASES, ids=lambda v: str(v))
-@pytest.mark.parametrize("schedule", ["grid", "balanced"])
+@pytest.mark.parametrize("schedule", ["grid", "balanced", "partitions"])
 def test_paged_attention_odd_gqa_groups(dtype, hq, hkv, head_dim, schedule, monkeypatch):
     """GQA groups that are not powers of two (the reference's benchmark models,
     benchmarks/bench_kernels.py:38-42), single pass and split-K."""
@@ -189,7 +192,7 @@ def test_paged_attention_strided_layouts(layout, seq_lens):
     _check_attention(_q(len(seq_lens), 8, 128, torch.float16), kv, torch.float16)
 
 
-@pytest.mark.parametrize("schedule", ["grid", "balanced"])
+@pytest.mark.parametrize("schedule", ["grid", "balanced", "partitions"])
 def test_paged_attention_token_stride_beyond_tile_offsets(schedule, monkeypatch):
     """A token stride of 2^26 elements (a [block_size, blocks, heads, D] cache
     viewed as [blocks, block_size, heads, D], 2 GiB per K/V): 16 rows of a tile
@@ -312,7 +315,7 @@ def test_paged_attention_head_dims_96_192(dtype, head_dim, group, layout):
 
 
 @pytest.mark.parametrize("head_dim", [96, 192])
-@pytest.mark.parametrize("schedule", ["grid", "balanced"])
+@pytest.mark.parametrize("schedule", ["grid", "balanced", "partitions"])
 def test_paged_attention_head_dims_96_192_long(head_dim, schedule, monkeypatch):
     monkeypatch.setenv("DK_ATTN_SCHEDULE", schedule)
     lens = _log_uniform_lens(24, 12000, seed=head_dim)
@@ -333,7 +336,7 @@ def test_paged_attention_head_dim_192_fp8_cache():
                                   kv96.seq_lens)
 
 
-@pytest.mark.parametrize("schedule", ["grid", "balanced"])
+@pytest.mark.parametrize("schedule", ["grid", "balanced", "partitions"])
 def test_paged_attention_group_16_fp8_cache(schedule, monkeypatch):
     monkeypatch.setenv("DK_ATTN_SCHEDULE", schedule)
     lens = [9000, 40, 3000, 1]
@@ -364,16 +367,17 @@ SCHEDULE_CASES = [
 
 @pytest.mark.parametrize("case", SCHEDULE_CASES, ids=lambda c: f"d{c[0]}_hkv{c[1]}_g{c[2]}_bs{c[3]}_{c[4]}")
 def test_paged_attention_split_k_schedules(case, monkeypatch):
-    """Split-K under both schedules -- one workgroup per unit slot, and resident
-    workgroups with equal tile shares of all sequences -- against the oracle.
-    The two cut the sequences differently (so they may differ in the last
-    bits); each is deterministic from call to call."""
+    """Split-K under the three schedules -- one workgroup per 1024-token unit,
+    resident workgroups with equal tile shares of all sequences, one workgroup
+    per 512-token partition -- against the oracle. They cut the sequences
+    differently (so they may differ in the last bits); each is deterministic
+    from call to call."""
     d, hkv, group, bs, layout, n, max_len, dtype = case
     lens = _log_uniform_lens(n, max_len, seed=d + bs)
     kv = make_paged_kv(lens, hkv, d, bs, dtype, "cuda", layout=layout, seed=d + 1)
     q = _q(n, hkv * group, d, dtype)
     ref = attention_f32(q, kv.k_cache, kv.v_cache, kv.block_tables, kv.seq_lens)
-    for schedule in ("grid", "balanced"):
+    for schedule in ("grid", "balanced", "partitions"):
         monkeypatch.setenv("DK_ATTN_SCHEDULE", schedule)
         run = lambda: dk.paged_attention_decode(  # noqa: E731
             q, kv.k_cache, kv.v_cache, kv.block_tables, kv.seq_lens, max_seq_len=max_len
@@ -430,7 +434,7 @@ def test_paged_attention_balanced_schedule_edge_shapes(case, monkeypatch):
         assert (out[torch.tensor(lens) == 0] == 0).all()
 
 
-@pytest.mark.parametrize("schedule", ["auto", "grid", "balanced"])
+@pytest.mark.parametrize("schedule", ["auto", "grid", "balanced", "partitions"])
 def test_paged_attention_graph_replay(schedule, monkeypatch):
     """Preallocated buffers make the op capturable; replays track new cache
     contents and lengths (within the captured max_seq_len)."""

@@ -50,7 +50,7 @@ def _both(kv, q, dtype, max_len):
     return want, got
 
 
-@pytest.mark.parametrize("schedule", ["auto", "grid", "balanced"])
+@pytest.mark.parametrize("schedule", ["auto", "grid", "balanced", "partitions"])
 def test_noalloc_matches_workspace_entry_point(schedule, monkeypatch):
     if schedule != "auto":
         monkeypatch.setenv("DK_ATTN_SCHEDULE", schedule)
