@@ -223,8 +223,10 @@ def declared_functions() -> list[str]:
 
 
 def gemm_plan(M: int, N: int, K: int, with_workspace: bool = True) -> tuple[int, int, int, int]:
-    """(waves along N, waves along K, K splits, columns per split) of gemm_tn's
-    skinny kernel for this shape (all 0 for M > 64); host arithmetic only."""
+    """gemm_tn's launch plan for this shape; host arithmetic only. Skinny
+    kernel (M <= 64): (waves along N, waves along K, K splits, columns per
+    split); LDS-DMA kernel (M > 64, and the 64-row tiles of some M <= 64
+    plans): (tile rows, tile columns, K splits, columns per split)."""
     out = (ctypes.c_int * 4)()
     rc = lib().dk_gemm_tn_plan(M, N, K, int(with_workspace), out)
     if rc != 0:

@@ -24,7 +24,9 @@
 //   through a multi-stage ring; six tile shapes from 256x256 down to 64x64,
 //   picked per call by a throughput model so that batches of a few hundred
 //   rows still fill all 256 CUs. The output tile leaves through the freed
-//   ring, read back row by row for 16-byte stores.
+//   ring, read back row by row for 16-byte stores. At M <= 64 its 64-row
+//   tiles (64 or 128 columns, K split) replace the skinny kernel from M = 32
+//   where they fill the CUs, and for N > 32768 (decode_dma_plan).
 #include <algorithm>
 
 #include "../../include/decodekernels_amd.h"
@@ -842,20 +844,103 @@ inline int64_t dma_workspace_bytes(const DmaPlan& d, int M, int N) {
   return d.splits > 1 ? static_cast<int64_t>(d.splits) * M * N * static_cast<int64_t>(sizeof(float)) : 0;
 }
 
+// The LDS-DMA kernel at decode sizes (M <= 64), on one 64-row tile: column
+// tiles of bn = 64 (4 waves, two workgroups per CU) or 128 (4 waves, one per
+// CU), K split over workgroup rows. Where it applies it replaces the skinny
+// plan; bn = 0 keeps the skinny kernel. Fitted to interleaved cold timings
+// of both kernels at M = 1 ... 64 on the Llama-3-8B, Qwen2.5-7B and
+// Qwen2.5-0.5B projections (every candidate below, bf16, with the split
+// reduce):
+//  * candidates: bn in {128, 64} x 1, 2, 4, 8 splits of >= 768 columns, at
+//    most 256 workgroups; the pick streams the fewest weight bytes per
+//    workgroup (bn x k_split), bn = 128 on a tie;
+//  * it replaces the skinny plan when M >= 32 and the pick fills at least half
+//    of the CUs: the skinny kernel's per-step activation work grows with M
+//    while the tile's stays flat. Llama-3-8B at M = 64: qkv 20.9 -> 18.7 us
+//    (128 x 4 splits), o 17.1 -> 14.9 (64 x 4), down 32.7 -> 30.1 (128 x 8);
+//    qkv at M = 32 18.7 -> 17.2 (hipBLASLt 18.0). Below M = 32 the skinny
+//    plans are 5-10% faster on the 8B shapes, and with fewer than 128
+//    workgroups (the 0.5B model's small matrices) at every M. An unsplit
+//    pick replaces only a skinny grid that leaves over a quarter of the CUs
+//    idle (0.5B gate_up, 152 workgroups: 12.8 -> 10.4 us at M = 64), not a
+//    full one (8B gate_up: 64 x 128 unsplit 56.4 against 51.8 us);
+//  * for N > 32768, where no skinny grid fits one workgroup per CU, 64 x 64
+//    unsplit at every M: Qwen2.5-7B gate_up (N 37888) 57.7 -> 56.0 us at
+//    M = 1, 80.3 -> 65.6 at M = 64. At N <= 32768 the skinny kernel's full
+//    one-per-CU grid stays (Llama-3-8B gate_up: 43.9 against 47.6 us).
+struct DecodeDmaPlan {
+  int bn, splits, k_split;
+};
+
+inline DecodeDmaPlan decode_dma_plan(int M, int N, int K, bool split_ok) {
+  DecodeDmaPlan none{0, 1, K};
+  if (M > 64 || K <= 0) return none;
+  if (skinny_plan_unsplit(M, N, K).wn == 0) return DecodeDmaPlan{64, 1, K};
+  if (M < 32) return none;
+  DecodeDmaPlan best = none;
+  int64_t best_bytes = -1, best_wgs = 0;
+  for (const int bn : {128, 64}) {
+    const int64_t tiles = ceil_div64(N, bn);
+    for (int s = 1; s <= 8; s *= 2) {
+      int ks = K, sp = 1;
+      if (s > 1) {
+        if (!split_ok) break;
+        const int per = (K + s - 1) / s;
+        ks = (per + kDmaBK - 1) / kDmaBK * kDmaBK;
+        sp = (K + ks - 1) / ks;
+        if (ks < 768) break;
+        if (sp < 2) continue;
+      }
+      if (tiles * sp > kSkinnyCus) break;
+      const int64_t bytes = static_cast<int64_t>(bn) * ks;
+      if (best_bytes < 0 || bytes < best_bytes) {
+        best = DecodeDmaPlan{bn, sp, ks};
+        best_bytes = bytes;
+        best_wgs = tiles * sp;
+      }
+    }
+  }
+  if (2 * best_wgs < kSkinnyCus) return none;
+  if (best.splits == 1) {
+    // Unsplit, a tile streams about the bytes per workgroup of the skinny
+    // kernel's full grid, which its 14-wave workgroups stream faster.
+    const SkinnyPlan u = skinny_plan_unsplit(M, N, K);
+    if (4 * ceil_div64(N, 16 * u.wn) >= 3 * kSkinnyCus) return none;
+  }
+  return best;
+}
+
+inline int64_t decode_dma_workspace_bytes(const DecodeDmaPlan& d, int M, int N) {
+  return d.bn > 0 && d.splits > 1 ? static_cast<int64_t>(d.splits) * M * N * static_cast<int64_t>(sizeof(float)) : 0;
+}
 
 // Launches C = A B^T (+ bias) with the plan for (M, N, K) and the workspace
 // given. With deferred_splits != nullptr, a plan that splits K stops after the
 // main kernel, leaving splits x M x N fp32 partial tiles (no bias) in the
 // workspace for the caller to sum in split order, and reports the split count
-// there (1: C was written directly).
+// there (1: C was written directly). dma_ok: the row strides allow the LDS-DMA
+// kernel's 32-bit offsets (M <= 64 then keeps to the skinny kernel without).
 template <typename E>
 hipError_t launch(const uint16_t* A, const uint16_t* B, const uint16_t* bias, uint16_t* C, int M, int N, int K,
                   int lda, int ldb, int ldc, void* workspace, int64_t workspace_bytes, hipStream_t s,
-                  int* deferred_splits = nullptr) {
+                  int* deferred_splits, bool dma_ok) {
   if (M <= 64) {
+    constexpr DecodeDmaPlan kNone{0, 1, 0};
+    DecodeDmaPlan d = dma_ok ? decode_dma_plan(M, N, K, true) : kNone;
     SkinnyPlan p = skinny_plan(M, N, K, true);
-    if (p.splits > 1 && (workspace == nullptr || skinny_workspace_bytes(p, M, N) > workspace_bytes))
+    // A workspace smaller than the plan's needs runs exactly the plan
+    // without one (both kernels' choices then exclude splits).
+    const int64_t need = d.bn > 0 ? decode_dma_workspace_bytes(d, M, N) : skinny_workspace_bytes(p, M, N);
+    if (need > 0 && (workspace == nullptr || need > workspace_bytes)) {
+      d = dma_ok ? decode_dma_plan(M, N, K, false) : kNone;
       p = skinny_plan(M, N, K, false);
+    }
+    if (d.bn > 0) {
+      if (deferred_splits != nullptr) *deferred_splits = d.splits;
+      const DmaLauncher fn = d.bn == 64 ? launch_dma<E, 64, 64, 2, 2, 4> : launch_dma<E, 64, 128, 2, 2, 4>;
+      return fn(A, B, bias, C, M, N, K, lda, ldb, ldc, s, d.splits > 1 ? static_cast<float*>(workspace) : nullptr,
+                d.splits, d.k_split, deferred_splits == nullptr);
+    }
     float* part = p.splits > 1 ? static_cast<float*>(workspace) : nullptr;
     if (deferred_splits != nullptr) *deferred_splits = p.splits;
     const dim3 g2(static_cast<unsigned>(ceil_div64(N, 16 * p.wn)), static_cast<unsigned>(p.splits));
@@ -912,8 +997,8 @@ int gemm_tn_checked(int dtype, const void* A, const void* B, const void* bias, v
   if (workspace != nullptr && !aligned_to(workspace, 16)) return fail("gemm_tn: workspace must be 16-byte aligned");
   if (workspace_bytes < 0) return fail("gemm_tn: workspace_bytes must be non-negative");
   if (M > 64 && ceil_div64(M, 64) * ceil_div64(N, 64) >= (int64_t{1} << 31)) return fail("gemm_tn: M x N is too large");
-  if (M > 64 && int64_t{256} * std::max(lda, ldb) * 2 >= (int64_t{1} << 31))
-    return fail("gemm_tn: row strides too large for 32-bit buffer offsets");
+  const bool dma_ok = int64_t{256} * std::max(lda, ldb) * 2 < (int64_t{1} << 31);
+  if (M > 64 && !dma_ok) return fail("gemm_tn: row strides too large for 32-bit buffer offsets");
   if (M <= 64 && (static_cast<int64_t>(M) * lda * 2 >= (int64_t{1} << 31) || int64_t{16} * ldb * 2 >= (int64_t{1} << 31)))
     return fail("gemm_tn: row strides too large for 32-bit buffer offsets");
   hipStream_t s = static_cast<hipStream_t>(stream);
@@ -923,8 +1008,10 @@ int gemm_tn_checked(int dtype, const void* A, const void* B, const void* bias, v
   auto* c = static_cast<uint16_t*>(C);
   const hipError_t e =
       dtype == DK_BFLOAT16
-          ? gemm::launch<Bf16>(a, b, bi, c, M, N, K, lda, ldb, ldc, workspace, workspace_bytes, s, deferred_splits)
-          : gemm::launch<F16>(a, b, bi, c, M, N, K, lda, ldb, ldc, workspace, workspace_bytes, s, deferred_splits);
+          ? gemm::launch<Bf16>(a, b, bi, c, M, N, K, lda, ldb, ldc, workspace, workspace_bytes, s, deferred_splits,
+                               dma_ok)
+          : gemm::launch<F16>(a, b, bi, c, M, N, K, lda, ldb, ldc, workspace, workspace_bytes, s, deferred_splits,
+                              dma_ok);
   return static_cast<int>(e);
 }
 
@@ -938,6 +1025,8 @@ extern "C" int dk_gemm_tn(int dtype, const void* A, const void* B, const void* b
 extern "C" int64_t dk_gemm_tn_workspace_bytes(int M, int N, int K) {
   if (M <= 0 || N <= 0 || K <= 0) return 0;
   if (M > 64) return dk::gemm::dma_workspace_bytes(dk::gemm::dma_plan(M, N, K, true), M, N);
+  const dk::gemm::DecodeDmaPlan d = dk::gemm::decode_dma_plan(M, N, K, true);
+  if (d.bn > 0) return dk::gemm::decode_dma_workspace_bytes(d, M, N);
   const dk::gemm::SkinnyPlan p = dk::gemm::skinny_plan(M, N, K, true);
   return dk::gemm::skinny_workspace_bytes(p, M, N);
 }
@@ -950,6 +1039,14 @@ extern "C" int dk_gemm_tn_plan(int M, int N, int K, int with_workspace, int* pla
     const dk::gemm::DmaPlan d = dk::gemm::dma_plan(M, N, K, with_workspace != 0);
     plan[0] = dk::gemm::kDmaShapes[d.shape].bm;
     plan[1] = dk::gemm::kDmaShapes[d.shape].bn;
+    plan[2] = d.splits;
+    plan[3] = d.k_split;
+    return hipSuccess;
+  }
+  const dk::gemm::DecodeDmaPlan d = dk::gemm::decode_dma_plan(M, N, K, with_workspace != 0);
+  if (d.bn > 0) {
+    plan[0] = 64;
+    plan[1] = d.bn;
     plan[2] = d.splits;
     plan[3] = d.k_split;
     return hipSuccess;

@@ -140,10 +140,11 @@ int64_t dk_gemm_tn_workspace_bytes(int M, int N, int K);
 
 /*
  * Launch plan of dk_gemm_tn_ws (with_workspace != 0, workspace large enough)
- * or dk_gemm_tn. For M <= 64 (skinny kernel) plan[0..3] = waves along N per
+ * or dk_gemm_tn. Skinny kernel (M <= 64): plan[0..3] = waves along N per
  * workgroup (16 columns each), waves along K, K splits, columns per split;
- * for M > 64 (tiled kernel) = tile rows, tile columns, K splits, columns per
- * split. For tests and tuning; launches nothing.
+ * tiled kernel (M > 64, and M <= 64 where 64-row tiles fill the CUs better:
+ * plan[0] = 64) = tile rows, tile columns, K splits, columns per split. For
+ * tests and tuning; launches nothing.
  * No counterpart in DecodeKernels.
  */
 int dk_gemm_tn_plan(int M, int N, int K, int with_workspace, int* plan);

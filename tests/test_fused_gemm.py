@@ -10,8 +10,9 @@
 
 The unfused ops are each checked against the oracle by their own tests, so
 bit equality pins the fused ones to the oracle too. The shapes cover the
-plans that split K (skinny M <= 64 with 2, 4 and 8 splits, the LDS-DMA
-kernel's split plans at M = 128 / 384 and, for qkv, 256), where the consumer sums the partial
+plans that split K (skinny M <= 64 with 2 splits, the LDS-DMA kernel's
+64-row tiles at M = 32 ... 64 with 4 and 8 splits, its split plans at M = 128 /
+384 and, for qkv, 256), where the consumer sums the partial
 tiles itself -- asserted from the plan -- and plans that do not, where the
 fused call runs the two ops; plus rows the norm cannot vectorise (N not a
 multiple of 8: the two ops run), strided rows, bias, and both dtypes.
@@ -38,10 +39,10 @@ def _splits(M, N, K):
 @pytest.mark.parametrize(
     "M,N,K,split",
     [
-        (64, 4096, 4096, True),    # o projection at batch 64: 4 splits
+        (64, 4096, 4096, True),    # o projection at batch 64: 4 splits (64 x 64 tiles)
         (48, 4096, 4096, True),
-        (64, 4096, 14336, True),   # down projection at batch 64: 8 splits
-        (32, 4096, 14336, True),   # 4 splits
+        (64, 4096, 14336, True),   # down projection at batch 64: 8 splits (64 x 128 tiles)
+        (32, 4096, 14336, True),   # 8 splits
         (16, 4096, 14336, True),   # 2 splits
         (8, 4096, 4096, False),
         (1, 4096, 14336, False),

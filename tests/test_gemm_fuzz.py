@@ -1,6 +1,7 @@
-"""Seeded random shapes through the tiled gemm_tn (M > 64): every tile shape
-and split plan the launcher picks, ragged M / N / K, odd and 4-aligned N,
-with and without a bias, fp16 and bf16, against an fp32 GEMM at the parity bar.
+"""Seeded random shapes through the tiled gemm_tn (M > 64, and M <= 64 where
+the decode plan picks the same kernel's 64-row tiles): every tile shape and
+split plan the launcher picks, ragged M / N / K, odd and 4-aligned N, with
+and without a bias, fp16 and bf16, against an fp32 GEMM at the parity bar.
 The torch op (workspace from the caching allocator, so split plans run) and
 the workspace-free C entry point must also agree bit for bit whenever both run
 the same unsplit plan."""
@@ -14,6 +15,7 @@ import torch
 import decodekernels_amd as dk
 from decodekernels_amd import capi
 from parity import assert_max_abs, gemm_f32_gpu
+from test_gemm_plan import replica_plan
 
 pytestmark = pytest.mark.gpu
 
@@ -26,6 +28,13 @@ def _shapes(count=48, seed=2024):
         N = rng.choice([rng.randint(1, 6000), 4 * rng.randint(1, 2200), 64 * rng.randint(1, 140)])
         K = 8 * rng.randint(1, 400)
         out.append((M, N, K, rng.random() < 0.5, rng.random() < 0.5))
+    # Decode sizes whose plan is the LDS-DMA kernel's 64-row tiles.
+    while len(out) < count + 24:
+        M = rng.randint(32, 64)
+        N = rng.choice([rng.randint(1000, 20000), 4 * rng.randint(250, 5000), rng.randint(32769, 40000)])
+        K = 8 * rng.randint(64, 1200)
+        if replica_plan(M, N, K)[0] == 64:  # host arithmetic, checked against the library on the CPU
+            out.append((M, N, K, rng.random() < 0.5, rng.random() < 0.5))
     return out
 
 

@@ -1,6 +1,5 @@
-"""CPU tests of gemm_tn's skinny launch plan (M <= 64), through
-``dk_gemm_tn_plan`` / ``dk_gemm_tn_workspace_bytes`` (host arithmetic, no
-kernel launch).
+"""CPU tests of gemm_tn's launch plans, through ``dk_gemm_tn_plan`` /
+``dk_gemm_tn_workspace_bytes`` (host arithmetic, no kernel launch).
 
 ``skinny_plan`` (decodekernels_amd/csrc/gemm.hip) picks the workgroup shape
 (waves along N, 16 columns each, x waves along K) and the number of K splits:
@@ -16,6 +15,15 @@ kernels rely on: every split non-empty and a multiple of 64 columns, at most
 256 workgroups whenever K is split, the workspace size, and a workgroup
 shape the launcher instantiates. The Llama-3-8B decode projections map to
 the shapes measured fastest.
+
+At M <= 64 ``decode_dma_plan`` can replace the skinny plan with the LDS-DMA
+kernel's 64-row tiles (reported as (64, tile columns, splits, k_split)): for
+N > 32768 (no skinny grid of one workgroup per CU) 64 x 64 unsplit; else
+from M = 32, among 64- and 128-column tiles with 1, 2, 4 or 8 K splits of
+>= 768 columns and <= 256 workgroups, the one streaming the fewest weight
+bytes per workgroup (128 columns on a tie), if it fills at least half the
+CUs and, unsplit, the skinny kernel's own unsplit grid leaves over a quarter
+of them idle. The M > 64 plan (``dma_plan``) is restated below it.
 """
 
 import random
@@ -35,16 +43,66 @@ def _wide(M, N, K):
     return (wn, 8 // wn, 1, K)
 
 
-def replica_plan(M, N, K, with_workspace=True, mistake=None):
-    """(wn, wk, splits, k_split) as skinny_plan computes it. ``mistake``
-    plants an error: "fill" drops the 3/4-fill condition of the unsplit grid,
-    "limit" compares activation bytes with the weight bytes instead of half
-    of them."""
-    u = None
+def _unsplit(N, K):
     for wn, wk in SHAPES:
         if -(-N // (16 * wn)) <= 256:
-            u = (wn, wk, 1, K)
-            break
+            return (wn, wk, 1, K)
+    return None
+
+
+def replica_decode_dma_plan(M, N, K, with_workspace=True, mistake=None):
+    """(64, tile columns, splits, k_split) as decode_dma_plan computes it, or
+    None (the skinny kernel). ``mistake``: "half" drops the half-fill
+    condition, "full" lets an unsplit tile replace a full skinny grid."""
+    if M > 64 or K <= 0:
+        return None
+    u = _unsplit(N, K)
+    if u is None:
+        return (64, 64, 1, K)
+    if M < 32:
+        return None
+    best, best_bytes, best_wgs = None, -1, 0
+    for bn in (128, 64):
+        tiles = -(-N // bn)
+        s = 1
+        while s <= 8:
+            ks, sp = K, 1
+            if s > 1:
+                if not with_workspace:
+                    break
+                ks = -(-(-(-K // s)) // 64) * 64
+                sp = -(-K // ks)
+                if ks < 768:
+                    break
+                if sp < 2:
+                    s *= 2
+                    continue
+            if tiles * sp > 256:
+                break
+            if best_bytes < 0 or bn * ks < best_bytes:
+                best, best_bytes, best_wgs = (64, bn, sp, ks), bn * ks, tiles * sp
+            s *= 2
+    if 2 * best_wgs < 256 and mistake != "half":
+        return None
+    if best is not None and best[2] == 1 and mistake != "full" and 4 * -(-N // (16 * u[0])) >= 3 * 256:
+        return None
+    return best
+
+
+def replica_plan(M, N, K, with_workspace=True, mistake=None):
+    """gemm_tn's plan at M <= 64: the decode DMA plan where it applies, else
+    (wn, wk, splits, k_split) as skinny_plan computes it. ``mistake`` plants
+    an error: "fill" drops the 3/4-fill condition of the unsplit grid,
+    "limit" compares activation bytes with the weight bytes instead of half
+    of them; "half" / "full" go to the decode DMA plan."""
+    d = replica_decode_dma_plan(M, N, K, with_workspace, mistake)
+    if d is not None:
+        return d
+    return replica_skinny_plan(M, N, K, with_workspace, mistake)
+
+
+def replica_skinny_plan(M, N, K, with_workspace=True, mistake=None):
+    u = _unsplit(N, K)
     if u is not None and M * K * 2 <= 256 * KIB and (mistake == "fill" or 4 * -(-N // (16 * u[0])) >= 3 * 256):
         return u
     cands = []
@@ -160,27 +218,34 @@ def test_plan_invariants_and_workspace_size():
     L = capi.lib()
     for M, N, K in _random_shapes(20000, 4):
         wn, wk, s, ks = capi.gemm_plan(M, N, K)
-        assert (wn, wk) in SHAPES, (M, N, K)
+        tile = wn == 64
+        assert (wn, wk) in SHAPES or (tile and wk in (64, 128)), (M, N, K)
         nbytes = L.dk_gemm_tn_workspace_bytes(M, N, K)
         if s == 1:
             assert ks == K and nbytes == 0
             continue
-        assert 2 <= s <= 8 and ks % 64 == 0 and ks >= 512, (M, N, K, s, ks)
+        assert 2 <= s <= 8 and ks % 64 == 0 and ks >= (768 if tile else 512), (M, N, K, s, ks)
         assert (s - 1) * ks < K <= s * ks, "a split is empty or K is not covered"
-        assert -(-N // (16 * wn)) * s <= 256, "a split plan over-fills the CUs"
+        assert -(-N // (wk if tile else 16 * wn)) * s <= 256, "a split plan over-fills the CUs"
         assert nbytes == s * M * N * 4
         # without a workspace the same shape is planned unsplit
         assert capi.gemm_plan(M, N, K, False)[2] == 1
 
 
-# (M, N, K) -> (waves along N, waves along K, splits): the measured-fastest
-# shapes of the Llama-3-8B decode projections.
+# (M, N, K) -> (waves along N, waves along K, splits) of the skinny kernel, or
+# (64, tile columns, splits) of the LDS-DMA kernel: the measured-fastest
+# plans of the Llama-3-8B, Qwen2.5-7B and Qwen2.5-0.5B decode projections.
 LLAMA_PICKS = {
-    (1, 6144, 4096): (2, 4, 1), (32, 6144, 4096): (2, 4, 1), (48, 6144, 4096): (6, 2, 4), (64, 6144, 4096): (6, 2, 4),
-    (1, 4096, 4096): (1, 8, 1), (32, 4096, 4096): (1, 8, 1), (48, 4096, 4096): (4, 2, 4), (64, 4096, 4096): (4, 2, 4),
-    (8, 4096, 14336): (1, 8, 1), (16, 4096, 14336): (2, 4, 2), (32, 4096, 14336): (4, 2, 4),
-    (48, 4096, 14336): (8, 1, 8), (64, 4096, 14336): (8, 1, 8),
-    (1, 28672, 4096): (7, 2, 1), (64, 28672, 4096): (7, 2, 1),
+    (1, 6144, 4096): (2, 4, 1), (16, 6144, 4096): (2, 4, 1), (32, 6144, 4096): (64, 128, 4),
+    (48, 6144, 4096): (64, 128, 4), (64, 6144, 4096): (64, 128, 4),
+    (1, 4096, 4096): (1, 8, 1), (16, 4096, 4096): (1, 8, 1), (32, 4096, 4096): (64, 64, 4),
+    (48, 4096, 4096): (64, 64, 4), (64, 4096, 4096): (64, 64, 4),
+    (8, 4096, 14336): (1, 8, 1), (16, 4096, 14336): (2, 4, 2), (32, 4096, 14336): (64, 128, 8),
+    (48, 4096, 14336): (64, 128, 8), (64, 4096, 14336): (64, 128, 8),
+    (1, 28672, 4096): (7, 2, 1), (32, 28672, 4096): (7, 2, 1), (64, 28672, 4096): (7, 2, 1),
+    (64, 4608, 3584): (64, 128, 4), (64, 3584, 3584): (64, 64, 4), (64, 3584, 18944): (64, 128, 8),
+    (1, 37888, 3584): (64, 64, 1), (64, 37888, 3584): (64, 64, 1),
+    (64, 1152, 896): (1, 8, 1), (1, 9728, 896): (4, 2, 1), (64, 9728, 896): (64, 64, 1),
 }
 
 
@@ -189,7 +254,7 @@ def test_llama_projections_get_the_measured_shapes(shape):
     assert capi.gemm_plan(*shape)[:3] == LLAMA_PICKS[shape]
 
 
-@pytest.mark.parametrize("mistake", ["fill", "limit"])
+@pytest.mark.parametrize("mistake", ["fill", "limit", "half", "full"])
 def test_planted_mistake_is_caught(mistake):
     """A replica with one condition changed must disagree with the library on
     some shape: the comparison above can see both conditions."""
@@ -206,16 +271,21 @@ def test_plan_validation():
         capi.gemm_plan(4, 8, -8)
 
 
-# One shape per (row tiles, workgroup shape, split or not) the plan reaches,
-# each with N not a multiple of the workgroup's columns; run on the GPU
-# against the oracle by tests/test_gemm_splitk.py.
+# One shape per (row tiles, workgroup shape, split or not) the skinny plan
+# reaches, and per (tile columns, split or not) of the decode DMA plan (plus
+# its N > 32768 case at M < 32), each with N not a multiple of the
+# workgroup's columns; run on the GPU against the oracle by
+# tests/test_gemm_splitk.py.
 COVERAGE_SHAPES = [
     (1, 8, 520), (1, 8, 1032), (1, 4101, 520), (1, 2050, 1032), (1, 8200, 520), (1, 4101, 1032),
     (1, 20000, 520), (1, 8200, 1032), (1, 28600, 520), (1, 8200, 2056), (1, 28680, 520), (16, 6150, 8200),
     (17, 8, 520), (17, 8, 1032), (17, 4101, 520), (17, 2050, 1032), (17, 8200, 520), (17, 4101, 1032),
-    (17, 20000, 520), (17, 8200, 1032), (17, 28600, 520), (17, 8200, 2056), (17, 28680, 520), (32, 6150, 4104),
-    (33, 8, 520), (33, 8, 1032), (33, 4101, 520), (33, 2050, 1032), (33, 8200, 520), (33, 4101, 1032),
-    (33, 20000, 520), (33, 8200, 1032), (33, 28600, 520), (64, 6150, 2056), (33, 28680, 520), (64, 8, 8200),
+    (17, 20000, 520), (17, 8200, 1032), (17, 28600, 520), (17, 8200, 2056), (17, 28680, 520), (18, 9622, 1624),
+    (33, 8, 520), (33, 8, 1032), (33, 4101, 520), (33, 2050, 1032), (35, 13089, 520), (33, 4101, 1032),
+    (33, 20000, 520), (55, 12225, 2656), (33, 28600, 520), (42, 12474, 3128), (33, 28680, 520), (64, 8, 8200),
+]
+DECODE_DMA_SHAPES = [
+    (33, 8296, 536), (32, 965, 5928), (34, 16507, 552), (32, 4162, 2952), (64, 4162, 2952), (7, 32780, 520),
 ]
 
 
@@ -226,3 +296,10 @@ def test_coverage_shapes_reach_every_plan():
         assert N % (16 * wn) != 0, (M, N, K)
         reached.add((1 if M <= 16 else (2 if M <= 32 else 4), wn, wk, s > 1))
     assert reached == {(mt, wn, wk, split) for mt in (1, 2, 4) for wn, wk in SHAPES for split in (False, True)}
+    tiles = set()
+    for M, N, K in DECODE_DMA_SHAPES:
+        bm, bn, s, _ = capi.gemm_plan(M, N, K)
+        assert bm == 64 and N % bn != 0, (M, N, K)
+        tiles.add((bn, s > 1, M < 32))
+    assert tiles == {(64, False, False), (64, True, False), (128, False, False), (128, True, False),
+                     (64, False, True)}

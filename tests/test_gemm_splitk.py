@@ -1,11 +1,13 @@
-"""GPU tests of gemm_tn's skinny plans (``dk_gemm_tn_ws`` and the torch op
+"""GPU tests of gemm_tn's decode plans (``dk_gemm_tn_ws`` and the torch op
 ``gemm_tn``, which passes it a workspace from the caching allocator).
 
 Decode shapes run one workgroup per CU, with wide column tiles and, where
 that leaves too few tiles, the K reduction split over workgroups writing fp32
-partial tiles that a second kernel sums in a fixed order. Checks: every
-(row tiles, workgroup shape, split or not) plan against the fp32 oracle with
-a bias and a ragged N, in fp16 and bf16; every partial entry written
+partial tiles that a second kernel sums in a fixed order; from M = 32 (and
+for N > 32768) the LDS-DMA kernel's 64-row tiles take over where they fill
+the CUs. Checks: every (row tiles, workgroup shape, split or not) skinny plan
+and every (tile columns, split or not) decode DMA plan against the fp32
+oracle with a bias and a ragged N, in fp16 and bf16; every partial entry written
 (workspace pre-filled with NaN); determinism (two calls equal bit for bit); a
 missing or undersized workspace runs exactly ``dk_gemm_tn``; the torch op
 equals the C-ABI call; graph replays equal the eager result.
@@ -19,7 +21,7 @@ import torch
 import decodekernels_amd as dk
 from decodekernels_amd import capi
 from parity import assert_max_abs, gemm_f32
-from test_gemm_plan import COVERAGE_SHAPES
+from test_gemm_plan import COVERAGE_SHAPES, DECODE_DMA_SHAPES
 
 pytestmark = pytest.mark.gpu
 
@@ -30,11 +32,11 @@ def _stream():
 
 # The Llama-3-8B decode projections that split K, and ragged splits.
 SPLIT_SHAPES = [
-    (64, 4096, 14336),  # MLP down projection: 8 waves along N, 8 splits
-    (32, 4096, 14336),  # 4 splits
-    (16, 4096, 14336),  # 2 splits
-    (64, 4096, 4096),  # attention output projection: 4 splits
-    (48, 6144, 4096),  # fused qkv projection: 6 x 2 waves, 4 splits
+    (64, 4096, 14336),  # MLP down projection: 64 x 128 tiles, 8 splits
+    (32, 4096, 14336),  # the same
+    (16, 4096, 14336),  # skinny, 2 splits
+    (64, 4096, 4096),  # attention output projection: 64 x 64 tiles, 4 splits
+    (48, 6144, 4096),  # fused qkv projection: 64 x 128 tiles, 4 splits
     (17, 1000, 8200),  # ragged N and K, the last split shorter
     (33, 4101, 4104),  # N not a multiple of 4 (scalar reduce)
     (64, 8, 1024),  # one N tile
@@ -64,7 +66,7 @@ def _ws_call(a, b, bias, c, ws, nbytes):
     _call(capi.lib().dk_gemm_tn_ws, a, b, bias, c, None if ws is None else ws.data_ptr(), nbytes)
 
 
-@pytest.mark.parametrize("M,N,K", COVERAGE_SHAPES)
+@pytest.mark.parametrize("M,N,K", COVERAGE_SHAPES + DECODE_DMA_SHAPES)
 def test_every_plan_against_the_oracle(M, N, K):
     dtype = torch.bfloat16 if (M + N) % 2 else torch.float16
     a, b, bias = _operands(M, N, K, dtype, M * 131 + N)
@@ -164,8 +166,8 @@ def test_unsplit_shapes_ignore_the_workspace():
     """Shapes planned unsplit (any workspace) run dk_gemm_tn's kernel."""
     L = capi.lib()
     ws = torch.empty(1 << 20, device="cuda")
-    for M, N, K in [(8, 4096, 14336), (32, 6144, 4096), (64, 28672, 4096), (40, 33000, 1032), (512, 6144, 4096),
-                    (4096, 4096, 1032)]:
+    for M, N, K in [(8, 4096, 14336), (16, 6144, 4096), (64, 28672, 4096), (40, 33000, 1032), (34, 16507, 552),
+                    (512, 6144, 4096), (4096, 4096, 1032)]:
         assert L.dk_gemm_tn_workspace_bytes(M, N, K) == 0
         a, b, bias = _operands(M, N, K, torch.bfloat16, M + N)
         want = torch.empty(M, N, device="cuda", dtype=torch.bfloat16)

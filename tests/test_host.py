@@ -149,9 +149,10 @@ def test_capi_gemm_workspace_sizes_and_validation():
     """Split-K workspace sizes (splits x M x N fp32) for decode shapes the plan
     splits, 0 for the rest; argument errors of dk_gemm_tn_ws."""
     L = capi.lib()
-    for M, N, K, splits in [(64, 4096, 14336, 8), (32, 4096, 14336, 4), (16, 4096, 14336, 2), (64, 4096, 4096, 4),
-                            (64, 6144, 4096, 4), (17, 1000, 8200, 4), (8, 4096, 14336, 0), (32, 4096, 4096, 0),
-                            (32, 6144, 4096, 0), (64, 28672, 4096, 0), (0, 8, 64, 0),
+    for M, N, K, splits in [(64, 4096, 14336, 8), (32, 4096, 14336, 8), (16, 4096, 14336, 2), (64, 4096, 4096, 4),
+                            (64, 6144, 4096, 4), (17, 1000, 8200, 4), (8, 4096, 14336, 0), (16, 4096, 4096, 0),
+                            (32, 4096, 4096, 4), (16, 6144, 4096, 0), (32, 6144, 4096, 4), (64, 28672, 4096, 0),
+                            (64, 37888, 3584, 0), (0, 8, 64, 0),
                             (256, 4096, 14336, 8), (512, 4096, 14336, 4), (256, 28672, 4096, 0),
                             (4096, 4096, 4096, 0)]:
         assert L.dk_gemm_tn_workspace_bytes(M, N, K) == splits * M * N * 4, (M, N, K)
