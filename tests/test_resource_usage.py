@@ -81,8 +81,9 @@ def _pick(table, *parts):
 # balanced kernel and its grid form hold two 4-wave workgroups per CU at
 # head_dim 128 (16-bit cache), three with an fp8 cache, four at head_dim 64;
 # the split-K reduce and norms are small. GEMM: one 8-wave LDS-DMA workgroup of
-# the 256-row tiles per CU (two waves per SIMD), and the skinny M <= 64 tiles at
-# least 6 waves per SIMD at M = 1.
+# the 256-row tiles per CU (two waves per SIMD), two 4-wave workgroups of the
+# 64 x 64 decode tile, and the skinny M <= 64 tiles at least 6 waves per SIMD
+# at M = 1.
 OCCUPANCY = [
     (("paged_attention_balanced_kernel<dk::Bf16, 128, true, 16, 4, false>",), 2),
     (("paged_attention_balanced_kernel<dk::F16, 128, true, 16, 4, false>",), 2),
@@ -93,6 +94,7 @@ OCCUPANCY = [
     (("paged_attention_reduce_kernel<dk::Bf16, 128",), 8),
     (("gemm_dma_kernel<dk::Bf16, 256, 256, 4, 2, 2>",), 2),
     (("gemm_dma_kernel<dk::Bf16, 256, 192, 4, 2, 2>",), 2),
+    (("gemm_dma_kernel<dk::Bf16, 64, 64, 2, 2, 4>",), 2),
     (("gemm_skinny_lds_kernel<dk::Bf16, 1,",), 6),
     (("rms_norm_vec_kernel<dk::Bf16, 8>",), 5),
     (("fused_add_rms_norm_vec_kernel<dk::Bf16, 8>",), 5),
