@@ -764,8 +764,9 @@ def pmc_workload_gemm(calls: int = 3) -> None:
 
 
 def pmc_workload_gemm_skinny(calls: int = 3) -> None:
-    """What the skinny-GEMM counter runs profile: the decode layer's down
-    projection (N=4096, K=14336) at M=1 and M=64, `calls` times each."""
+    """What the decode-GEMM counter runs profile: the decode layer's down
+    projection (N=4096, K=14336) at M=1 (the skinny kernel) and M=64 (the
+    LDS-DMA kernel's 64-row tile with K in 8 splits), `calls` times each."""
     g = torch.Generator(device="cuda").manual_seed(1)
     w = torch.randn(4096, 14336, generator=g, device="cuda", dtype=torch.bfloat16) * 0.02
     for m in (1, 64):
@@ -774,7 +775,7 @@ def pmc_workload_gemm_skinny(calls: int = 3) -> None:
         for _ in range(calls):
             torch.ops.decode_kernels.gemm_tn(c, a, w, None)
     torch.cuda.synchronize()
-    print(f"pmc skinny gemm workload done: {calls} calls each at M=1 and M=64 (N=4096, K=14336)", flush=True)
+    print(f"pmc decode gemm workload done: {calls} calls each at M=1 and M=64 (N=4096, K=14336)", flush=True)
 
 
 def pmc_workload_attention_fp8(calls: int = 3) -> None:
