@@ -38,7 +38,7 @@ CSRC = PKG / "csrc"
 INCLUDE = ROOT / "include"
 BUILD = PKG / "_build"
 
-HIP_SOURCES = ["capi.hip", "paged_attention.hip", "gemm.hip", "norm_act.hip", "rope_cache.hip"]
+HIP_SOURCES = ["capi.hip", "paged_attention.hip", "gemm.hip", "norm_act.hip", "rope_cache.hip", "noalloc_scratch.hip"]
 LIB_NAME = "libdecodekernels_amd.so"
 EXT_NAME = "_C.so"
 ARCH = "gfx950"

@@ -48,4 +48,11 @@ int rotary_and_cache_on_rows(const char* op, const dk_rotary_params* r, const dk
                              bool fp8, float k_scale, float v_scale, const float* part, int splits, const void* bias,
                              void* C, int64_t ldc, int M, int N, bool check_only, hipStream_t s);
 
+namespace attn {
+// Device address of the current device's DK_NOALLOC_SCRATCH_BYTES-byte
+// workspace of the allocation-free attention entry point (noalloc_scratch.hip);
+// nullptr with *err set on failure.
+void* noalloc_scratch_address(int* err);
+}  // namespace attn
+
 }  // namespace dk

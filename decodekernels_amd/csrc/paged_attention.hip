@@ -1514,39 +1514,6 @@ int paged_attention_entry(const dk_paged_attn_params* a, int dtype, int head_dim
   return static_cast<int>(e);
 }
 
-// Split-K workspace of the allocation-free entry point: one array per GPU,
-// held by every device the library runs on until the process ends, shared
-// by all calls on that device (overlapping calls on one GPU race). Nothing in
-// it has to start at zero: the kernels read only rows written by the same call.
-static __device__ __align__(256) unsigned char scratch[DK_NOALLOC_SCRATCH_BYTES];
-
-// Device address of this device's `scratch` (host code must not use the
-// array's name, a host-side stand-in): looked up with hipGetSymbolAddress on
-// the first call on each device, with that device current, then cached.
-void* scratch_address(int* err) {
-  static std::atomic<void*> addr[kMaxDevices];
-  int dev = 0;
-  hipError_t e = hipGetDevice(&dev);
-  if (e != hipSuccess) {
-    *err = static_cast<int>(e);
-    return nullptr;
-  }
-  if (dev < 0 || dev >= kMaxDevices) {
-    *err = fail("paged_attention_decode_noalloc: device %d is beyond the %d devices supported", dev, kMaxDevices);
-    return nullptr;
-  }
-  void* p = addr[dev].load(std::memory_order_acquire);
-  if (p == nullptr) {
-    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
-    if (e != hipSuccess || p == nullptr) {
-      *err = e != hipSuccess ? static_cast<int>(e) : static_cast<int>(hipErrorInvalidSymbol);
-      return nullptr;
-    }
-    addr[dev].store(p, std::memory_order_release);  // every thread finds the same address
-  }
-  return p;
-}
-
 int paged_attention_noalloc(const dk_paged_attn_params* a, int dtype, int head_dim, int max_seq_len, void* stream) {
   clear_error();
   if (a == nullptr) return fail("paged_attention_decode_noalloc: params must not be NULL");
@@ -1571,7 +1538,7 @@ int paged_attention_noalloc(const dk_paged_attn_params* a, int dtype, int head_d
                 "ceil(max_seq_len / 512) x (head_dim + 2) x 4), more than the %lld-byte scratch",
                 static_cast<long long>(need), static_cast<long long>(DK_NOALLOC_SCRATCH_BYTES));
   int err = 0;
-  unsigned char* base = static_cast<unsigned char*>(scratch_address(&err));
+  unsigned char* base = static_cast<unsigned char*>(noalloc_scratch_address(&err));
   if (base == nullptr) return err;
   dk_paged_attn_params b = *a;
   b.tmp_out = reinterpret_cast<float*>(base);

@@ -99,7 +99,9 @@ int dk_paged_attention_decode_fp8(const dk_paged_attn_params* p, int dtype, int 
                                   float k_scale, float v_scale, void* stream);
 
 /* Size of the device array that dk_paged_attention_decode_noalloc uses as its
- * split-K workspace (64 MiB per GPU the library runs on). */
+ * split-K workspace: 64 MiB on each GPU where a no-alloc call has run (the
+ * array is in a code object of its own, loaded on a device at its first use
+ * there), held until the process ends. */
 #define DK_NOALLOC_SCRATCH_BYTES 67108864
 
 /*
