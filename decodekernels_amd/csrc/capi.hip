@@ -28,4 +28,6 @@ extern "C" const char* dk_last_error(void) { return dk::g_last_error.c_str(); }
 
 extern "C" const char* dk_error_string(int code) { return hipGetErrorString(static_cast<hipError_t>(code)); }
 
-extern "C" const char* dk_version(void) { return "decodekernels_amd 0.1.0 (gfx950)"; }
+// The package version (pyproject.toml's [project] version, checked by
+// tests/test_packaging.py) and the target.
+extern "C" const char* dk_version(void) { return "decodekernels_amd 0.2.0 (gfx950)"; }

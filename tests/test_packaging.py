@@ -64,6 +64,12 @@ def test_vllm_entry_point_from_package_metadata(tmp_path):
     assert dists[0].metadata["Version"] == decodekernels_amd.__version__
 
 
+def test_c_library_reports_the_package_version():
+    from decodekernels_amd import capi
+
+    assert capi.lib().dk_version().decode() == f"decodekernels_amd {decodekernels_amd.__version__} (gfx950)"
+
+
 def test_plugin_docstring_names_the_registered_entry_point():
     text = decodekernels_amd.vllm_plugin.__doc__
     assert 'decode_kernels = "decode_kernels.vllm_plugin:register"' in text
