@@ -378,10 +378,17 @@ __global__ __launch_bounds__(WM * WN * kWave) void gemm_dma_kernel(const uint16_
   constexpr int TM = BM / WM / 16;  // 16-row fragments per wave
   constexpr int TN = BN / WN / 16;
   constexpr int LA = BM / 8 / NW;   // 1 KB DMA loads per wave per slice
-  constexpr int LB = BN / 8 / NW;
+  // B's 8-row load groups need not divide among the waves (256 x 224: 28 groups
+  // for 8 waves); the waves past the last group skip their final load.
+  constexpr int kGroupsB = BN / 8;
+  constexpr int LB = (kGroupsB + NW - 1) / NW;
+  constexpr bool kTailB = kGroupsB % NW != 0;
   constexpr int kSlice = (BM + BN) * 8;  // u32x4 per slice
-  static_assert(BM % (8 * NW) == 0 && BN % (8 * NW) == 0 && TM >= 1 && TN >= 1, "tile shape");
+  static_assert(BM % (8 * NW) == 0 && BN % 8 == 0 && TM >= 1 && TN >= 1 && BN % (16 * WN) == 0, "tile shape");
   static_assert(STAGES >= 2 && (STAGES - 2) * (LA + LB) < 64, "vmcnt range");
+  // With uneven B loads the waves have different counts in flight, which only
+  // a 2-stage ring's vmcnt(0) waits allow.
+  static_assert(!kTailB || STAGES == 2, "uneven B loads need STAGES == 2");
   constexpr int kStagePitch = BN / WN * 2 + 16;         // bytes per staged output row
   constexpr int kStageWave = BM / WM * kStagePitch;     // bytes of one wave's staged tile
   static_assert((BM / WM) * (BN / WN / 8) % kWave == 0, "staged tile: whole 64-lane passes");
@@ -430,10 +437,11 @@ __global__ __launch_bounds__(WM * WN * kWave) void gemm_dma_kernel(const uint16_
     const int r = 8 * (wave + j * NW) + lane / 8;
     const int c = (lane % 8) ^ swz(r);
     kbc[j] = 8 * c;
-    offb[j] = r < rows_b ? r * ldb * 2 + 16 * c : kOutOfRange;
+    offb[j] = r < rows_b && r < BN ? r * ldb * 2 + 16 * c : kOutOfRange;
   }
   // Issued for every slice index, also past the last one (those lanes are out
-  // of range and move no data), so each wave always has the same count in flight.
+  // of range and move no data), so each wave keeps the same count in flight
+  // from slice to slice.
   auto issue = [&](int t, int buf) {
     const int k0 = kb + t * kDmaBK;
     u32x4* base = lds + buf * kSlice;
@@ -445,6 +453,8 @@ __global__ __launch_bounds__(WM * WN * kWave) void gemm_dma_kernel(const uint16_
     }
 #pragma unroll
     for (int j = 0; j < LB; ++j) {
+      // A wave past B's last load group issues nothing (its LDS target would be past the slice).
+      if (kTailB && j == LB - 1 && wave + j * NW >= kGroupsB) break;
       const int off = (offb[j] != kOutOfRange && k0 + kbc[j] < ke) ? offb[j] + 2 * k0 : kOutOfRange;
       __builtin_amdgcn_raw_ptr_buffer_load_lds(
           rb, (__attribute__((address_space(3))) void*)(base + BM * 8 + (wave + j * NW) * 64), 16, off, 0, 0, 0);
@@ -630,8 +640,9 @@ using DmaLauncher = hipError_t (*)(const uint16_t*, const uint16_t*, const uint1
 template <typename E>
 const DmaLauncher* dma_launchers() {
   static const DmaLauncher fns[] = {
-      launch_dma<E, 256, 256, 4, 2, 2>, launch_dma<E, 256, 192, 4, 2, 2>, launch_dma<E, 256, 128, 4, 2, 3>,
-      launch_dma<E, 128, 128, 4, 2, 3>, launch_dma<E, 128, 64, 2, 2, 4>,  launch_dma<E, 64, 64, 2, 2, 4>,
+      launch_dma<E, 256, 256, 4, 2, 2>, launch_dma<E, 256, 224, 4, 2, 2>, launch_dma<E, 256, 192, 4, 2, 2>,
+      launch_dma<E, 256, 128, 4, 2, 3>, launch_dma<E, 128, 128, 4, 2, 3>, launch_dma<E, 128, 64, 2, 2, 4>,
+      launch_dma<E, 64, 64, 2, 2, 4>,
   };
   return fns;
 }
@@ -796,7 +807,12 @@ inline int64_t skinny_workspace_bytes(const SkinnyPlan& p, int M, int N) {
 // whole rounds where 256 x 256 leaves the last one part-empty: qkv (N 6144)
 // M = 1536 / 3072 / 4096 / 6000 103.9 / 188.3 / 194.1 / 298.7 -> 93.5 / 175.7
 // / 182.2 / 258.1, N 3072 and 5120 at M = 4096 105.2 / 185.9 -> 98.3 / 175.3
-// (each pick the fastest of the three 256-row tiles).
+// (each pick the fastest of the three 256-row tiles). The 256 x 224 tile does
+// the same for N = 28672 (128 column tiles; its rate fitted to gate_up at
+// M = 384 ... 4096, where 256 x 256 leaves the last round part-empty):
+// gate_up M = 384 / 512 / 1024 / 1536 / 2048 / 3072 102.7 / 110.0 / 206.7 /
+// 306.0 / 411.7 / 604.3 -> 96.9 / 104.3 / 197.0 / 289.5 / 378.0 / 570.7 (M =
+// 768 and 4096 keep 256 x 192 and 256 x 256, measured as fast or faster).
 struct DmaPlan {
   int shape, splits, k_split;
 };
@@ -809,7 +825,8 @@ struct DmaShape {
   double rate;  // TFLOP/s per CU
 };
 constexpr DmaShape kDmaShapes[] = {
-    {256, 256, 5.355}, {256, 192, 5.15}, {256, 128, 4.776}, {128, 128, 3.48}, {128, 64, 2.398}, {64, 64, 2.007},
+    {256, 256, 5.355}, {256, 224, 4.95}, {256, 192, 5.15}, {256, 128, 4.776},
+    {128, 128, 3.48},  {128, 64, 2.398}, {64, 64, 2.007},
 };
 
 inline DmaPlan dma_plan(int M, int N, int K, bool split_ok) {

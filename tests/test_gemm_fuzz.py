@@ -57,3 +57,30 @@ def test_tiled_gemm_random_shapes(M, N, K, with_bias, bf16):
         assert rc == 0, capi.last_error()
         torch.cuda.synchronize()
         assert torch.equal(c, out)
+
+
+# Shapes whose plan is the 256 x 224 tile, whose 28 B load groups do not divide
+# among its 8 waves (the last 4 waves skip a load): full tiles, ragged M, ragged
+# N, both, and K in 4 splits.
+TILE_224_SHAPES = [(512, 28672, 4096), (1053, 11424, 88), (768, 18728, 120), (522, 16519, 64), (271, 6563, 5824)]
+
+
+@pytest.mark.parametrize("M,N,K", TILE_224_SHAPES)
+@pytest.mark.parametrize("bf16", [True, False])
+def test_tile_224_against_fp32(M, N, K, bf16):
+    dtype = torch.bfloat16 if bf16 else torch.float16
+    plan = capi.gemm_plan(M, N, K)
+    print(f"gemm {M}x{N}x{K} {dtype} plan {plan}", flush=True)
+    assert plan[:2] == (256, 224), plan
+    g = torch.Generator(device="cuda").manual_seed(M + N + K)
+    a = torch.randn(M, K, generator=g, device="cuda", dtype=dtype)
+    b = torch.randn(N, K, generator=g, device="cuda", dtype=dtype) / K**0.5
+    bias = torch.randn(N, generator=g, device="cuda", dtype=dtype)
+    out = dk.gemm(a, b, bias)
+    assert_max_abs(out, gemm_f32_gpu(a, b, bias), dtype, f"gemm {M}x{N}x{K} plan {plan}")
+    c = torch.full((M, N), float("nan"), device="cuda", dtype=dtype)
+    rc = capi.lib().dk_gemm_tn(capi.dtype_code(dtype), a.data_ptr(), b.data_ptr(), None, c.data_ptr(), M, N, K, K, K, N,
+                               ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+    assert rc == 0, capi.last_error()
+    torch.cuda.synchronize()
+    assert_max_abs(c, gemm_f32_gpu(a, b), dtype, f"gemm {M}x{N}x{K} unsplit, no bias")

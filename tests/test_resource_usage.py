@@ -95,6 +95,7 @@ OCCUPANCY = [
     (("paged_attention_reduce_kernel<dk::Bf16, 128",), 8),
     (("gemm_dma_kernel<dk::Bf16, 256, 256, 4, 2, 2>",), 2),
     (("gemm_dma_kernel<dk::Bf16, 256, 192, 4, 2, 2>",), 2),
+    (("gemm_dma_kernel<dk::Bf16, 256, 224, 4, 2, 2>",), 2),
     (("gemm_dma_kernel<dk::Bf16, 64, 64, 2, 2, 4>",), 2),
     (("gemm_skinny_lds_kernel<dk::Bf16, 1,",), 6),
     (("rms_norm_vec_kernel<dk::Bf16, 8>",), 5),
