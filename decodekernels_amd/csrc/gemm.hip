@@ -641,8 +641,8 @@ template <typename E>
 const DmaLauncher* dma_launchers() {
   static const DmaLauncher fns[] = {
       launch_dma<E, 256, 256, 4, 2, 2>, launch_dma<E, 256, 224, 4, 2, 2>, launch_dma<E, 256, 192, 4, 2, 2>,
-      launch_dma<E, 256, 128, 4, 2, 3>, launch_dma<E, 128, 128, 4, 2, 3>, launch_dma<E, 128, 64, 2, 2, 4>,
-      launch_dma<E, 64, 64, 2, 2, 4>,
+      launch_dma<E, 256, 128, 4, 2, 3>, launch_dma<E, 192, 192, 4, 2, 3>, launch_dma<E, 128, 128, 4, 2, 3>,
+      launch_dma<E, 128, 64, 2, 2, 4>,  launch_dma<E, 64, 64, 2, 2, 4>,
   };
   return fns;
 }
@@ -813,6 +813,12 @@ inline int64_t skinny_workspace_bytes(const SkinnyPlan& p, int M, int N) {
 // gate_up M = 384 / 512 / 1024 / 1536 / 2048 / 3072 102.7 / 110.0 / 206.7 /
 // 306.0 / 411.7 / 604.3 -> 96.9 / 104.3 / 197.0 / 289.5 / 378.0 / 570.7 (M =
 // 768 and 4096 keep 256 x 192 and 256 x 256, measured as fast or faster).
+// The 192 x 192 tile (8 waves, 3 stages; N = 6144 is 32 of its columns, so
+// M = 1536 is one full round): its rate is the one, on a grid search over
+// every (tile, split) candidate timed for six projections at M = 128 ... 6144,
+// that adds no pick more than 2% slower than the plan before it. It takes qkv
+// (N 6144) at M = 384 / 768 / 1536 / 3072 from 43.8 / 62.3 / 90.8 / 159.5 to
+// 38.0 / 53.6 / 70.8 / 133.1 us (hipBLASLt 40.1 / 52.8 / 78.1 / 141.0).
 struct DmaPlan {
   int shape, splits, k_split;
 };
@@ -825,8 +831,8 @@ struct DmaShape {
   double rate;  // TFLOP/s per CU
 };
 constexpr DmaShape kDmaShapes[] = {
-    {256, 256, 5.355}, {256, 224, 4.95}, {256, 192, 5.15}, {256, 128, 4.776},
-    {128, 128, 3.48},  {128, 64, 2.398}, {64, 64, 2.007},
+    {256, 256, 5.355}, {256, 224, 4.95}, {256, 192, 5.15},  {256, 128, 4.776},
+    {192, 192, 3.95},  {128, 128, 3.48}, {128, 64, 2.398}, {64, 64, 2.007},
 };
 
 inline DmaPlan dma_plan(int M, int N, int K, bool split_ok) {

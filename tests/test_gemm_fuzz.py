@@ -60,18 +60,24 @@ def test_tiled_gemm_random_shapes(M, N, K, with_bias, bf16):
 
 
 # Shapes whose plan is the 256 x 224 tile, whose 28 B load groups do not divide
-# among its 8 waves (the last 4 waves skip a load): full tiles, ragged M, ragged
-# N, both, and K in 4 splits.
-TILE_224_SHAPES = [(512, 28672, 4096), (1053, 11424, 88), (768, 18728, 120), (522, 16519, 64), (271, 6563, 5824)]
+# among its 8 waves (the last 4 waves skip a load), or the 192 x 192 tile (3
+# stages): full tiles, ragged M, ragged N, both, and K in 4 or 8 splits.
+TILE_SHAPES = [
+    ((256, 224), (512, 28672, 4096)), ((256, 224), (1053, 11424, 88)), ((256, 224), (768, 18728, 120)),
+    ((256, 224), (522, 16519, 64)), ((256, 224), (271, 6563, 5824)),
+    ((192, 192), (1536, 6144, 4096)), ((192, 192), (1844, 4416, 72)), ((192, 192), (612, 11259, 64)),
+    ((192, 192), (384, 6144, 4808)), ((192, 192), (1152, 1800, 3528)), ((192, 192), (131, 5464, 4512)),
+]
 
 
-@pytest.mark.parametrize("M,N,K", TILE_224_SHAPES)
+@pytest.mark.parametrize("tile,shape", TILE_SHAPES, ids=[f"{t[0]}x{t[1]}-{m}x{n}x{k}" for t, (m, n, k) in TILE_SHAPES])
 @pytest.mark.parametrize("bf16", [True, False])
-def test_tile_224_against_fp32(M, N, K, bf16):
+def test_tile_shapes_against_fp32(tile, shape, bf16):
+    M, N, K = shape
     dtype = torch.bfloat16 if bf16 else torch.float16
     plan = capi.gemm_plan(M, N, K)
     print(f"gemm {M}x{N}x{K} {dtype} plan {plan}", flush=True)
-    assert plan[:2] == (256, 224), plan
+    assert plan[:2] == tile, plan
     g = torch.Generator(device="cuda").manual_seed(M + N + K)
     a = torch.randn(M, K, generator=g, device="cuda", dtype=dtype)
     b = torch.randn(N, K, generator=g, device="cuda", dtype=dtype) / K**0.5
