@@ -21,7 +21,7 @@
 //   in flight across the per-step barrier.
 // * LDS-DMA (M > 64, batched decode and prefill): A and B tiles go from HBM
 //   straight into LDS (buffer_load ... lds), bank-conflict-free XOR-swizzled,
-//   through a multi-stage ring; six tile shapes from 256x256 down to 64x64,
+//   through a multi-stage ring; nine tile shapes from 256x256 down to 64x64,
 //   picked per call by a throughput model so that batches of a few hundred
 //   rows still fill all 256 CUs. The output tile leaves through the freed
 //   ring, read back row by row for 16-byte stores. At M <= 64 its 64-row
@@ -391,7 +391,6 @@ __global__ __launch_bounds__(WM * WN * kWave) void gemm_dma_kernel(const uint16_
   static_assert(!kTailB || STAGES == 2, "uneven B loads need STAGES == 2");
   constexpr int kStagePitch = BN / WN * 2 + 16;         // bytes per staged output row
   constexpr int kStageWave = BM / WM * kStagePitch;     // bytes of one wave's staged tile
-  static_assert((BM / WM) * (BN / WN / 8) % kWave == 0, "staged tile: whole 64-lane passes");
   constexpr int kLdsU4 = STAGES * kSlice > NW * kStageWave / 16 ? STAGES * kSlice : NW * kStageWave / 16;
   static_assert(kLdsU4 * 16 <= 160 * 1024, "LDS of one workgroup (gfx950: 160 KB)");
   __shared__ u32x4 lds[kLdsU4];
@@ -591,9 +590,11 @@ __global__ __launch_bounds__(WM * WN * kWave) void gemm_dma_kernel(const uint16_
     }
   }
   __syncthreads();  // the tile's rows come from the other lanes of the wave
+  constexpr int kChunks = (BM / WM) * kNc;  // 16-byte chunks of a wave's tile
 #pragma unroll
-  for (int it = 0; it < (BM / WM) * kNc / kWave; ++it) {
+  for (int it = 0; it < (kChunks + kWave - 1) / kWave; ++it) {
     const int idx = it * kWave + lane;
+    if (kChunks % kWave != 0 && idx >= kChunks) break;  // last pass part-filled (192 x 224: 10.5 passes)
     const int row = idx / kNc;
     const int c = idx % kNc;
     const u32x4 val = *reinterpret_cast<const u32x4*>(stg + row * kStagePitch + c * 16);
@@ -641,8 +642,8 @@ template <typename E>
 const DmaLauncher* dma_launchers() {
   static const DmaLauncher fns[] = {
       launch_dma<E, 256, 256, 4, 2, 2>, launch_dma<E, 256, 224, 4, 2, 2>, launch_dma<E, 256, 192, 4, 2, 2>,
-      launch_dma<E, 256, 128, 4, 2, 3>, launch_dma<E, 192, 192, 4, 2, 3>, launch_dma<E, 128, 128, 4, 2, 3>,
-      launch_dma<E, 128, 64, 2, 2, 4>,  launch_dma<E, 64, 64, 2, 2, 4>,
+      launch_dma<E, 256, 128, 4, 2, 3>, launch_dma<E, 192, 224, 4, 2, 2>, launch_dma<E, 192, 192, 4, 2, 3>,
+      launch_dma<E, 128, 128, 4, 2, 3>, launch_dma<E, 128, 64, 2, 2, 4>,  launch_dma<E, 64, 64, 2, 2, 4>,
   };
   return fns;
 }
@@ -819,6 +820,12 @@ inline int64_t skinny_workspace_bytes(const SkinnyPlan& p, int M, int N) {
 // that adds no pick more than 2% slower than the plan before it. It takes qkv
 // (N 6144) at M = 384 / 768 / 1536 / 3072 from 43.8 / 62.3 / 90.8 / 159.5 to
 // 38.0 / 53.6 / 70.8 / 133.1 us (hipBLASLt 40.1 / 52.8 / 78.1 / 141.0).
+// The 192 x 224 tile (2 stages, 106 KB; its last epilogue pass is half
+// filled) got its rate the same way, on eight projections (Qwen2.5-7B's
+// gate_up and down added): every rate in 4.51 ... 4.60 picks it for 12 shapes,
+// none more than 0.4% slower, and from 4.61 on it displaces 192 x 192 at
+// 7-32% cost. Gains: Llama gate_up M = 768 182.1 -> 166.1 us; Qwen2.5-7B down
+// M = 384 ... 6144 4.5-7.5%, gate_up M = 512 5%, o M = 3072 6%, qkv M = 2048 7%.
 struct DmaPlan {
   int shape, splits, k_split;
 };
@@ -831,7 +838,7 @@ struct DmaShape {
   double rate;  // TFLOP/s per CU
 };
 constexpr DmaShape kDmaShapes[] = {
-    {256, 256, 5.355}, {256, 224, 4.95}, {256, 192, 5.15},  {256, 128, 4.776},
+    {256, 256, 5.355}, {256, 224, 4.95}, {256, 192, 5.15}, {256, 128, 4.776}, {192, 224, 4.55},
     {192, 192, 3.95},  {128, 128, 3.48}, {128, 64, 2.398}, {64, 64, 2.007},
 };
 

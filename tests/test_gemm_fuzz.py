@@ -59,14 +59,17 @@ def test_tiled_gemm_random_shapes(M, N, K, with_bias, bf16):
         assert torch.equal(c, out)
 
 
-# Shapes whose plan is the 256 x 224 tile, whose 28 B load groups do not divide
-# among its 8 waves (the last 4 waves skip a load), or the 192 x 192 tile (3
-# stages): full tiles, ragged M, ragged N, both, and K in 4 or 8 splits.
+# Shapes whose plan is the 256 x 224 or 192 x 224 tile, whose 28 B load groups
+# do not divide among the 8 waves (the last 4 waves skip a load; 192 x 224 also
+# fills its last epilogue pass half), or the 192 x 192 tile (3 stages): full
+# tiles, ragged M, ragged N, both, and K in 4 or 8 splits.
 TILE_SHAPES = [
     ((256, 224), (512, 28672, 4096)), ((256, 224), (1053, 11424, 88)), ((256, 224), (768, 18728, 120)),
-    ((256, 224), (522, 16519, 64)), ((256, 224), (271, 6563, 5824)),
+    ((256, 224), (795, 13247, 64)), ((192, 224), (271, 6563, 5824)),
     ((192, 192), (1536, 6144, 4096)), ((192, 192), (1844, 4416, 72)), ((192, 192), (612, 11259, 64)),
     ((192, 192), (384, 6144, 4808)), ((192, 192), (1152, 1800, 3528)), ((192, 192), (131, 5464, 4512)),
+    ((192, 224), (768, 28672, 4096)), ((192, 224), (1049, 8736, 144)), ((192, 224), (1728, 5472, 136)),
+    ((192, 224), (263, 24976, 64)), ((192, 224), (132, 6168, 5440)),
 ]
 
 

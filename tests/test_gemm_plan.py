@@ -129,8 +129,8 @@ def replica_skinny_plan(M, N, K, with_workspace=True, mistake=None):
     return u if u is not None else _wide(M, N, K)
 
 
-DMA_SHAPES = [(256, 256, 5.355), (256, 224, 4.95), (256, 192, 5.15), (256, 128, 4.776), (192, 192, 3.95), (128, 128, 3.48),
-              (128, 64, 2.398), (64, 64, 2.007)]
+DMA_SHAPES = [(256, 256, 5.355), (256, 224, 4.95), (256, 192, 5.15), (256, 128, 4.776), (192, 224, 4.55),
+              (192, 192, 3.95), (128, 128, 3.48), (128, 64, 2.398), (64, 64, 2.007)]
 DMA_MAX_WORKSPACE = 64 << 20
 
 
@@ -201,17 +201,19 @@ def test_tiled_plans_like_the_replica():
 
 
 # (M, N, K) -> (tile rows, tile columns, splits) measured fastest at batched decode
-# and, for the 256 x 192, 256 x 224 and 192 x 192 tiles, at sizes where 256 x 256
-# leaves a round part-empty.
+# and, for the 256 x 192, 256 x 224, 192 x 224 and 192 x 192 tiles, at sizes where
+# 256 x 256 leaves a round part-empty.
 TILED_PICKS = {
     (128, 4096, 14336): (128, 128, 8), (256, 4096, 14336): (256, 128, 8), (512, 4096, 14336): (256, 128, 4),
     (256, 6144, 4096): (128, 128, 2), (256, 28672, 4096): (256, 128, 1), (512, 6144, 4096): (128, 128, 1),
     (4096, 4096, 4096): (256, 256, 1), (4096, 28672, 4096): (256, 256, 1),
     (4096, 6144, 4096): (256, 192, 1), (4096, 3072, 4096): (256, 192, 1),
     (512, 28672, 4096): (256, 224, 1), (2048, 28672, 4096): (256, 224, 1), (3072, 28672, 4096): (256, 224, 1),
-    (768, 28672, 4096): (256, 192, 1),
+    (768, 28672, 4096): (192, 224, 1), (384, 3584, 18944): (192, 224, 8), (768, 3584, 18944): (192, 224, 4),
+    (3072, 3584, 18944): (192, 224, 1), (512, 37888, 3584): (192, 224, 1), (3072, 3584, 3584): (192, 224, 1),
+    (2048, 4608, 3584): (192, 224, 1),
     (384, 6144, 4096): (192, 192, 4), (768, 6144, 4096): (192, 192, 2), (1536, 6144, 4096): (192, 192, 1),
-    (3072, 6144, 4096): (192, 192, 1),
+    (3072, 6144, 4096): (192, 192, 1), (128, 37888, 3584): (192, 192, 1), (384, 37888, 3584): (192, 192, 1),
 }
 
 

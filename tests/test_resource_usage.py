@@ -97,6 +97,7 @@ OCCUPANCY = [
     (("gemm_dma_kernel<dk::Bf16, 256, 192, 4, 2, 2>",), 2),
     (("gemm_dma_kernel<dk::Bf16, 256, 224, 4, 2, 2>",), 2),
     (("gemm_dma_kernel<dk::Bf16, 192, 192, 4, 2, 3>",), 2),
+    (("gemm_dma_kernel<dk::Bf16, 192, 224, 4, 2, 2>",), 2),
     (("gemm_dma_kernel<dk::Bf16, 64, 64, 2, 2, 4>",), 2),
     (("gemm_skinny_lds_kernel<dk::Bf16, 1,",), 6),
     (("rms_norm_vec_kernel<dk::Bf16, 8>",), 5),
