@@ -132,6 +132,31 @@ def test_paged_attention_reduce_many_rows(seq_len, min_rows, schedule, monkeypat
         assert (_workspace_rows(ws[2]) == -(-seq_len // 512)).all()
 
 
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("lens", [[2048] * 32, [8192] * 8, [700] * 24, [3000, 1, 2047, 0] * 6],
+                         ids=["32x2048", "8x8192", "24x700", "mixed24"])
+def test_paged_attention_balanced_small_totals(dtype, lens, monkeypatch):
+    """Balanced schedule with too little work for the first-dispatched half's
+    full share ratio above the 64-tile minimum share: the second half keeps the
+    minimum and the first half takes the rest. Against the oracle, and every
+    stream's pieces stay inside the workspace's rows."""
+    monkeypatch.setenv("DK_ATTN_SCHEDULE", "balanced")
+    n, ml = len(lens), max(lens)
+    kv = make_paged_kv(lens, 8, 128, 16, dtype, "cuda", layout="nhd", seed=n + ml)
+    q = _q(n, 32, 128, dtype, seed=ml)
+    ws = dk.alloc_workspace(n, 32, 128, ml, "cuda")
+    for t in ws:
+        t.fill_(float("nan"))
+    out = dk.paged_attention_decode(q, kv.k_cache, kv.v_cache, kv.block_tables, kv.seq_lens, max_seq_len=ml,
+                                    workspace=ws)
+    torch.cuda.synchronize()
+    assert_max_abs(out, attention_f32(q, kv.k_cache, kv.v_cache, kv.block_tables, kv.seq_lens), dtype,
+                   f"balanced, {n} sequences up to {ml} tokens")
+    rows = _workspace_rows(ws[2])
+    live = torch.tensor(lens).repeat_interleave(32).view(n, 32) > 0
+    assert (rows[live] >= 1).all() and (rows <= ws[2].shape[-1]).all()
+
+
 # Qwen2.5-7B (28 query / 4 KV heads, group 7, head_dim 128), Qwen2.5-0.5B
 # (14 / 2, group 7, head_dim 64) and groups 3, 5 and 6.
 ODD_GROUP_CASES = [(28, 4, 128), (14, 2, 64), (6, 2, 128), (10, 2, 64), (12, 2, 256), (21, 3, 96)]
