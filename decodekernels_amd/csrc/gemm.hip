@@ -812,8 +812,9 @@ inline int64_t skinny_workspace_bytes(const SkinnyPlan& p, int M, int N) {
 // the same for N = 28672 (128 column tiles; its rate fitted to gate_up at
 // M = 384 ... 4096, where 256 x 256 leaves the last round part-empty):
 // gate_up M = 384 / 512 / 1024 / 1536 / 2048 / 3072 102.7 / 110.0 / 206.7 /
-// 306.0 / 411.7 / 604.3 -> 96.9 / 104.3 / 197.0 / 289.5 / 378.0 / 570.7 (M =
-// 768 and 4096 keep 256 x 192 and 256 x 256, measured as fast or faster).
+// 306.0 / 411.7 / 604.3 -> 96.9 / 104.3 / 197.0 / 289.5 / 378.0 / 570.7 (at
+// M = 768 it ties 256 x 192, and the 192 x 224 tile below beats both; M = 4096
+// keeps 256 x 256, measured faster).
 // The 192 x 192 tile (8 waves, 3 stages; N = 6144 is 32 of its columns, so
 // M = 1536 is one full round): its rate is the one, on a grid search over
 // every (tile, split) candidate timed for six projections at M = 128 ... 6144,
