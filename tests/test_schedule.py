@@ -27,7 +27,10 @@ the reduce rely on:
   table entries one wave holds (one per lane) for block sizes that are
   multiples of 16;
 * the 128K batch-1 configuration spans more than 64 rows per stream (the
-  reduce's second ballot pass, also asserted on the GPU).
+  reduce's second ballot pass, also asserted on the GPU);
+* when the work is too small for the pair ratio above the 64-tile minimum
+  share, the second half of the grid keeps the minimum and still gets work
+  (the ratio shrinks instead of the first half's shares taking it all).
 """
 
 import math
@@ -57,8 +60,15 @@ def balanced_schedule(lens, hkv, P, G, pair_ratio, stream_cost, mistake=None, wi
     H = G // 2
     r = pair_ratio
     denom = H * r + (G - H) * 100
-    share_b = max(MIN_SHARE, (total * 100 + denom - 1) // denom)
-    share_a = max(MIN_SHARE, (share_b * r + 99) // 100)
+    share_b = (total * 100 + denom - 1) // denom
+    if share_b >= MIN_SHARE:
+        share_a = max(MIN_SHARE, (share_b * r + 99) // 100)
+    elif mistake == "clamp":  # the second half at the minimum, the ratio kept
+        share_b = MIN_SHARE
+        share_a = max(MIN_SHARE, (share_b * r + 99) // 100)
+    else:  # too little work for the ratio above the minimum: the first half takes the rest
+        share_b = MIN_SHARE
+        share_a = max(MIN_SHARE, (total - (G - H) * MIN_SHARE + H - 1) // max(H, 1))
     split_at = H * share_a
 
     def first_pos(wg):
@@ -183,6 +193,9 @@ def llama_lens():
         ("one_stream_140k", [140000], 1, 274, 512, 200),
         ("one_stream_270k", [270000], 1, 528, 512, 200),
         ("fp8_three_per_cu", llama_lens(), 8, 8, 768, 100),
+        ("small_llama_b32_2048", [2048] * 32, 8, 4, 512, 200),
+        ("small_llama_b8_8192", [8192] * 8, 8, 16, 512, 200),
+        ("small_qwen7b_b64", llama_lens(), 4, 8, 512, 200),
     ],
 )
 def test_benchmark_shapes(name, lens, hkv, P, G, ratio):
@@ -238,3 +251,20 @@ def test_largest_balanced_launch_keeps_32_bit_boundaries(G):
     assert 2048 * 8 * P * (PART // TILE) < 2**30
     pieces, _, _, tiles_of = balanced_schedule(lens, 8, P, G, 200 if G == 512 else 100, 12, with_subs=False)
     assert sum(hi - lo for ps in pieces.values() for _, _, lo, hi, _ in ps) == 8 * sum(tiles_of)
+
+
+@pytest.mark.parametrize("lens,hkv,P", [([2048] * 32, 8, 4), ([8192] * 8, 8, 16), ([1500] * 40, 8, 3)])
+def test_small_totals_keep_both_halves_busy(lens, hkv, P):
+    """Cost lines too short for a 2:1 first-half ratio above the minimum share:
+    at least as many workgroups of the second half get work as the minimum
+    share allows, so the grid is not left half idle. Keeping the ratio with
+    the second half raised to the minimum (a planted mistake) fails this."""
+    def busy_second_half(mistake=None):
+        pieces, _, _, _ = balanced_schedule(lens, hkv, P, 512, 200, 8, mistake=mistake, with_subs=False)
+        return len({w for ps in pieces.values() for w, *_ in ps if w >= 256})
+
+    total = sum(((min(x, P * PART) + TILE - 1) // TILE + 8) * hkv for x in lens)
+    expect = min(256, max(0, total - 256 * MIN_SHARE) // MIN_SHARE)  # second-half shares the work fills
+    assert busy_second_half() >= expect
+    assert busy_second_half("clamp") < expect
+    check(lens, hkv, P, 512)
