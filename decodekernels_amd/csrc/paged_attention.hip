@@ -135,6 +135,7 @@ struct KParams {
   int num_units;  // split-K grid: unit positions per sequence, ceil(max_partitions / 2)
   int unit512;    // split-K grid: one 512-token unit per workspace row instead (small grids)
   int pair_ratio;  // balanced kernel: share of workgroups [0, grid/2) over the others', x100
+  int lockstep;    // balanced kernel: groups of num_kv_heads workgroups share one token range (grid % heads == 0)
   float scale_log2;  // softmax scale x log2(e) (x k_scale for an fp8 cache)
   float v_scale;     // multiplies the output (fp8 cache's v_scale; 1 otherwise)
 };
@@ -807,6 +808,12 @@ void paged_attention_kernel(const KParams p) {
 // next piece's block-table entries, query and first tiles load while the
 // current one finishes: no piece start waits on a round trip, no atomics.
 //
+// Lockstep variant (16-bit caches): the line holds sequences only, each
+// costing its tiles plus the overhead once, and its shares go to groups of
+// num_kv_heads consecutive workgroups; workgroup h of a group runs KV head h
+// of the group's share, so a sequence's KV heads read the same tokens at
+// about the same time. Everything below holds with "group" for "workgroup".
+//
 // A piece is one stream's tiles inside a workgroup's share (run as sub-units
 // of at most 64 tiles sharing one softmax state). Its partial result goes to
 // workspace row (w - workgroup of the stream's first tile) of the stream's
@@ -842,6 +849,10 @@ void paged_attention_balanced_kernel(const KParams p) {
   // The query strides, read from here once per stream: kept in scalar
   // registers across the piece loop, they were what spilled at head_dim 96.
   __shared__ int32_t q_str[2];
+  // The stream walk's KV-head step: [0] heads per sequence on the line (hl
+  // below), [1] this workgroup's first KV head (kv0). Read from LDS in the
+  // walk for the same reason (two more scalar registers spilled at head_dim 96).
+  __shared__ int32_t walk[2];
   // Wave totals of the set-up scan, in wave 0's region (no tile is processed before the set-up's last barrier).
   static_assert(sizeof(sm.w[0]) >= NW * sizeof(int), "scan space");
   int* scan = reinterpret_cast<int*>(&sm.w[0]);
@@ -885,13 +896,24 @@ void paged_attention_balanced_kernel(const KParams p) {
   if (tid == 0) {
     q_str[0] = p.q_ss;
     q_str[1] = p.q_sh;
+    walk[0] = p.lockstep ? 1 : p.num_kv_heads;
+    walk[1] = p.lockstep ? static_cast<int>(blockIdx.x) % p.num_kv_heads : 0;
   }
   __syncthreads();
 
   const int hkv = p.num_kv_heads;
-  const int total = pre[S] * hkv;  // < 2^31 (checked by the host)
-  const int G = gridDim.x;
-  // Shares: workgroups [0, H) take share_a each, [H, G) share_b.
+  // Lockstep: the line holds sequences only (one position per tile of every
+  // KV head at once) and its shares go to groups of hkv consecutive
+  // workgroups, workgroup kv0 of a group taking KV head kv0 of the group's
+  // share. Otherwise every workgroup is a group of one and the line holds
+  // the (sequence, KV head) streams. The host sets lockstep only when hkv
+  // divides the grid into at least two groups.
+  const bool lock = p.lockstep != 0;
+  const int R = lock ? hkv : 1;   // workgroups per group
+  const int hl = lock ? 1 : hkv;  // KV heads laid on the line per sequence
+  const int total = pre[S] * hl;  // < 2^31 (checked by the host)
+  const int G = static_cast<int>(gridDim.x) / R;  // groups
+  // Shares: groups [0, H) take share_a each, [H, G) share_b.
   const int H = G / 2;
   int share_a, share_b;
   {
@@ -919,34 +941,35 @@ void paged_attention_balanced_kernel(const KParams p) {
   // positions per workgroup.
   const int split_at = H * share_a;
   auto first_pos = [&](int wg) -> int { return wg < H ? wg * share_a : split_at + (wg - H) * share_b; };
-  auto owner = [&](int x) -> int {  // workgroup whose share holds cost position x
+  auto owner = [&](int x) -> int {  // group whose share holds cost position x
     return x < split_at ? x / share_a : H + (x - split_at) / share_b;
   };
-  const int w = blockIdx.x;
-  if (first_pos(w) >= total) return;
+  const int w = static_cast<int>(blockIdx.x) / R;  // group
+  const int kv0 = static_cast<int>(blockIdx.x) - w * R;  // lockstep: this workgroup's KV head; else 0
+  if (w >= G || first_pos(w) >= total) return;
   const int a = first_pos(w);
   const int b = min(first_pos(w + 1), total);
   auto cost_of = [&](int s) { return pre[s + 1] - pre[s]; };
 
   // Stream holding cost position a: the last sequence whose first position
-  // is <= a (it has tiles, since pre[S] * hkv > a), then the KV head.
+  // is <= a (it has tiles, since pre[S] * hl > a), then the KV head.
   int seq = 0;
   {
     int lo = 0, hi = S;
     while (hi - lo > 1) {
       const int mid = (lo + hi) >> 1;
-      if (pre[mid] * hkv <= a) lo = mid;
+      if (pre[mid] * hl <= a) lo = mid;
       else hi = mid;
     }
     seq = lo;
   }
-  int kv = (a - pre[seq] * hkv) / cost_of(seq);
+  int kv = kv0 + (a - pre[seq] * hl) / cost_of(seq);
   // Row of this share's piece of that stream: the number of shares before
   // this one that hold its tiles. Every later stream starts inside this share
   // (its first tile lies at or past a), so its row is 0; the share layout
   // (and its scalar registers) is not needed past this point.
   const int first_row = [&]() {
-    const int first = pre[seq] * hkv + kv * cost_of(seq) + kStreamCost;
+    const int first = pre[seq] * hl + (kv - kv0) * cost_of(seq) + kStreamCost;
     return first < a ? w - owner(first) : 0;
   }();
 
@@ -955,8 +978,8 @@ void paged_attention_balanced_kernel(const KParams p) {
   int u = 0, hi = 0, row = 0;
   bool last_tile_here = false;  // this share holds the stream's last tile
   auto advance = [&]() {        // to the next stream with tiles; false if none
-    if (++kv < hkv) return true;
-    kv = 0;
+    if (++kv < walk[1] + walk[0]) return true;
+    kv = walk[1];
     for (;;) {
       if (++seq >= S) return false;
       if (cost_of(seq) > 0) return true;
@@ -964,7 +987,7 @@ void paged_attention_balanced_kernel(const KParams p) {
   };
   auto enter_stream = [&]() {  // false once the streams start past the share
     for (;;) {
-      const int first = pre[seq] * hkv + kv * cost_of(seq) + kStreamCost;  // position of tile 0
+      const int first = pre[seq] * walk[0] + (kv - walk[1]) * cost_of(seq) + kStreamCost;  // position of tile 0
       const int n = tiles_of(seq);
       if (first >= b) return false;
       const int lo = max(a, first) - first;
@@ -1308,6 +1331,15 @@ inline Schedule forced_schedule() {
   return Schedule::kAuto;
 }
 
+// DK_ATTN_LOCKSTEP=0 / 1 overrides the balanced schedule's default grouping
+// (read on every call, for tests and measurements).
+inline bool lockstep_wanted(bool by_default) {
+  const char* v = std::getenv("DK_ATTN_LOCKSTEP");
+  if (v != nullptr && std::strcmp(v, "0") == 0) return false;
+  if (v != nullptr && std::strcmp(v, "1") == 0) return true;
+  return by_default;
+}
+
 template <int D, int WPH, bool PIECES, typename E>
 void launch_reduce(const KParams& kp, int num_seqs, hipStream_t stream) {
   constexpr int HPW = reduce_waves<WPH>() / WPH;
@@ -1349,13 +1381,28 @@ hipError_t launch_split(KParams kp, int num_kv_heads, int num_seqs, int align, h
   // each CU's second slot) streams faster, so the first half of the grid
   // takes the larger shares. (2-wave workgroups at 1 wave/SIMD do not share.)
   kp.pair_ratio = per_cu == 2 && waves_per_group<D>() == 4 ? DK_ATTN_PAIR_RATIO : 100;
-  // Automatic choice: a grid of 512-token units when it fits in one round of
-  // resident workgroups (a small call: twice the workgroups of 1024-token
-  // units, each with half the tokens, so the call's critical path halves);
-  // else the balanced schedule when the 1024-token grid would exceed a round;
-  // else that grid.
-  const bool partitions = forced == Schedule::kPartitions ||
-                          (forced == Schedule::kAuto && resident > 0 && partition_units <= resident);
+  // Lockstep groups (a sequence's KV heads over the same tokens at once) for
+  // 16-bit caches: 0.5-3% faster over most measured shapes (128K batch 1
+  // 2.6%, Llama-3-8B 8 x 32K 3.3%), one 2.5% slower (64 x 8K). With an fp8
+  // cache they were up to 23% slower on an NHD cache, so fp8 keeps one
+  // workgroup per share.
+  kp.lockstep = lockstep_wanted(!KV8) && resident > 0 && resident % num_kv_heads == 0 && resident / num_kv_heads >= 2;
+  // Automatic choice: a grid of 512-token units while it needs at most
+  // kPartThirds / 3 rounds of resident workgroups (a small call: twice the
+  // workgroups of 1024-token units, each with half the tokens, so the call's
+  // critical path halves, and no set-up scan); else the balanced schedule
+  // when the 1024-token grid would exceed a round; else that grid. The
+  // limit per kernel class, measured against the balanced schedule on
+  // uniform and ragged batches, vLLM and NHD caches (cold calls):
+  //   head_dim <= 64 (4 workgroups per CU): up to 2 rounds (up to 3 still won 5-12%);
+  //   head_dim 96/128, 16-bit cache: 2 rounds (1-2: 0-11% faster; 2-3: vLLM 1-4% slower);
+  //   head_dim 96/128, fp8 cache (3 per CU): 4/3 of a round (to 1024 units:
+  //     5-15% faster; 1.7-2 rounds: ragged vLLM batches up to 11% slower);
+  //   head_dim > 128 (2-wave workgroups): 1 round (1.5-2 rounds: 3-12% slower).
+  constexpr int64_t kPartThirds = D > 128 ? 3 : (KV8 && D > 64 ? 4 : 6);
+  const bool partitions =
+      forced == Schedule::kPartitions ||
+      (forced == Schedule::kAuto && resident > 0 && 3 * partition_units <= kPartThirds * resident);
   const bool balanced = !partitions && balanced_ok && resident > 0 &&
                         (forced == Schedule::kBalanced || (forced == Schedule::kAuto && grid_units > resident));
   hipError_t e;

@@ -73,9 +73,13 @@ def test_fp8_head_dim_192_and_group_16(dtype, head_dim, group, schedule, monkeyp
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
-@pytest.mark.parametrize("schedule", ["grid", "balanced", "partitions"])
+@pytest.mark.parametrize("schedule", ["grid", "balanced", "balanced-lockstep", "partitions"])
 def test_fp8_long_contexts_both_schedules(dtype, schedule, monkeypatch):
-    monkeypatch.setenv("DK_ATTN_SCHEDULE", schedule)
+    """Long ragged contexts under every schedule, including the balanced
+    schedule's lockstep groups (not the fp8 default; DK_ATTN_LOCKSTEP=1)."""
+    monkeypatch.setenv("DK_ATTN_SCHEDULE", schedule.split("-")[0])
+    if schedule == "balanced-lockstep":
+        monkeypatch.setenv("DK_ATTN_LOCKSTEP", "1")
     lens = [16384, 3000, 7777, 1, 600, 9000, 12000, 5]
     kv = make_paged_kv(lens, 8, 128, 16, FP8, "cuda", layout="vllm", seed=7)
     _check(_q(len(lens), 32, 128, dtype, seed=3), kv, 0.031, 0.25, dtype)

@@ -6,9 +6,9 @@
 * C3 -- 128K-token contexts, batch 4, fp16, HND cache, 1% of K/V rows scaled
   by 8; every sequence against the CPU oracle (one at a time).
 * C3 -- the same at batch 1 (one 128K context, 8 KV streams): under the
-  balanced schedule each stream is cut into one piece per workgroup share,
-  so the reduce merges more than 64 workspace rows per query head (asserted
-  from the workspace contents).
+  balanced schedule with one workgroup per share each stream is cut into one
+  piece per share, so the reduce merges more than 64 workspace rows per
+  query head (asserted from the workspace contents).
 * C5 -- the head-dim-256 / group-8 stress batch: 256 sequences with
   log-uniform lengths in [1, 32768] and 8 empty ones, 16 query / 2 KV heads,
   block 32, bf16 and fp16; every sequence against the CPU oracle. The NHD
@@ -23,7 +23,9 @@ unchanged bit for bit, and doubling V (exact in bf16 / fp16) doubles it bit
 for bit wherever the output is a normal number (subnormal outputs round on a
 fixed grid, so round(2x) and 2 round(x) may differ there by one spacing).
 All three split-K schedules (1024-token grid units, balanced shares, 512-token
-partitions) run on every configuration.
+partitions) run on every configuration, the balanced one both with its default
+grouping (lockstep groups of KV heads for 16-bit caches) and with one
+workgroup per share (``balanced-plain``).
 """
 
 import math
@@ -134,10 +136,12 @@ def case(request):
     torch.cuda.empty_cache()
 
 
-@pytest.mark.parametrize("schedule", ["grid", "balanced", "partitions"])
+@pytest.mark.parametrize("schedule", ["grid", "balanced", "balanced-plain", "partitions"])
 def test_full_size_against_oracle(case, schedule, monkeypatch):
     name, c, kv, q, ref = case
-    monkeypatch.setenv("DK_ATTN_SCHEDULE", schedule)
+    monkeypatch.setenv("DK_ATTN_SCHEDULE", schedule.split("-")[0])
+    if schedule == "balanced-plain":
+        monkeypatch.setenv("DK_ATTN_LOCKSTEP", "0")
     ws = dk.alloc_workspace(q.shape[0], q.shape[1], q.shape[2], kv.max_seq_len, "cuda")
     for t in ws:
         t.fill_(float("nan"))  # every row the reduce reads must have been written by this call
@@ -148,7 +152,7 @@ def test_full_size_against_oracle(case, schedule, monkeypatch):
     assert_max_abs(out, ref, c["dtype"], f"{name} ({schedule})")
     empty = kv.seq_lens == 0
     assert (out[empty] == 0).all(), f"{name}: empty sequences must give zeros"
-    if schedule == "balanced" and c.get("min_rows"):
+    if schedule == "balanced-plain" and c.get("min_rows"):
         rows = int(_workspace_rows(ws[2]).max())
         assert rows > c["min_rows"], f"{name}: the longest stream spans {rows} workspace rows (> {c['min_rows']} expected)"
 

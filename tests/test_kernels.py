@@ -157,6 +157,39 @@ def test_paged_attention_balanced_small_totals(dtype, lens, monkeypatch):
     assert (rows[live] >= 1).all() and (rows <= ws[2].shape[-1]).all()
 
 
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("lockstep", ["0", "1"])
+@pytest.mark.parametrize("hkv", [8, 4, 3, 1])
+def test_paged_attention_balanced_lockstep(dtype, lockstep, hkv, monkeypatch):
+    """Balanced schedule with one workgroup per share (DK_ATTN_LOCKSTEP=0) and
+    with lockstep groups of hkv workgroups sharing each share (=1; 3 KV heads
+    do not divide the resident grid, so the host keeps one workgroup per
+    share). Ragged lengths with empty sequences, against the oracle; every
+    stream's pieces stay inside the workspace rows, and under lockstep all
+    query heads of a sequence fill the same number of rows (its KV heads take
+    the same pieces)."""
+    monkeypatch.setenv("DK_ATTN_SCHEDULE", "balanced")
+    monkeypatch.setenv("DK_ATTN_LOCKSTEP", lockstep)
+    lens = [5000, 0, 1, 777, 2048, 16, 9000, 513, 0, 3100] * 3
+    n, ml, hq = len(lens), max(lens), 4 * hkv
+    kv = make_paged_kv(lens, hkv, 128, 16, dtype, "cuda", layout="nhd", seed=hkv)
+    q = _q(n, hq, 128, dtype, seed=hkv + 1)
+    ws = dk.alloc_workspace(n, hq, 128, ml, "cuda")
+    for t in ws:
+        t.fill_(float("nan"))
+    out = dk.paged_attention_decode(q, kv.k_cache, kv.v_cache, kv.block_tables, kv.seq_lens, max_seq_len=ml,
+                                    workspace=ws)
+    torch.cuda.synchronize()
+    assert_max_abs(out, attention_f32(q, kv.k_cache, kv.v_cache, kv.block_tables, kv.seq_lens), dtype,
+                   f"balanced, lockstep={lockstep}, {hkv} KV heads")
+    assert (out[torch.tensor(lens) == 0] == 0).all(), "empty sequences give zeros"
+    rows = _workspace_rows(ws[2])
+    live = torch.tensor(lens) > 0
+    assert (rows[live] >= 1).all() and (rows <= ws[2].shape[-1]).all()
+    if lockstep == "1" and hkv != 3:
+        assert (rows == rows[:, :1]).all(), "lockstep: every KV head of a sequence takes the same pieces"
+
+
 # Qwen2.5-7B (28 query / 4 KV heads, group 7, head_dim 128), Qwen2.5-0.5B
 # (14 / 2, group 7, head_dim 64) and groups 3, 5 and 6.
 ODD_GROUP_CASES = [(28, 4, 128), (14, 2, 64), (6, 2, 128), (10, 2, 64), (12, 2, 256), (21, 3, 96)]

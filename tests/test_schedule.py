@@ -43,12 +43,16 @@ PART = 512
 MIN_SHARE = 64
 
 
-def balanced_schedule(lens, hkv, P, G, pair_ratio, stream_cost, mistake=None, with_subs=True):
-    """Pieces {(seq, kv): [(wg, row, tile_lo, tile_hi, sub_units)]} and marks
-    {(seq, kv): row} as the kernel computes them. ``mistake`` plants an error
-    (tests show the checks catch it): "row" numbers rows from the owner of the
-    stream's overhead instead of its first tile; "end" ends a piece one tile
-    early."""
+def balanced_schedule(lens, hkv, P, grid, pair_ratio, stream_cost, mistake=None, with_subs=True, lockstep=False):
+    """Pieces {(seq, kv): [(group, row, tile_lo, tile_hi, sub_units)]} and
+    marks {(seq, kv): row} as the kernel computes them for a launch of ``grid``
+    workgroups. ``lockstep``: the line holds sequences only and groups of hkv
+    consecutive workgroups share each share, one KV head each (else every
+    workgroup is a group of one). ``mistake`` plants an error (tests show the
+    checks catch it): "row" numbers rows from the owner of the stream's
+    overhead instead of its first tile; "end" ends a piece one tile early;
+    "clamp" keeps the pair ratio for small totals; "head" gives the lockstep
+    walk the head of the group's first workgroup instead of its own."""
     S = len(lens)
     ln = [min(max(x, 0), P * PART) for x in lens]
     tiles_of = [(x + TILE - 1) // TILE for x in ln]
@@ -56,7 +60,10 @@ def balanced_schedule(lens, hkv, P, G, pair_ratio, stream_cost, mistake=None, wi
     pre = [0]
     for c in cost_len:
         pre.append(pre[-1] + c)
-    total = pre[S] * hkv
+    R = hkv if lockstep else 1  # workgroups per group
+    hl = 1 if lockstep else hkv  # KV heads laid on the line per sequence
+    total = pre[S] * hl
+    G = grid // R  # groups
     H = G // 2
     r = pair_ratio
     denom = H * r + (G - H) * 100
@@ -83,30 +90,32 @@ def balanced_schedule(lens, hkv, P, G, pair_ratio, stream_cost, mistake=None, wi
     assert max(split_at, first_pos(G)) < 2**31, "share boundaries must fit 32-bit integers"
 
     pieces, marks = {}, {}
-    for w in range(G):
-        if first_pos(w) >= total:
+    for x in range(grid):
+        w = x // R
+        kv0 = 0 if mistake == "head" else x - w * R
+        if w >= G or first_pos(w) >= total:
             continue
         a = first_pos(w)
         b = min(first_pos(w + 1), total)
         lo, hi_s = 0, S
         while hi_s - lo > 1:
             mid = (lo + hi_s) >> 1
-            if pre[mid] * hkv <= a:
+            if pre[mid] * hl <= a:
                 lo = mid
             else:
                 hi_s = mid
         st = {"seq": lo}
         assert cost_of(lo) > 0
-        st["kv"] = (a - pre[lo] * hkv) // cost_of(lo)
-        first0 = pre[lo] * hkv + st["kv"] * cost_of(lo) + stream_cost
+        st["kv"] = kv0 + (a - pre[lo] * hl) // cost_of(lo)
+        first0 = pre[lo] * hl + (st["kv"] - kv0) * cost_of(lo) + stream_cost
         anchor0 = first0 - stream_cost if mistake == "row" else first0
         first_row = w - owner(anchor0) if first0 < a else 0
 
         def advance():
             st["kv"] += 1
-            if st["kv"] < hkv:
+            if st["kv"] < kv0 + hl:
                 return True
-            st["kv"] = 0
+            st["kv"] = kv0
             while True:
                 st["seq"] += 1
                 if st["seq"] >= S:
@@ -117,7 +126,7 @@ def balanced_schedule(lens, hkv, P, G, pair_ratio, stream_cost, mistake=None, wi
         def enter():
             while True:
                 seq, kv = st["seq"], st["kv"]
-                first = pre[seq] * hkv + kv * cost_of(seq) + stream_cost
+                first = pre[seq] * hl + (kv - kv0) * cost_of(seq) + stream_cost
                 n = tiles_of[seq]
                 if first >= b:
                     return False
@@ -150,8 +159,9 @@ def balanced_schedule(lens, hkv, P, G, pair_ratio, stream_cost, mistake=None, wi
     return pieces, marks, ln, tiles_of
 
 
-def check(lens, hkv, P, G, pair_ratio=200, stream_cost=8, block_size=16, mistake=None):
-    pieces, marks, ln, tiles_of = balanced_schedule(lens, hkv, P, G, pair_ratio, stream_cost, mistake)
+def check(lens, hkv, P, G, pair_ratio=200, stream_cost=8, block_size=16, mistake=None, lockstep=False):
+    pieces, marks, ln, tiles_of = balanced_schedule(lens, hkv, P, G, pair_ratio, stream_cost, mistake,
+                                                    lockstep=lockstep)
     max_rows = 0
     for s in range(len(lens)):
         for kv in range(hkv):
@@ -159,7 +169,10 @@ def check(lens, hkv, P, G, pair_ratio=200, stream_cost=8, block_size=16, mistake
             if ln[s] == 0:
                 assert key not in pieces
                 continue
+            assert key in pieces, key
             ps = sorted(pieces[key], key=lambda p: p[2])
+            if lockstep:  # every KV head of the sequence takes the same pieces (groups, rows, tiles)
+                assert [p[:4] for p in ps] == [p[:4] for p in sorted(pieces[(s, 0)], key=lambda p: p[2])], key
             pos = 0
             for _, _, t_lo, t_hi, subs in ps:
                 assert t_lo == pos, (key, ps)
@@ -198,9 +211,10 @@ def llama_lens():
         ("small_qwen7b_b64", llama_lens(), 4, 8, 512, 200),
     ],
 )
-def test_benchmark_shapes(name, lens, hkv, P, G, ratio):
-    rows = check(lens, hkv, P, G, ratio, stream_cost=12 if name.startswith("fp8") else 8)
-    if name == "c3_128k_b1":
+@pytest.mark.parametrize("lockstep", [False, True])
+def test_benchmark_shapes(name, lens, hkv, P, G, ratio, lockstep):
+    rows = check(lens, hkv, P, G, ratio, stream_cost=12 if name.startswith("fp8") else 8, lockstep=lockstep)
+    if name == "c3_128k_b1" and not lockstep:  # lockstep: 64 groups, at most one piece each
         assert rows > 64
     if name == "one_stream_140k":
         assert rows > 64
@@ -226,30 +240,37 @@ def test_random_shapes():
             lens.append(x)
         if sum(lens) == 0:
             lens[0] = 1
-        check(lens, rng.choice([1, 2, 4, 8]), P, rng.choice([1, 2, 7, 64, 256, 512, 768, 1024]),
-              rng.choice([100, 150, 200, 240]), rng.choice([0, 1, 8, 12, 70]), rng.choice([16, 32, 48]))
+        hkv = rng.choice([1, 2, 4, 5, 8])
+        grid = rng.choice([1, 2, 7, 64, 256, 510, 512, 768, 1024])
+        lockstep = grid % hkv == 0 and grid // hkv >= 2 and rng.random() < 0.5  # the host's condition
+        check(lens, hkv, P, grid, rng.choice([100, 150, 200, 240]), rng.choice([0, 1, 8, 12, 70]),
+              rng.choice([16, 32, 48]), lockstep=lockstep)
 
 
-@pytest.mark.parametrize("mistake", ["row", "end"])
-def test_planted_mistake_is_caught(mistake):
+@pytest.mark.parametrize("mistake,lockstep", [("row", False), ("end", False), ("row", True), ("end", True),
+                                              ("head", True)])
+def test_planted_mistake_is_caught(mistake, lockstep):
     """Row numbers anchored on a stream's overhead instead of its first tile
-    (a stream whose overhead starts in the previous share gets no row 0), or a
-    piece that stops one tile short, must fail the checks."""
+    (a stream whose overhead starts in the previous share gets no row 0), a
+    piece that stops one tile short, or lockstep workgroups that all walk the
+    group's first KV head, must fail the checks."""
     lens = llama_lens()
-    check(lens, 8, 8, 512)
+    check(lens, 8, 8, 512, lockstep=lockstep)
     with pytest.raises(AssertionError):
-        check(lens, 8, 8, 512, mistake=mistake)
+        check(lens, 8, 8, 512, mistake=mistake, lockstep=lockstep)
 
 
 @pytest.mark.parametrize("G", [512, 768])
-def test_largest_balanced_launch_keeps_32_bit_boundaries(G):
+@pytest.mark.parametrize("lockstep", [False, True])
+def test_largest_balanced_launch_keeps_32_bit_boundaries(G, lockstep):
     """The host takes the balanced schedule while sequences x KV heads x
     partitions x 32 tiles < 2^30: at 2048 sequences of the longest length the
     cost line is just below that, and every share boundary still fits."""
     P = (2**30 // (2048 * 8 * 32)) - 1
     lens = [P * PART] * 2048
     assert 2048 * 8 * P * (PART // TILE) < 2**30
-    pieces, _, _, tiles_of = balanced_schedule(lens, 8, P, G, 200 if G == 512 else 100, 12, with_subs=False)
+    pieces, _, _, tiles_of = balanced_schedule(lens, 8, P, G, 200 if G == 512 else 100, 12, with_subs=False,
+                                               lockstep=lockstep)
     assert sum(hi - lo for ps in pieces.values() for _, _, lo, hi, _ in ps) == 8 * sum(tiles_of)
 
 
