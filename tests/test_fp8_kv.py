@@ -131,6 +131,18 @@ def test_fp8_odd_gqa_groups(dtype, hq, hkv, head_dim, schedule, monkeypatch):
     _check(_q(len(short), hq, head_dim, dtype, seed=hq + 1), kv_s, 0.2, 0.7, dtype)
 
 
+@pytest.mark.parametrize("layout", ["nhd", "vllm"])
+def test_fp8_automatic_schedule_llama_batch(layout):
+    """The automatic schedule at the Llama-3-8B batch-64 shape (lengths
+    U[512, 4096], 32 / 8 heads) over an fp8 cache: the NHD cache takes the
+    1024-token grid, the vLLM cache the balanced schedule; both against the
+    oracle on every sequence."""
+    g = torch.Generator().manual_seed(0)
+    lens = torch.randint(512, 4097, (64,), generator=g).tolist()
+    kv = make_paged_kv(lens, 8, 128, 16, FP8, "cuda", layout=layout, seed=23)
+    _check(_q(64, 32, 128, torch.bfloat16, seed=24) * 128**-0.5, kv, 0.5, 0.5, torch.bfloat16)
+
+
 @pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("split", [False, True])
 def test_fp8_equals_16bit_path_on_the_converted_cache(dtype, split):
