@@ -1449,7 +1449,6 @@ hipError_t launch_kv(const KParams& kp, int num_kv_heads, int num_seqs, bool spl
              : launch<E, D, false>(kp, num_kv_heads, num_seqs, split, bs16, align, stream);
 }
 
-// Largest of 16/8/4 bytes that every K/V row start is aligned to.
 // Largest of 16/8/4 bytes that every K/V row start is aligned to, for
 // elements of `elt` bytes.
 int kv_alignment(const dk_paged_attn_params& a, int elt) {
