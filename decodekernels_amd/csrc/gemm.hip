@@ -1021,6 +1021,16 @@ int gemm_tn_checked(int dtype, const void* A, const void* B, const void* bias, v
     return fail("gemm_tn: expected float16 or bfloat16, got dtype code %d", dtype);
   if (M < 0 || N < 0 || K < 0) return fail("gemm_tn: M, N and K must be non-negative");
   if (M == 0 || N == 0) return hipSuccess;
+  // A lone row's stride is never used: take the row length. Otherwise a row
+  // stride below the row length would overlap rows, cut the last rows off the
+  // load descriptors' extents (read as zeros) and write C out of bounds.
+  if (M == 1) {
+    lda = K;
+    ldc = N;
+  }
+  if (N == 1) ldb = K;
+  if (lda < K || ldb < K || ldc < N)
+    return fail("gemm_tn: row strides must be at least the row lengths (lda, ldb >= K, ldc >= N)");
   if (K % 8 != 0 || lda % 8 != 0 || ldb % 8 != 0)
     return fail("gemm_tn: K and row strides of a/b must be multiples of 8");
   if (!aligned_to(A, 16) || !aligned_to(B, 16)) return fail("gemm_tn: a and b must be 16-byte aligned");

@@ -127,7 +127,9 @@ int dk_paged_attention_decode_noalloc(const dk_paged_attn_params* p, int dtype, 
 /*
  * C[M,N] = A[M,K] * B[N,K]^T (+ bias[N]), fp32 accumulation, one rounding.
  * Replaces dk::launch_gemm_tn<T> (csrc/gemm_wmma.cuh:209-219).
- * K, lda and ldb must be multiples of 8; A and B 16-byte aligned; bias may be NULL.
+ * K, lda and ldb must be multiples of 8, lda and ldb >= K, ldc >= N (the
+ * stride of a single row, M = 1 or N = 1, is ignored); A and B 16-byte
+ * aligned; bias may be NULL.
  * Takes no workspace: shapes whose fastest plan splits K (see dk_gemm_tn_ws)
  * run unsplit.
  */

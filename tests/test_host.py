@@ -143,6 +143,14 @@ def test_capi_gemm_validation():
     assert L.dk_gemm_tn(capi.DK_BFLOAT16, 0x1000, 0x1000, None, 0x1000, 4, 0, 64, 64, 64, 8, None) == 0
     rc = L.dk_gemm_tn(5, 0x1000, 0x1000, None, 0x1000, 4, 8, 64, 64, 64, 8, None)
     assert rc == capi.HIP_ERROR_INVALID_VALUE and "float16 or bfloat16" in capi.last_error()
+    # Row strides below the row lengths (overlapping rows; C written out of bounds) are refused,
+    # negative ones included.
+    for lda, ldb, ldc in [(56, 64, 16), (64, 56, 16), (64, 64, 8), (-64, 64, 16), (64, 64, -16)]:
+        rc = L.dk_gemm_tn(capi.DK_BFLOAT16, 0x1000, 0x1000, None, 0x1000, 4, 16, 64, lda, ldb, ldc, None)
+        assert rc == capi.HIP_ERROR_INVALID_VALUE and "at least the row lengths" in capi.last_error(), (lda, ldb, ldc)
+    rc = L.dk_gemm_tn_ws(capi.DK_BFLOAT16, 0x1000, 0x1000, None, 0x1000, 64, 4096, 14336, 14336, 14336, 4000,
+                         None, 0, None)
+    assert rc == capi.HIP_ERROR_INVALID_VALUE and "at least the row lengths" in capi.last_error()
 
 
 def test_capi_gemm_workspace_sizes_and_validation():
