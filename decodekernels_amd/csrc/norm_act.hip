@@ -380,6 +380,9 @@ extern "C" int dk_rms_norm(int dtype, void* out, const void* input, const void* 
   if (rows < 0 || H < 0) return fail("rms_norm: rows and H must be non-negative");
   if (rows == 0 || H == 0) return hipSuccess;
   if (out == nullptr || input == nullptr || weight == nullptr) return fail("rms_norm: pointers must not be NULL");
+  // Rows read may repeat (stride 0 broadcasts one row); rows written may not overlap.
+  if (in_stride < 0 || (rows > 1 && out_stride < H))
+    return fail("rms_norm: strides must be non-negative and out_stride >= H (written rows must not overlap)");
   const bool vec = H % kVec == 0 && in_stride % kVec == 0 && out_stride % kVec == 0 && aligned_to(input, 16) &&
                    aligned_to(out, 16) && aligned_to(weight, 16);
   auto* o = static_cast<uint16_t*>(out);
@@ -398,6 +401,8 @@ extern "C" int dk_fused_add_rms_norm(int dtype, void* input, void* residual, con
   if (rows == 0 || H == 0) return hipSuccess;
   if (input == nullptr || residual == nullptr || weight == nullptr)
     return fail("fused_add_rms_norm: pointers must not be NULL");
+  if (rows > 1 && (in_stride < H || res_stride < H))
+    return fail("fused_add_rms_norm: in_stride and res_stride must be >= H (both are written; rows must not overlap)");
   const bool vec = H % kVec == 0 && in_stride % kVec == 0 && res_stride % kVec == 0 && aligned_to(input, 16) &&
                    aligned_to(residual, 16) && aligned_to(weight, 16);
   auto* x = static_cast<uint16_t*>(input);
@@ -438,6 +443,8 @@ extern "C" int dk_silu_and_mul(int dtype, void* out, const void* input, int rows
   if (rows < 0 || d < 0) return fail("silu_and_mul: rows and d must be non-negative");
   if (rows == 0 || d == 0) return hipSuccess;
   if (out == nullptr || input == nullptr) return fail("silu_and_mul: pointers must not be NULL");
+  if (in_stride < 0 || (rows > 1 && out_stride < d))
+    return fail("silu_and_mul: strides must be non-negative and out_stride >= d (written rows must not overlap)");
   if (ceil_div64(d, kSiluThreads) > 65535) return fail("silu_and_mul: d is too large");
   const bool vec =
       d % kVec == 0 && in_stride % kVec == 0 && out_stride % kVec == 0 && aligned_to(input, 16) && aligned_to(out, 16);

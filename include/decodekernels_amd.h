@@ -176,6 +176,8 @@ int dk_gemm_tn_ws(int dtype, const void* A, const void* B, const void* bias, voi
 /*
  * out = x * rsqrt(mean(x^2) + eps) * weight, per row of H elements.
  * Replaces dk::launch_rms_norm<T> (csrc/norm_act.cuh:153-166).
+ * Strides in elements, non-negative; out_stride >= H when rows > 1 (rows
+ * written must not overlap; in_stride 0 repeats one input row).
  */
 int dk_rms_norm(int dtype, void* out, const void* input, const void* weight, int rows, int H, int64_t in_stride,
                 int64_t out_stride, float eps, void* stream);
@@ -183,6 +185,7 @@ int dk_rms_norm(int dtype, void* out, const void* input, const void* weight, int
 /*
  * In place: residual = round(input + residual); input = rms_norm(residual) * weight.
  * Replaces dk::launch_fused_add_rms_norm<T> (csrc/norm_act.cuh:168-183).
+ * Both buffers are written: in_stride, res_stride >= H when rows > 1.
  */
 int dk_fused_add_rms_norm(int dtype, void* input, void* residual, const void* weight, int rows, int H,
                           int64_t in_stride, int64_t res_stride, float eps, void* stream);
@@ -190,6 +193,7 @@ int dk_fused_add_rms_norm(int dtype, void* input, void* residual, const void* we
 /*
  * out[r, :d] = silu(input[r, :d]) * input[r, d:2d].
  * Replaces dk::launch_silu_and_mul<T> (csrc/norm_act.cuh:185-198).
+ * Strides in elements, non-negative; out_stride >= d when rows > 1.
  */
 int dk_silu_and_mul(int dtype, void* out, const void* input, int rows, int d, int64_t in_stride, int64_t out_stride,
                     void* stream);

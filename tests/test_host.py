@@ -185,6 +185,14 @@ def test_capi_norm_validation():
     assert L.dk_silu_and_mul(capi.DK_FLOAT16, 0x1000, 0x1000, 5, 0, 0, 0, None) == 0
     rc = L.dk_silu_and_mul(capi.DK_FLOAT16, 0x1000, 0x1000, -1, 8, 16, 8, None)
     assert rc == capi.HIP_ERROR_INVALID_VALUE
+    # Written rows may not overlap and no stride may be negative (a read-only input may repeat a row).
+    for rc in (L.dk_rms_norm(capi.DK_BFLOAT16, 0x1000, 0x1000, 0x1000, 4, 64, 64, 32, 1e-6, None),
+               L.dk_rms_norm(capi.DK_BFLOAT16, 0x1000, 0x1000, 0x1000, 4, 64, -64, 64, 1e-6, None),
+               L.dk_fused_add_rms_norm(capi.DK_BFLOAT16, 0x1000, 0x1000, 0x1000, 4, 64, 0, 64, 1e-6, None),
+               L.dk_fused_add_rms_norm(capi.DK_BFLOAT16, 0x1000, 0x1000, 0x1000, 4, 64, 64, 8, 1e-6, None),
+               L.dk_silu_and_mul(capi.DK_FLOAT16, 0x1000, 0x1000, 4, 8, 16, 4, None),
+               L.dk_silu_and_mul(capi.DK_FLOAT16, 0x1000, 0x1000, 4, 8, -16, 8, None)):
+        assert rc == capi.HIP_ERROR_INVALID_VALUE and "overlap" in capi.last_error()
     assert capi.lib().dk_error_string(1)
 
 
