@@ -376,10 +376,12 @@ def extras_attention() -> dict:
                                         **attention_cpu_path(cpu, len(c["seq_lens"]))}
         progress(f"D=256 stress {tag}: {t['median_us']} us (checked, max abs err {err:.2e})")
         del c
-    # fp8 (e4m3fn) KV cache, bf16 queries: the headline batch and 128K batch 1
-    # (half the bytes of the 16-bit cache; GB/s counts the fp8 bytes).
+    # fp8 (e4m3fn) KV cache, bf16 queries: the headline batch (vLLM cache, and
+    # the reference's default NHD cache, which takes the 1024-token grid) and
+    # 128K batch 1 (half the bytes of the 16-bit cache; GB/s counts the fp8 bytes).
     llama_lens = torch.randint(512, 4097, (64,), generator=torch.Generator().manual_seed(0)).tolist()
     for name, args in (("fp8_kv_llama3_8b_b64", (64, 32, 8, 128, 16, llama_lens, torch.bfloat16, "vllm")),
+                       ("fp8_kv_llama3_8b_b64_nhd", (64, 32, 8, 128, 16, llama_lens, torch.bfloat16, "nhd")),
                        ("fp8_kv_128k_b1", (1, 32, 8, 128, 16, [131072], torch.bfloat16, "hnd"))):
         c = attention_case(*args, seed=60, q_scale=128**-0.5, kv_dtype=torch.float8_e4m3fn, k_scale=0.5, v_scale=0.5)
         cpu = {}
