@@ -1394,7 +1394,7 @@ hipError_t launch_split(KParams kp, int num_kv_heads, int num_seqs, int align, h
   // when the 1024-token grid would exceed a round; else that grid. The
   // limit per kernel class, measured against the balanced schedule on
   // uniform and ragged batches, vLLM and NHD caches (cold calls):
-  //   head_dim <= 64 (4 workgroups per CU): up to 2 rounds (up to 3 still won 5-12%);
+  //   head_dim <= 64 (4 workgroups per CU): up to 2 rounds (2.5-3 rounds: within +-5%, 4-5: 2-9% slower);
   //   head_dim 96/128, 16-bit cache: 2 rounds (1-2: 0-11% faster; 2-3: vLLM 1-4% slower);
   //   head_dim 96/128, fp8 cache (3 per CU): 4/3 of a round (to 1024 units:
   //     5-15% faster; 1.7-2 rounds: ragged vLLM batches up to 11% slower);
